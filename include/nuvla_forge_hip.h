@@ -1,0 +1,165 @@
+/*
+ * nuvla_forge_hip.h -- C ABI of the MI355X (gfx950) kernels behind
+ * nuvla_forge_amd.kernels.
+ *
+ * Every entry point
+ *   - takes device pointers, int64_t sizes/strides (in elements) and a
+ *     hipStream_t passed as `void *` (NULL = the null stream);
+ *   - only enqueues work on that stream: it never allocates, frees or
+ *     synchronises (callers own every buffer, including workspaces);
+ *   - returns NF_OK (0) or a negative status; nf_last_error() then describes
+ *     the failure (thread-local string, valid until the next call on the
+ *     same thread).
+ *
+ * Element types are passed as NF_DTYPE_* codes.  Row strides ("ld_*") are in
+ * elements; the last dimension is always unit-stride.  A row stride of 0 is
+ * allowed for the [B, N] conditioning inputs (a broadcast `expand` view).
+ *
+ * The functions replace the launch sites of the reference's Triton kernels;
+ * each declaration cites the reference code it stands in for (paths relative
+ * to the nuvla-forge repository root).
+ */
+#ifndef NUVLA_FORGE_HIP_H
+#define NUVLA_FORGE_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define NF_ABI_VERSION 1
+
+/* element type codes */
+#define NF_DTYPE_F32 0
+#define NF_DTYPE_BF16 1
+#define NF_DTYPE_F16 2
+
+/* status codes */
+#define NF_OK 0
+#define NF_ERR_ARG (-1)       /* bad pointer / size / stride / alignment   */
+#define NF_ERR_DTYPE (-2)     /* unsupported element type or combination  */
+#define NF_ERR_WORKSPACE (-3) /* workspace too small                      */
+#define NF_ERR_LAUNCH (-4)    /* hipLaunchKernel / hipGetLastError failed */
+
+/* ABI version compiled into the library (NF_ABI_VERSION). */
+int nf_abi_version(void);
+
+/* Description of the last failure on the calling thread ("" if none). */
+const char *nf_last_error(void);
+
+/* ------------------------------------------------------------------------
+ * SwiGLU: out = silu(a) * b, elementwise over n contiguous elements.
+ * Replaces the `_swiglu_fwd` launch in nuvla_forge/kernels/swiglu.py:35-46
+ * (called from _FusedSwiGLU.forward, swiglu.py:66-79).
+ * fp32 math, one rounding at the store; a, b, out share `dtype`.
+ * ---------------------------------------------------------------------- */
+int nf_swiglu_fwd(const void *a, const void *b, void *out, int64_t n,
+                  int dtype, void *stream);
+
+/* SwiGLU backward, sigmoid recomputed from a:
+ *   da = dout * b * s * (1 + a * (1 - s)),  db = dout * a * s,  s = sigmoid(a)
+ * Replaces the `_swiglu_bwd` launch in nuvla_forge/kernels/swiglu.py:48-63
+ * (called from _FusedSwiGLU.backward, swiglu.py:81-92). */
+int nf_swiglu_bwd(const void *dout, const void *a, const void *b, void *da,
+                  void *db, int64_t n, int dtype, void *stream);
+
+/* ------------------------------------------------------------------------
+ * adaLN-Zero seam: gated residual add, RMSNorm, modulation.  Row m of the
+ * [M, N] activations belongs to sample m / T (M = B * T).
+ *   h   = x + gate[b] * y                                  (stored as dt_x)
+ *   rstd= 1 / sqrt(mean(h*h) + eps)      (fp32, from the unrounded fp32 h)
+ *   out = h * rstd * weight * (1 + scale[b]) + shift[b]   (stored as dt_x)
+ * Replaces the `_adaln_rmsnorm_fwd` launch in
+ * nuvla_forge/kernels/adaln_rmsnorm.py:61-95 (launched at :178-187).
+ * h and out are contiguous [M, N]; rstd is fp32 [M].  x may differ in type
+ * from y (dt_y); the conditioning tensors and weight carry their own types.
+ * ---------------------------------------------------------------------- */
+int nf_adaln_fwd(const void *x, int64_t ld_x, const void *y, int64_t ld_y,
+                 const void *gate, int64_t ld_gate, const void *weight,
+                 const void *scale, int64_t ld_scale, const void *shift,
+                 int64_t ld_shift, void *h, void *out, float *rstd, int64_t M,
+                 int64_t N, int64_t T, float eps, int dt_x, int dt_y,
+                 int dt_gate, int dt_weight, int dt_scale, int dt_shift,
+                 void *stream);
+
+/* Bytes of fp32 workspace nf_adaln_bwd needs for this shape (per-block
+ * partial rows of the M-axis reductions). */
+size_t nf_adaln_bwd_workspace(int64_t M, int64_t N, int64_t T);
+
+/* adaLN seam backward.  h is recomputed in fp32 from x and y; rstd is the
+ * forward's.  With dxhat = dout * weight * (1 + scale[b]) and
+ * xhat = h * rstd:
+ *   dh     = dh_up + rstd * (dxhat - xhat * mean(dxhat * xhat))
+ *   dx     = dh                          (contiguous [M, N], dt_x)
+ *   dy     = dh * gate[b]                (contiguous [M, N], dt_y)
+ *   dgate  = sum_t dh * y                ([B, N], dt_gate)
+ *   dscale = sum_t dout * xhat * weight  ([B, N], dt_scale)
+ *   dshift = sum_t dout                  ([B, N], dt_shift)
+ *   dweight= sum_m dout * xhat * (1 + scale[b])   ([N], dt_weight)
+ * The M-axis sums are deterministic: per-block partials reduced in LDS, then
+ * a fixed-order second pass; no atomics.
+ * Replaces the `_adaln_rmsnorm_bwd` launch and the partial `.sum` reductions
+ * in nuvla_forge/kernels/adaln_rmsnorm.py:97-162 and :194-236.
+ * dh_up / dout are contiguous [M, N] of dt_x; either may be NULL (= zero).
+ * dgate / dweight / dscale / dshift may each be NULL (not computed). */
+int nf_adaln_bwd(const void *dh_up, const void *dout, const void *x,
+                 int64_t ld_x, const void *y, int64_t ld_y, const void *gate,
+                 int64_t ld_gate, const void *weight, const void *scale,
+                 int64_t ld_scale, const float *rstd, void *dx, void *dy,
+                 void *dgate, void *dweight, void *dscale, void *dshift,
+                 void *workspace, size_t workspace_bytes, int64_t M,
+                 int64_t N, int64_t T, int dt_x, int dt_y, int dt_gate,
+                 int dt_weight, int dt_scale, int dt_shift, void *stream);
+
+/* ------------------------------------------------------------------------
+ * Chunked cross entropy with the gradient formed during the forward pass.
+ *   logits = hidden @ weight^T          ([M, V], never materialised)
+ *   lse    = logsumexp_v logits         (fp32)
+ *   n      = #(targets != ignore_index);  inv = 1 / max(n, 1)
+ *   loss   = inv * sum_{valid m} (lse[m] - logits[m, t_m])   (fp32 scalar)
+ *   dhidden= inv * (softmax - onehot) @ weight        (fp32 [M, D])
+ *   dweight= inv * (softmax - onehot)^T @ hidden      (fp32 [V, D])
+ * Ignored rows contribute no loss and no gradient; an all-ignored batch
+ * gives loss 0 and zero gradients.  Targets outside [0, V) other than
+ * ignore_index are recorded in *bad_targets (device int32, may be NULL)
+ * and treated as ignored.
+ * `vocab_chunk` columns of the softmax gradient exist at a time (bf16 or
+ * fp32 like the inputs), so memory is O(M * vocab_chunk), not O(M * V).
+ * Replaces _ChunkedCrossEntropy.forward and the `_ce_fwd_bwd` kernel,
+ * nuvla_forge/kernels/chunked_ce.py:49-98 and :120-172 (the reference
+ * chunks rows of M; the result does not depend on either chunking beyond
+ * fp rounding).
+ * hidden [M, D] and weight [V, D] are contiguous and share `dtype`
+ * (NF_DTYPE_BF16 uses bf16 MFMA with fp32 accumulation, NF_DTYPE_F32 uses
+ * fp32 MFMA).  targets is int64 [M].  loss, dhidden, dweight are fp32. */
+size_t nf_ce_workspace(int64_t M, int64_t D, int64_t V, int64_t vocab_chunk,
+                       int dtype);
+int nf_ce_fwd_bwd(const void *hidden, const void *weight,
+                  const int64_t *targets, int64_t M, int64_t D, int64_t V,
+                  int64_t ignore_index, int64_t vocab_chunk, int dtype,
+                  float *loss, float *dhidden, float *dweight,
+                  int32_t *bad_targets, void *workspace,
+                  size_t workspace_bytes, void *stream);
+
+/* CE backward: dst[i] = (dtype)(src[i] * (*grad_output)) for n fp32 elements,
+ * grad_output being a device fp32 scalar.  Replaces the scaling and casts in
+ * _ChunkedCrossEntropy.backward, nuvla_forge/kernels/chunked_ce.py:174-182. */
+int nf_scale_cast(const float *src, const float *grad_output, void *dst,
+                  int64_t n, int dtype, void *stream);
+
+/* ------------------------------------------------------------------------
+ * Test hook with no counterpart in the reference: C[M, N] (fp32, row stride
+ * ldc) = A[M, K] @ B[N, K]^T with the MFMA core the cross entropy uses.
+ * A and B are row-major with unit-stride K, type `dtype` (bf16 or f32).
+ * ---------------------------------------------------------------------- */
+int nf_gemm_nt(const void *A, int64_t lda, const void *B, int64_t ldb,
+               float *C, int64_t ldc, int64_t M, int64_t N, int64_t K,
+               int dtype, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* NUVLA_FORGE_HIP_H */

@@ -1,0 +1,474 @@
+// adaLN-Zero seam: gated residual add + RMSNorm + modulation, fwd and bwd.
+//
+// Layout.  x, y, h, out, dh_up, dout, dx, dy are [M, N] row-major (unit
+// stride along N); row m belongs to sample b = m / T.  gate, scale, shift are
+// [B, N] with an arbitrary row stride (0 for a broadcast view), weight is [N].
+//
+// Row mapping.  A row is owned by R = 64 * WPR threads (WPR wavefronts); each
+// thread holds K 8-element chunks of the row in registers, chunk k of thread
+// r covering columns [(k * R + r) * 8, +8), so every load instruction of a
+// wavefront touches one contiguous 1 KiB (bf16) or 2 KiB (f32) span.  With
+// WPR == 1 the row's sum of squares is a pure DPP wavefront reduction; with
+// WPR > 1 the per-wave sums meet in LDS.
+//
+// Backward.  Block (b, j) owns a contiguous run of rows of sample b.  Each
+// thread accumulates three per-column partials over its rows:
+//   A  = sum dout * xhat,  S = sum dout,  G = sum dh * y
+// (dscale = weight * A, dshift = S, dgate = G, dweight = sum_b (1+scale_b) A_b),
+// the row groups of the block combine them in LDS in a fixed order, and the
+// block writes one [3, N] fp32 partial row.  adaln_reduce_samples then sums
+// each sample's J partial rows in a fixed order and adaln_reduce_weight sums
+// samples in order: no atomics, bit-identical from run to run.
+#pragma once
+#include "nf_device.h"
+
+namespace nf {
+namespace adaln {
+
+constexpr int kMaxN = 16384;  // 64 lanes * 8 waves * 8 elems * 4 chunks
+
+struct FwdArgs {
+  const void *x;
+  const void *y;
+  const void *gate;
+  const void *weight;
+  const void *scale;
+  const void *shift;
+  void *h;
+  void *out;
+  float *rstd;
+  int64_t ld_x, ld_y, ld_gate, ld_scale, ld_shift;
+  int64_t M, T;
+  int N;
+  float eps;
+  int dt_gate, dt_weight, dt_scale, dt_shift;
+};
+
+struct BwdArgs {
+  const void *dh_up;
+  const void *dout;
+  const void *x;
+  const void *y;
+  const void *gate;
+  const void *weight;
+  const void *scale;
+  const float *rstd;
+  void *dx;
+  void *dy;
+  float *partial;  // [B * J, 3, N]
+  int64_t ld_x, ld_y, ld_gate, ld_scale;
+  int64_t M, T;
+  int N;
+  int J;               // blocks per sample
+  int rows_per_block;  // ceil(T / J)
+  int dt_gate, dt_weight, dt_scale;
+};
+
+template <int WPR>
+struct FwdShape {
+  static constexpr int R = 64 * WPR;
+  static constexpr int BLK = R < 256 ? 256 : R;
+  static constexpr int G = BLK / R;
+};
+template <int WPR>
+struct BwdShape {
+  static constexpr int R = 64 * WPR;
+  static constexpr int BLK = R < 512 ? 512 : R;
+  static constexpr int G = BLK / R;
+};
+
+__device__ __forceinline__ int chunk_valid(int N, int col) {
+  const int v = N - col;
+  return v < 0 ? 0 : (v > 8 ? 8 : v);
+}
+
+// Sum over the WPR wavefronts that share one row.  `red` holds G * WPR
+// floats; every thread of the block must call this (it may synchronise).
+template <int WPR>
+__device__ __forceinline__ float row_sum(float v, float *red, int g, int rt) {
+  v = wave_sum(v);
+  if constexpr (WPR == 1) {
+    return v;
+  } else {
+    if ((rt & 63) == 0) red[g * WPR + (rt >> 6)] = v;
+    __syncthreads();
+    float t = 0.f;
+#pragma unroll
+    for (int i = 0; i < WPR; ++i) t += red[g * WPR + i];
+    __syncthreads();
+    return t;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// forward
+// ---------------------------------------------------------------------------
+template <typename TX, typename TY, int K, int WPR, bool VEC>
+__global__ __launch_bounds__(FwdShape<WPR>::BLK) void adaln_fwd_kernel(
+    FwdArgs p) {
+  using S = FwdShape<WPR>;
+  __shared__ float red[S::G * WPR];
+  const int g = threadIdx.x / S::R;
+  const int rt = threadIdx.x % S::R;
+  const int64_t row = (int64_t)blockIdx.x * S::G + g;
+  const bool active = row < p.M;
+  const int64_t b = active ? row / p.T : 0;
+
+  const TX *xr = static_cast<const TX *>(p.x) + row * p.ld_x;
+  const TY *yr = static_cast<const TY *>(p.y) + row * p.ld_y;
+
+  float hv[K][8];
+  float ss = 0.f;
+#pragma unroll
+  for (int k = 0; k < K; ++k) {
+    const int col = (k * S::R + rt) * 8;
+    const int valid = active ? chunk_valid(p.N, col) : 0;
+    float xv[8], yv[8], gv[8];
+    if (valid > 0) {
+      load8<TX, VEC>(xr + col, valid, xv);
+      load8<TY, VEC>(yr + col, valid, yv);
+      load8_dyn<VEC>(p.gate, p.dt_gate, b * p.ld_gate + col, valid, gv);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) xv[i] = yv[i] = gv[i] = 0.f;
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      hv[k][i] = xv[i] + gv[i] * yv[i];
+      ss += hv[k][i] * hv[k][i];
+    }
+    if (valid > 0)
+      store8<TX, VEC>(static_cast<TX *>(p.h) + row * (int64_t)p.N + col,
+                      valid, hv[k]);
+  }
+
+  ss = row_sum<WPR>(ss, red, g, rt);
+  const float rstd = 1.f / __builtin_sqrtf(ss / (float)p.N + p.eps);
+  if (active && rt == 0) p.rstd[row] = rstd;
+
+#pragma unroll
+  for (int k = 0; k < K; ++k) {
+    const int col = (k * S::R + rt) * 8;
+    const int valid = active ? chunk_valid(p.N, col) : 0;
+    if (valid > 0) {
+      float wv[8], sv[8], shv[8], o[8];
+      load8_dyn<VEC>(p.weight, p.dt_weight, col, valid, wv);
+      load8_dyn<VEC>(p.scale, p.dt_scale, b * p.ld_scale + col, valid, sv);
+      load8_dyn<VEC>(p.shift, p.dt_shift, b * p.ld_shift + col, valid, shv);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const float xhat = hv[k][i] * rstd;
+        o[i] = xhat * wv[i] * (1.f + sv[i]) + shv[i];
+      }
+      store8<TX, VEC>(static_cast<TX *>(p.out) + row * (int64_t)p.N + col,
+                      valid, o);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// backward: per-row gradients + per-block partial rows
+// ---------------------------------------------------------------------------
+
+// Sum one accumulator over the G row groups of the block (group order
+// 0, 1, ..., G-1) and store the result row.  All threads must call it.
+template <int K, int G, int R, bool VEC>
+__device__ __forceinline__ void combine_store(float (&acc)[K][8], float *comb,
+                                              int g, int rt, float *dst,
+                                              int N) {
+  constexpr int kRowElems = R * K * 8;
+  if constexpr (G > 1) {
+    if (g > 0) {
+#pragma unroll
+      for (int k = 0; k < K; ++k)
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+          comb[(g - 1) * kRowElems + (k * R + rt) * 8 + i] = acc[k][i];
+    }
+    __syncthreads();
+    if (g == 0) {
+#pragma unroll
+      for (int gg = 1; gg < G; ++gg)
+#pragma unroll
+        for (int k = 0; k < K; ++k)
+#pragma unroll
+          for (int i = 0; i < 8; ++i)
+            acc[k][i] += comb[(gg - 1) * kRowElems + (k * R + rt) * 8 + i];
+    }
+    __syncthreads();
+  }
+  if (g == 0) {
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+      const int col = (k * R + rt) * 8;
+      const int valid = chunk_valid(N, col);
+      if (valid > 0) store8<float, VEC>(dst + col, valid, acc[k]);
+    }
+  }
+}
+template <typename TX, typename TY, int K, int WPR, bool VEC>
+__global__ __launch_bounds__(BwdShape<WPR>::BLK) void adaln_bwd_kernel(
+    BwdArgs p) {
+  using S = BwdShape<WPR>;
+  __shared__ float red[S::G * WPR];
+  // combine buffer for the G row groups: (G - 1) x (R * K * 8) floats
+  __shared__ float comb[S::G > 1 ? (S::G - 1) * S::R * K * 8 : 1];
+
+  const int g = threadIdx.x / S::R;
+  const int rt = threadIdx.x % S::R;
+  const int64_t b = blockIdx.x / p.J;
+  const int j = blockIdx.x % p.J;
+  const int64_t t0 = (int64_t)j * p.rows_per_block;
+  int64_t t1 = t0 + p.rows_per_block;
+  if (t1 > p.T) t1 = p.T;
+
+  // per-sample conditioning, held in registers across the rows:
+  // wo = weight * (1 + scale[b]) (the dout -> dxhat factor) and gate[b]
+  float wo[K][8], gv[K][8];
+#pragma unroll
+  for (int k = 0; k < K; ++k) {
+    const int col = (k * S::R + rt) * 8;
+    const int valid = chunk_valid(p.N, col);
+    float wv[8], sv[8];
+    if (valid > 0) {
+      load8_dyn<VEC>(p.weight, p.dt_weight, col, valid, wv);
+      load8_dyn<VEC>(p.scale, p.dt_scale, b * p.ld_scale + col, valid, sv);
+      load8_dyn<VEC>(p.gate, p.dt_gate, b * p.ld_gate + col, valid, gv[k]);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) wv[i] = sv[i] = gv[k][i] = 0.f;
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) wo[k][i] = wv[i] * (1.f + sv[i]);
+  }
+
+  float accA[K][8], accS[K][8], accG[K][8];
+#pragma unroll
+  for (int k = 0; k < K; ++k)
+#pragma unroll
+    for (int i = 0; i < 8; ++i) accA[k][i] = accS[k][i] = accG[k][i] = 0.f;
+
+  const TX *const xp = static_cast<const TX *>(p.x);
+  const TY *const yp = static_cast<const TY *>(p.y);
+  const TX *const dop = static_cast<const TX *>(p.dout);
+  const TX *const dhp = static_cast<const TX *>(p.dh_up);
+
+  const int64_t nrows = t1 > t0 ? t1 - t0 : 0;
+  const int64_t iters = (nrows + S::G - 1) / S::G;
+  for (int64_t it = 0; it < iters; ++it) {
+    const int64_t t = t0 + it * S::G + g;
+    const bool active = t < t1;
+    const int64_t row = b * p.T + t;
+    const float rstd = active ? p.rstd[row] : 0.f;
+
+    Raw8<TX> xr[K], dor[K], dhr[K];
+    Raw8<TY> yr[K];
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+      const int col = (k * S::R + rt) * 8;
+      const int valid = active ? chunk_valid(p.N, col) : 0;
+      if (valid > 0) {
+        xr[k].template load<VEC>(xp + row * p.ld_x + col, valid);
+        yr[k].template load<VEC>(yp + row * p.ld_y + col, valid);
+        if (dop) dor[k].template load<VEC>(dop + row * (int64_t)p.N + col, valid);
+        else dor[k].zero();
+        if (dhp) dhr[k].template load<VEC>(dhp + row * (int64_t)p.N + col, valid);
+        else dhr[k].zero();
+      } else {
+        xr[k].zero(); yr[k].zero(); dor[k].zero(); dhr[k].zero();
+      }
+    }
+
+    // xhat = (x + gate * y) * rstd (h recomputed in fp32, never re-read)
+    float xh[K][8];
+    float dot = 0.f;
+#pragma unroll
+    for (int k = 0; k < K; ++k)
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        xh[k][i] = (xr[k][i] + gv[k][i] * yr[k][i]) * rstd;
+        dot += (dor[k][i] * wo[k][i]) * xh[k][i];
+      }
+    dot = row_sum<WPR>(dot, red, g, rt);
+    const float c = dot / (float)p.N;
+
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+      const int col = (k * S::R + rt) * 8;
+      const int valid = active ? chunk_valid(p.N, col) : 0;
+      if (valid > 0) {
+        float dh[8], dyv[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const float d = dor[k][i];
+          dh[i] = dhr[k][i] + rstd * (d * wo[k][i] - xh[k][i] * c);
+          dyv[i] = dh[i] * gv[k][i];
+          accA[k][i] += d * xh[k][i];
+          accS[k][i] += d;
+          accG[k][i] += dh[i] * yr[k][i];
+        }
+        store8<TX, VEC>(static_cast<TX *>(p.dx) + row * (int64_t)p.N + col, valid, dh);
+        store8<TY, VEC>(static_cast<TY *>(p.dy) + row * (int64_t)p.N + col, valid, dyv);
+      }
+    }
+  }
+
+  // combine the G row groups in a fixed order (group 0 + 1 + ... + G-1) and
+  // write the block's [3, N] partial row
+  float *dst = p.partial + (int64_t)blockIdx.x * 3 * p.N;
+  combine_store<K, S::G, S::R, VEC>(accA, comb, g, rt, dst, p.N);
+  combine_store<K, S::G, S::R, VEC>(accS, comb, g, rt, dst + p.N, p.N);
+  combine_store<K, S::G, S::R, VEC>(accG, comb, g, rt, dst + 2 * (int64_t)p.N, p.N);
+}
+
+// ---------------------------------------------------------------------------
+// planning
+// ---------------------------------------------------------------------------
+struct Plan {
+  int fwd_wpr;  // forward: wavefronts per row (1, 2, 4, 8)
+  int fwd_k;    // forward: 8-element chunks per thread (1, 2, 4)
+  int bwd_wpr;  // backward: wavefronts per row (1, 2, 4, 8, 16)
+  int bwd_k;    // backward: 8-element chunks per thread (1, 2)
+  int J;        // backward blocks per sample
+  int rows_per_block;
+  int64_t B;
+};
+
+// Target number of backward blocks: one 512-thread block per CU on the
+// 256-CU MI355X (8 wavefronts per CU), so each block covers many rows and the
+// partial-row traffic stays a few percent of the tensor traffic.
+constexpr int kBwdBlocksTarget = 256;
+
+inline int pick_wpr(int64_t N, int max_k) {
+  int wpr = 1;
+  while ((int64_t)64 * wpr * 8 * max_k < N) wpr *= 2;
+  return wpr;
+}
+inline int pick_k(int64_t N, int wpr) {
+  const int64_t per_chunk = (int64_t)64 * wpr * 8;
+  const int64_t k = (N + per_chunk - 1) / per_chunk;
+  return k <= 1 ? 1 : (k <= 2 ? 2 : 4);
+}
+
+inline Plan make_plan(int64_t M, int64_t N, int64_t T) {
+  Plan pl{};
+  // forward holds up to 4 chunks per thread (no LDS sync up to N = 2048);
+  // backward holds up to 2 (its per-column accumulators live in registers)
+  pl.fwd_wpr = pick_wpr(N, 4);
+  pl.fwd_k = pick_k(N, pl.fwd_wpr);
+  pl.bwd_wpr = pick_wpr(N, 2);
+  pl.bwd_k = pick_k(N, pl.bwd_wpr);
+  pl.B = M / T;
+  const int R = 64 * pl.bwd_wpr;
+  const int G = (R < 512 ? 512 : R) / R;
+  int64_t J = (kBwdBlocksTarget + pl.B - 1) / pl.B;
+  const int64_t jmax = (T + 2 * G - 1) / (2 * G);  // >= 2 rows per row group
+  if (J > jmax) J = jmax;
+  if (J < 1) J = 1;
+  pl.rows_per_block = (int)((T + J - 1) / J);
+  pl.J = (int)((T + pl.rows_per_block - 1) / pl.rows_per_block);
+  return pl;
+}
+
+inline size_t workspace_bytes(const Plan &pl, int64_t N) {
+  return (size_t)(pl.B * pl.J * 3 * N + pl.B * N) * sizeof(float);
+}
+
+// ---------------------------------------------------------------------------
+// dispatch over (TX, TY) x K x WPR x VEC
+// ---------------------------------------------------------------------------
+template <typename TX, typename TY, bool VEC, int WPR, int K>
+int launch_fwd_t(const FwdArgs &a, hipStream_t s) {
+  using S = FwdShape<WPR>;
+  const unsigned grid = (unsigned)((a.M + S::G - 1) / S::G);
+  adaln_fwd_kernel<TX, TY, K, WPR, VEC><<<grid, S::BLK, 0, s>>>(a);
+  return check_launch("nf_adaln_fwd");
+}
+template <typename TX, typename TY, bool VEC, int WPR, int K>
+int launch_bwd_t(const BwdArgs &a, int64_t B, hipStream_t s) {
+  using S = BwdShape<WPR>;
+  const unsigned grid = (unsigned)(B * a.J);
+  adaln_bwd_kernel<TX, TY, K, WPR, VEC><<<grid, S::BLK, 0, s>>>(a);
+  return check_launch("nf_adaln_bwd");
+}
+
+template <typename TX, typename TY, bool VEC, int WPR>
+int fwd_k(const FwdArgs &a, const Plan &pl, hipStream_t s) {
+  if constexpr (!VEC) {
+    return launch_fwd_t<TX, TY, false, WPR, 4>(a, s);
+  } else {
+    switch (pl.fwd_k) {
+      case 1: return launch_fwd_t<TX, TY, true, WPR, 1>(a, s);
+      case 2: return launch_fwd_t<TX, TY, true, WPR, 2>(a, s);
+      default: return launch_fwd_t<TX, TY, true, WPR, 4>(a, s);
+    }
+  }
+}
+template <typename TX, typename TY, bool VEC, int WPR>
+int bwd_k(const BwdArgs &a, const Plan &pl, hipStream_t s) {
+  if constexpr (!VEC) {
+    return launch_bwd_t<TX, TY, false, WPR, 2>(a, pl.B, s);
+  } else {
+    if (pl.bwd_k == 1) return launch_bwd_t<TX, TY, true, WPR, 1>(a, pl.B, s);
+    return launch_bwd_t<TX, TY, true, WPR, 2>(a, pl.B, s);
+  }
+}
+
+template <typename TX, typename TY, bool VEC>
+int fwd_w(const FwdArgs &a, const Plan &pl, hipStream_t s) {
+  switch (pl.fwd_wpr) {
+    case 1: return fwd_k<TX, TY, VEC, 1>(a, pl, s);
+    case 2: return fwd_k<TX, TY, VEC, 2>(a, pl, s);
+    case 4: return fwd_k<TX, TY, VEC, 4>(a, pl, s);
+    default: return fwd_k<TX, TY, VEC, 8>(a, pl, s);
+  }
+}
+template <typename TX, typename TY, bool VEC>
+int bwd_w(const BwdArgs &a, const Plan &pl, hipStream_t s) {
+  switch (pl.bwd_wpr) {
+    case 1: return bwd_k<TX, TY, VEC, 1>(a, pl, s);
+    case 2: return bwd_k<TX, TY, VEC, 2>(a, pl, s);
+    case 4: return bwd_k<TX, TY, VEC, 4>(a, pl, s);
+    case 8: return bwd_k<TX, TY, VEC, 8>(a, pl, s);
+    default: return bwd_k<TX, TY, VEC, 16>(a, pl, s);
+  }
+}
+
+// Explicitly instantiated once per (TX, TY) pair in adaln_inst_*.hip so the
+// kernel variants compile in parallel translation units.
+template <typename TX, typename TY>
+int fwd_v(const FwdArgs &a, const Plan &pl, bool vec, hipStream_t s) {
+  return vec ? fwd_w<TX, TY, true>(a, pl, s) : fwd_w<TX, TY, false>(a, pl, s);
+}
+template <typename TX, typename TY>
+int bwd_v(const BwdArgs &a, const Plan &pl, bool vec, hipStream_t s) {
+  return vec ? bwd_w<TX, TY, true>(a, pl, s) : bwd_w<TX, TY, false>(a, pl, s);
+}
+
+// supported (x, y) type pairs: equal types, or fp32 residual with a 16-bit
+// branch output (the autocast mix of the DiT seams)
+template <class F>
+inline int dispatch_xy(int dt_x, int dt_y, const char *who, F &&f) {
+  if (dt_x == NF_DTYPE_F32 && dt_y == NF_DTYPE_F32) return f(float(), float());
+  if (dt_x == NF_DTYPE_BF16 && dt_y == NF_DTYPE_BF16) return f(bf16(), bf16());
+  if (dt_x == NF_DTYPE_F16 && dt_y == NF_DTYPE_F16) return f(f16(), f16());
+  if (dt_x == NF_DTYPE_F32 && dt_y == NF_DTYPE_BF16) return f(float(), bf16());
+  if (dt_x == NF_DTYPE_F32 && dt_y == NF_DTYPE_F16) return f(float(), f16());
+  return set_error(NF_ERR_DTYPE, "%s: unsupported (x, y) dtypes (%d, %d)", who,
+                   dt_x, dt_y);
+}
+
+inline int check_shape(const char *who, int64_t M, int64_t N, int64_t T) {
+  if (M < 0 || N <= 0 || T <= 0)
+    return set_error(NF_ERR_ARG, "%s: bad shape M=%lld N=%lld T=%lld", who,
+                     (long long)M, (long long)N, (long long)T);
+  if (M % T != 0)
+    return set_error(NF_ERR_ARG, "%s: M=%lld is not a multiple of T=%lld", who,
+                     (long long)M, (long long)T);
+  if (N > kMaxN)
+    return set_error(NF_ERR_ARG, "%s: N=%lld exceeds %d", who, (long long)N, kMaxN);
+  return NF_OK;
+}
+
+}  // namespace adaln
+}  // namespace nf

@@ -1,0 +1,530 @@
+// Chunked cross entropy with the gradient formed in the forward pass, on the
+// MFMA GEMM core of gemm_core.h.
+//
+// Pipeline (all on the caller's stream, fixed reduction orders throughout):
+//   1. transpose  W [V, D] -> Wt [D, ldwt],  H [M, D] -> Ht [D, ldht]
+//      (zero-padded columns), so every GEMM below is K-contiguous (NT).
+//   2. ce_stats:  S = H W^T tile by tile; per (row, 128-column tile) the
+//      row max and sum of exp(S - max), plus S[m, t_m] for the target column.
+//      S itself is never stored.
+//   3. ce_lse:    lse[m] = combine of the tile partials (fixed order);
+//                 loss_row[m] = lse - S[m, t_m] for valid rows.
+//   4. ce_loss:   one block: n_valid, loss = sum(loss_row) / max(n, 1),
+//                 inv = 1 / max(n, 1).
+//   5. per vocabulary chunk c of `vocab_chunk` columns:
+//      ce_prob:  recompute S_c = H W_c^T; P_c = inv * (softmax - onehot)
+//                (0 for ignored rows) in the input type, written row-major
+//                [M, Vc] and transposed [Vc, M] (through an LDS tile);
+//      dW_c  = P_c^T H        (gemm_store, K = M)   -> dweight rows of c
+//      dH   += P_c   W_c      (gemm_store, K = Vc)  -> dhidden (chunk 0
+//                                                     writes, later add)
+// Memory is O(M * vocab_chunk) for P; the [M, V] logits never exist.
+#include <type_traits>
+
+#include "gemm_core.h"
+
+namespace nf {
+namespace ce {
+
+using gemm::Cfg;
+using gemm::floatx16;
+
+constexpr int kTileN = 128;  // vocabulary columns per stats partial
+
+template <typename TI>
+using MainCfg = Cfg<TI, 128, 128, 2, 2>;
+
+__device__ __forceinline__ float log_f32(float x) {
+  constexpr float kLn2 = 0.6931471805599453f;  // ln(2)
+  return __builtin_amdgcn_logf(x) * kLn2;       // log2 on the hardware
+}
+
+// ---------------------------------------------------------------------------
+// plain store epilogue: C[m, n] (+)= acc
+// ---------------------------------------------------------------------------
+template <class C, bool VK>
+__global__ __launch_bounds__(C::NT) void gemm_store_kernel(
+    const typename C::TI *A, int64_t lda, const typename C::TI *B, int64_t ldb,
+    float *Cout, int64_t ldc, int64_t M, int64_t N, int64_t K, int accumulate) {
+  __shared__ __attribute__((aligned(16))) char smem[C::LDS_BYTES];
+  const int64_t m0 = (int64_t)blockIdx.x * C::BM;
+  const int64_t n0 = (int64_t)blockIdx.y * C::BN;
+  floatx16 acc[C::TM][C::TN];
+  gemm::mainloop<C, VK>(A, lda, B, ldb, M, N, K, m0, n0, smem, acc);
+  const int w = threadIdx.x >> 6, wm = w / C::WN, wn = w % C::WN;
+#pragma unroll
+  for (int i = 0; i < C::TM; ++i)
+#pragma unroll
+    for (int j = 0; j < C::TN; ++j) {
+      const int64_t col = n0 + gemm::acc_col<C>(wn, j);
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int64_t row = m0 + gemm::acc_row<C>(wm, i, r);
+        if (row < M && col < N) {
+          float *p = Cout + row * ldc + col;
+          *p = accumulate ? *p + acc[i][j][r] : acc[i][j][r];
+        }
+      }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// stats epilogue: per-row (max, sum exp) over this block's 128 columns
+// ---------------------------------------------------------------------------
+template <class C, bool VK>
+__global__ __launch_bounds__(C::NT) void ce_stats_kernel(
+    const typename C::TI *H, const typename C::TI *W, int64_t M, int64_t V,
+    int64_t D, const int64_t *targets, float2 *stats, float *tgt_logit,
+    int ntiles) {
+  static_assert(C::BN == kTileN, "stats tile width");
+  __shared__ __attribute__((aligned(16))) char smem[C::LDS_BYTES];
+  __shared__ int tgt_s[C::BM];
+  __shared__ float redm[C::BM][C::WN];
+  __shared__ float reds[C::BM][C::WN];
+  const int64_t m0 = (int64_t)blockIdx.x * C::BM;
+  const int64_t n0 = (int64_t)blockIdx.y * C::BN;
+  for (int t = threadIdx.x; t < C::BM; t += C::NT) {
+    int tc = -1;
+    if (m0 + t < M) {
+      const int64_t tg = targets[m0 + t];
+      if (tg >= n0 && tg < n0 + C::BN && tg < V) tc = (int)(tg - n0);
+    }
+    tgt_s[t] = tc;
+  }
+  floatx16 acc[C::TM][C::TN];
+  gemm::mainloop<C, VK>(H, D, W, D, M, V, D, m0, n0, smem, acc);
+
+  const int l = threadIdx.x & 63;
+  const int w = threadIdx.x >> 6, wm = w / C::WN, wn = w % C::WN;
+#pragma unroll
+  for (int i = 0; i < C::TM; ++i)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      float mx = -INFINITY;
+#pragma unroll
+      for (int j = 0; j < C::TN; ++j)
+        if (n0 + gemm::acc_col<C>(wn, j) < V) mx = fmaxf(mx, acc[i][j][r]);
+      mx = half_wave_max(mx);
+      if ((l & 31) == 0) redm[gemm::acc_row<C>(wm, i, r)][wn] = mx;
+    }
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < C::TM; ++i)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int lr = gemm::acc_row<C>(wm, i, r);
+      float bm = redm[lr][0];
+#pragma unroll
+      for (int q = 1; q < C::WN; ++q) bm = fmaxf(bm, redm[lr][q]);
+      float s = 0.f;
+#pragma unroll
+      for (int j = 0; j < C::TN; ++j) {
+        const int lc = gemm::acc_col<C>(wn, j);
+        if (n0 + lc < V) s += exp_f32(acc[i][j][r] - bm);
+        if (lc == tgt_s[lr]) tgt_logit[m0 + lr] = acc[i][j][r];
+      }
+      s = half_wave_sum(s);
+      if ((l & 31) == 0) reds[lr][wn] = s;
+    }
+  __syncthreads();
+  for (int t = threadIdx.x; t < C::BM; t += C::NT) {
+    if (m0 + t >= M) continue;
+    // every wave's sum is taken relative to the same block-row max
+    float bm = redm[t][0], s = reds[t][0];
+#pragma unroll
+    for (int q = 1; q < C::WN; ++q) {
+      bm = fmaxf(bm, redm[t][q]);
+      s += reds[t][q];
+    }
+    stats[(m0 + t) * ntiles + blockIdx.y] = make_float2(bm, s);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// lse per row (one wavefront per row)
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void ce_lse_kernel(
+    const float2 *__restrict__ stats, int ntiles, const float *tgt_logit,
+    const int64_t *targets, int64_t M, int64_t V, int64_t ignore_index,
+    float *lse, int *tcol, float *loss_row, int *flags) {
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int l = threadIdx.x & 63;
+  if (row >= M) return;
+  const float2 *sr = stats + row * ntiles;
+  float mx = -INFINITY;
+  for (int t = l; t < ntiles; t += 64) mx = fmaxf(mx, sr[t].x);
+  mx = wave_max(mx);
+  float s = 0.f;
+  for (int t = l; t < ntiles; t += 64) s += sr[t].y * exp_f32(sr[t].x - mx);
+  s = wave_sum(s);
+  if (l == 0) {
+    const float ls = mx + log_f32(s);
+    const int64_t tg = targets[row];
+    const bool in_range = tg >= 0 && tg < V;
+    const bool valid = tg != ignore_index && in_range;
+    lse[row] = ls;
+    tcol[row] = valid ? (int)tg : -1;
+    loss_row[row] = valid ? ls - tgt_logit[row] : 0.f;
+    flags[row] = (valid ? 1 : 0) | ((tg != ignore_index && !in_range) ? 2 : 0);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// loss, n_valid, inv_count: one block, fixed-order tree
+// ---------------------------------------------------------------------------
+constexpr int kLossThreads = 1024;
+
+__global__ __launch_bounds__(kLossThreads) void ce_loss_kernel(
+    const float *loss_row, const int *flags, int64_t M, float *loss,
+    float *inv_out, int *bad_out) {
+  __shared__ float sl[kLossThreads];
+  __shared__ int sn[kLossThreads];
+  __shared__ int sb[kLossThreads];
+  float a = 0.f;
+  int n = 0, bad = 0;
+  for (int64_t i = threadIdx.x; i < M; i += kLossThreads) {
+    a += loss_row[i];
+    n += flags[i] & 1;
+    bad += (flags[i] >> 1) & 1;
+  }
+  sl[threadIdx.x] = a;
+  sn[threadIdx.x] = n;
+  sb[threadIdx.x] = bad;
+  __syncthreads();
+  for (int s = kLossThreads / 2; s > 0; s >>= 1) {
+    if ((int)threadIdx.x < s) {
+      sl[threadIdx.x] += sl[threadIdx.x + s];
+      sn[threadIdx.x] += sn[threadIdx.x + s];
+      sb[threadIdx.x] += sb[threadIdx.x + s];
+    }
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) {
+    const float inv = 1.f / (float)(sn[0] > 1 ? sn[0] : 1);
+    *loss = sl[0] * inv;
+    *inv_out = inv;
+    if (bad_out) *bad_out = sb[0];
+  }
+}
+
+// ---------------------------------------------------------------------------
+// probability epilogue: P = inv * (softmax - onehot) for one vocab chunk
+// ---------------------------------------------------------------------------
+template <class C, bool VK>
+__global__ __launch_bounds__(C::NT) void ce_prob_kernel(
+    const typename C::TI *H, const typename C::TI *Wc, int64_t M, int64_t Vc,
+    int64_t D, int64_t vbase, const int *tcol, const float *lse,
+    const float *inv_ptr, typename C::TI *P, int64_t ldp, int64_t kpad,
+    typename C::TI *PT, int64_t ldpt) {
+  using TI = typename C::TI;
+  constexpr int TP = C::BM + 16;  // transposed-tile pitch (elements)
+  static_assert(C::BN * TP * sizeof(TI) <= C::LDS_BYTES, "transpose tile");
+  __shared__ __attribute__((aligned(16))) char smem[C::LDS_BYTES];
+  __shared__ int tc_s[C::BM];
+  __shared__ float lse_s[C::BM];
+  const int64_t m0 = (int64_t)blockIdx.x * C::BM;
+  const int64_t n0 = (int64_t)blockIdx.y * C::BN;
+  for (int t = threadIdx.x; t < C::BM; t += C::NT) {
+    const bool in = m0 + t < M;
+    tc_s[t] = in ? tcol[m0 + t] : -1;
+    lse_s[t] = in ? lse[m0 + t] : 0.f;
+  }
+  floatx16 acc[C::TM][C::TN];
+  gemm::mainloop<C, VK>(H, D, Wc, D, M, Vc, D, m0, n0, smem, acc);
+  const float inv = *inv_ptr;
+
+  TI *tile = reinterpret_cast<TI *>(smem);  // [BN][TP]: tile[col][row]
+  const int w = threadIdx.x >> 6, wm = w / C::WN, wn = w % C::WN;
+#pragma unroll
+  for (int i = 0; i < C::TM; ++i)
+#pragma unroll
+    for (int j = 0; j < C::TN; ++j) {
+      const int lc = gemm::acc_col<C>(wn, j);
+      const int64_t col = n0 + lc;
+      const int64_t gcol = vbase + col;
+#pragma unroll
+      for (int rg = 0; rg < 4; ++rg) {
+        const int lr0 = gemm::acc_row<C>(wm, i, rg * 4);  // rows lr0 .. lr0 + 3
+        TI pv[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int lr = lr0 + q;
+          const int tc = tc_s[lr];
+          float p = 0.f;
+          if (tc >= 0 && col < Vc) {
+            p = exp_f32(acc[i][j][rg * 4 + q] - lse_s[lr]);
+            if (gcol == tc) p -= 1.f;
+            p *= inv;
+          }
+          pv[q] = static_cast<TI>(p);
+          if (m0 + lr < M && col < kpad) P[(m0 + lr) * ldp + col] = pv[q];
+        }
+#pragma unroll
+        for (int q = 0; q < 4; ++q) tile[lc * TP + lr0 + q] = pv[q];
+      }
+    }
+  __syncthreads();
+  // P^T rows (vocabulary entries) of this tile: BM contiguous tokens each
+  constexpr int VPR = C::BM * sizeof(TI) / 16;  // 16-byte vectors per row
+  for (int v = threadIdx.x; v < C::BN * VPR; v += C::NT) {
+    const int c = v / VPR, seg = v % VPR;
+    const int64_t vr = n0 + c;                        // P^T row
+    const int64_t tok = m0 + seg * (16 / sizeof(TI)); // first token
+    if (vr < Vc && tok < ldpt)
+      *reinterpret_cast<u32x4 *>(PT + vr * ldpt + tok) =
+          *reinterpret_cast<const u32x4 *>(tile + c * TP + seg * (16 / sizeof(TI)));
+  }
+}
+
+// ---------------------------------------------------------------------------
+// transpose with zero padding: out[c, r] = in[r, c] (r < R), 0 for R <= r < ldo
+// ---------------------------------------------------------------------------
+template <typename T>
+__global__ __launch_bounds__(256) void transpose_pad_kernel(
+    const T *__restrict__ in, int64_t R, int64_t Cn, int64_t ldi,
+    T *__restrict__ out, int64_t ldo) {
+  __shared__ T tile[64][65];
+  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+  const int64_t r0 = (int64_t)blockIdx.x * 64, c0 = (int64_t)blockIdx.y * 64;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int64_t r = r0 + ty + 4 * i, c = c0 + tx;
+    tile[ty + 4 * i][tx] = (r < R && c < Cn) ? in[r * ldi + c] : static_cast<T>(0.f);
+  }
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int64_t c = c0 + ty + 4 * i, r = r0 + tx;
+    if (c < Cn && r < ldo) out[c * ldo + r] = tile[tx][ty + 4 * i];
+  }
+}
+
+// ---------------------------------------------------------------------------
+// backward scale + cast
+// ---------------------------------------------------------------------------
+template <typename T, bool VEC>
+__global__ __launch_bounds__(256) void scale_cast_kernel(
+    const float *__restrict__ src, const float *__restrict__ g,
+    T *__restrict__ dst, int64_t n) {
+  const float gv = *g;
+  const int64_t nchunks = (n + 7) >> 3;
+  for (int64_t c = (int64_t)blockIdx.x * 256 + threadIdx.x; c < nchunks;
+       c += (int64_t)gridDim.x * 256) {
+    const int64_t rem = n - c * 8;
+    const int valid = rem >= 8 ? 8 : (int)rem;
+    float v[8];
+    load8<float, VEC>(src + c * 8, valid, v);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] *= gv;
+    store8<T, VEC>(dst + c * 8, valid, v);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// host side
+// ---------------------------------------------------------------------------
+inline int64_t round_up(int64_t x, int64_t m) { return (x + m - 1) / m * m; }
+inline size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+struct Layout {
+  int64_t ldwt, ldht, vc, ldp, ntiles;
+  size_t off_wt, off_ht, off_stats, off_tgt, off_lse, off_tcol, off_loss, off_flags,
+      off_scal, off_p, off_pt, total;
+};
+
+inline Layout make_layout(int64_t M, int64_t D, int64_t V, int64_t vocab_chunk, int es) {
+  Layout L{};
+  L.ldwt = round_up(V, 8);
+  L.ldht = round_up(M, 8);
+  L.vc = round_up(vocab_chunk < V ? vocab_chunk : V, 8);
+  L.ldp = L.vc;
+  L.ntiles = (V + kTileN - 1) / kTileN;
+  size_t o = 0;
+  auto take = [&](size_t bytes) { const size_t at = o; o = align256(o + bytes); return at; };
+  L.off_wt = take((size_t)D * L.ldwt * es);
+  L.off_ht = take((size_t)D * L.ldht * es);
+  L.off_stats = take((size_t)M * L.ntiles * sizeof(float2));
+  L.off_tgt = take((size_t)M * sizeof(float));
+  L.off_lse = take((size_t)M * sizeof(float));
+  L.off_tcol = take((size_t)M * sizeof(int));
+  L.off_loss = take((size_t)M * sizeof(float));
+  L.off_flags = take((size_t)M * sizeof(int));
+  L.off_scal = take(64);
+  L.off_p = take((size_t)M * L.ldp * es);
+  L.off_pt = take((size_t)L.vc * L.ldht * es);
+  L.total = o;
+  return L;
+}
+
+template <class C>
+int launch_gemm_store(const typename C::TI *A, int64_t lda, const typename C::TI *B,
+                      int64_t ldb, float *Cout, int64_t ldc, int64_t M, int64_t N,
+                      int64_t K, int accumulate, hipStream_t s) {
+  using TI = typename C::TI;
+  constexpr int VE = 16 / sizeof(TI);
+  const bool vk = K % VE == 0 && lda % VE == 0 && ldb % VE == 0 && aligned16(A) &&
+                  aligned16(B);
+  dim3 grid((unsigned)((M + C::BM - 1) / C::BM), (unsigned)((N + C::BN - 1) / C::BN));
+  if (vk)
+    gemm_store_kernel<C, true><<<grid, C::NT, 0, s>>>(A, lda, B, ldb, Cout, ldc, M, N, K, accumulate);
+  else
+    gemm_store_kernel<C, false><<<grid, C::NT, 0, s>>>(A, lda, B, ldb, Cout, ldc, M, N, K, accumulate);
+  return check_launch("gemm_store");
+}
+
+template <typename T>
+int launch_transpose(const void *in, int64_t R, int64_t Cn, int64_t ldi, void *out,
+                     int64_t ldo, hipStream_t s) {
+  dim3 grid((unsigned)((ldo + 63) / 64), (unsigned)((Cn + 63) / 64));
+  transpose_pad_kernel<T><<<grid, 256, 0, s>>>((const T *)in, R, Cn, ldi, (T *)out, ldo);
+  return check_launch("transpose");
+}
+
+template <typename TI>
+int ce_run(const TI *H, const TI *W, const int64_t *targets, int64_t M, int64_t D,
+           int64_t V, int64_t ignore_index, int64_t vocab_chunk, float *loss,
+           float *dH, float *dW, int32_t *bad, char *ws, hipStream_t s) {
+  using C = MainCfg<TI>;
+  constexpr int VE = 16 / sizeof(TI);
+  const Layout L = make_layout(M, D, V, vocab_chunk, sizeof(TI));
+  TI *Wt = reinterpret_cast<TI *>(ws + L.off_wt);
+  TI *Ht = reinterpret_cast<TI *>(ws + L.off_ht);
+  float2 *stats = reinterpret_cast<float2 *>(ws + L.off_stats);
+  float *tgt = reinterpret_cast<float *>(ws + L.off_tgt);
+  float *lse = reinterpret_cast<float *>(ws + L.off_lse);
+  int *tcol = reinterpret_cast<int *>(ws + L.off_tcol);
+  float *loss_row = reinterpret_cast<float *>(ws + L.off_loss);
+  int *flags = reinterpret_cast<int *>(ws + L.off_flags);
+  float *inv = reinterpret_cast<float *>(ws + L.off_scal);
+  TI *P = reinterpret_cast<TI *>(ws + L.off_p);
+  TI *PT = reinterpret_cast<TI *>(ws + L.off_pt);
+  int e;
+
+  using U = typename std::conditional<sizeof(TI) == 2, uint16_t, uint32_t>::type;
+  if ((e = launch_transpose<U>(W, V, D, D, Wt, L.ldwt, s))) return e;
+  if ((e = launch_transpose<U>(H, M, D, D, Ht, L.ldht, s))) return e;
+
+  const bool vk = D % VE == 0 && aligned16(H) && aligned16(W);
+  dim3 gs((unsigned)((M + C::BM - 1) / C::BM), (unsigned)L.ntiles);
+  if (vk)
+    ce_stats_kernel<C, true><<<gs, C::NT, 0, s>>>(H, W, M, V, D, targets, stats, tgt, (int)L.ntiles);
+  else
+    ce_stats_kernel<C, false><<<gs, C::NT, 0, s>>>(H, W, M, V, D, targets, stats, tgt, (int)L.ntiles);
+  if ((e = check_launch("ce_stats"))) return e;
+
+  ce_lse_kernel<<<(unsigned)((M + 3) / 4), 256, 0, s>>>(stats, (int)L.ntiles, tgt, targets, M, V,
+                                                       ignore_index, lse, tcol, loss_row, flags);
+  if ((e = check_launch("ce_lse"))) return e;
+  ce_loss_kernel<<<1, kLossThreads, 0, s>>>(loss_row, flags, M, loss, inv, bad);
+  if ((e = check_launch("ce_loss"))) return e;
+
+  for (int64_t vb = 0; vb < V; vb += L.vc) {
+    const int64_t vc = (V - vb < L.vc) ? V - vb : L.vc;  // columns in this chunk
+    const int64_t kpad = round_up(vc, 8);
+    const TI *Wc = W + vb * D;
+    dim3 gp((unsigned)((M + C::BM - 1) / C::BM), (unsigned)((vc + C::BN - 1) / C::BN));
+    if (vk)
+      ce_prob_kernel<C, true><<<gp, C::NT, 0, s>>>(H, Wc, M, vc, D, vb, tcol, lse, inv, P, L.ldp,
+                                                   kpad, PT, L.ldht);
+    else
+      ce_prob_kernel<C, false><<<gp, C::NT, 0, s>>>(H, Wc, M, vc, D, vb, tcol, lse, inv, P, L.ldp,
+                                                    kpad, PT, L.ldht);
+    if ((e = check_launch("ce_prob"))) return e;
+    // dW[vb:vb+vc, :] = P_c^T H   (K = tokens, zero-padded to ldht)
+    if ((e = launch_gemm_store<C>(PT, L.ldht, Ht, L.ldht, dW + vb * D, D, vc, D, L.ldht, 0, s)))
+      return e;
+    // dH += P_c W_c   (K = chunk columns, zero-padded to kpad)
+    if ((e = launch_gemm_store<C>(P, L.ldp, Wt + vb, L.ldwt, dH, D, M, D, kpad, vb > 0 ? 1 : 0, s)))
+      return e;
+  }
+  return NF_OK;
+}
+
+}  // namespace ce
+}  // namespace nf
+
+using namespace nf;
+using namespace nf::ce;
+
+extern "C" size_t nf_ce_workspace(int64_t M, int64_t D, int64_t V, int64_t vocab_chunk,
+                                  int dtype) {
+  if (M <= 0 || D <= 0 || V <= 0 || vocab_chunk <= 0) return 0;
+  if (dtype != NF_DTYPE_BF16 && dtype != NF_DTYPE_F32) return 0;
+  return make_layout(M, D, V, vocab_chunk, dtype == NF_DTYPE_BF16 ? 2 : 4).total;
+}
+
+extern "C" int nf_ce_fwd_bwd(const void *hidden, const void *weight, const int64_t *targets,
+                             int64_t M, int64_t D, int64_t V, int64_t ignore_index,
+                             int64_t vocab_chunk, int dtype, float *loss, float *dhidden,
+                             float *dweight, int32_t *bad_targets, void *workspace,
+                             size_t workspace_bytes, void *stream) {
+  if (M <= 0 || D <= 0 || V <= 0 || vocab_chunk <= 0)
+    return set_error(NF_ERR_ARG, "nf_ce_fwd_bwd: bad shape M=%lld D=%lld V=%lld chunk=%lld",
+                     (long long)M, (long long)D, (long long)V, (long long)vocab_chunk);
+  if (V > 0x7fffffffLL || M > 0x7fffffffLL)
+    return set_error(NF_ERR_ARG, "nf_ce_fwd_bwd: M or V exceeds int32");
+  if (!hidden || !weight || !targets || !loss || !dhidden || !dweight)
+    return set_error(NF_ERR_ARG, "nf_ce_fwd_bwd: null pointer");
+  if (dtype != NF_DTYPE_BF16 && dtype != NF_DTYPE_F32)
+    return set_error(NF_ERR_DTYPE, "nf_ce_fwd_bwd: dtype %d unsupported (bf16 or f32)", dtype);
+  const size_t need = nf_ce_workspace(M, D, V, vocab_chunk, dtype);
+  if (!workspace || workspace_bytes < need || !aligned16(workspace))
+    return set_error(NF_ERR_WORKSPACE, "nf_ce_fwd_bwd: workspace %zu bytes < required %zu",
+                     workspace_bytes, need);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  char *ws = static_cast<char *>(workspace);
+  if (dtype == NF_DTYPE_BF16)
+    return ce_run<bf16>((const bf16 *)hidden, (const bf16 *)weight, targets, M, D, V,
+                        ignore_index, vocab_chunk, loss, dhidden, dweight, bad_targets, ws, s);
+  return ce_run<float>((const float *)hidden, (const float *)weight, targets, M, D, V,
+                       ignore_index, vocab_chunk, loss, dhidden, dweight, bad_targets, ws, s);
+}
+
+extern "C" int nf_scale_cast(const float *src, const float *grad_output, void *dst, int64_t n,
+                             int dtype, void *stream) {
+  if (n < 0) return set_error(NF_ERR_ARG, "nf_scale_cast: n < 0");
+  if (n == 0) return NF_OK;
+  if (!src || !grad_output || !dst) return set_error(NF_ERR_ARG, "nf_scale_cast: null pointer");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const bool vec = aligned16(src) && aligned16(dst);
+  const int64_t nchunks = (n + 7) / 8;
+  int64_t blocks = (nchunks + 255) / 256;
+  if (blocks > 4096) blocks = 4096;
+  const unsigned g = (unsigned)blocks;
+  switch (dtype) {
+    case NF_DTYPE_F32:
+      if (vec) scale_cast_kernel<float, true><<<g, 256, 0, s>>>(src, grad_output, (float *)dst, n);
+      else scale_cast_kernel<float, false><<<g, 256, 0, s>>>(src, grad_output, (float *)dst, n);
+      break;
+    case NF_DTYPE_BF16:
+      if (vec) scale_cast_kernel<bf16, true><<<g, 256, 0, s>>>(src, grad_output, (bf16 *)dst, n);
+      else scale_cast_kernel<bf16, false><<<g, 256, 0, s>>>(src, grad_output, (bf16 *)dst, n);
+      break;
+    case NF_DTYPE_F16:
+      if (vec) scale_cast_kernel<f16, true><<<g, 256, 0, s>>>(src, grad_output, (f16 *)dst, n);
+      else scale_cast_kernel<f16, false><<<g, 256, 0, s>>>(src, grad_output, (f16 *)dst, n);
+      break;
+    default:
+      return set_error(NF_ERR_DTYPE, "nf_scale_cast: dtype %d", dtype);
+  }
+  return check_launch("nf_scale_cast");
+}
+
+extern "C" int nf_gemm_nt(const void *A, int64_t lda, const void *B, int64_t ldb, float *C,
+                          int64_t ldc, int64_t M, int64_t N, int64_t K, int dtype,
+                          void *stream) {
+  if (M < 0 || N < 0 || K < 0) return set_error(NF_ERR_ARG, "nf_gemm_nt: negative size");
+  if (M == 0 || N == 0) return NF_OK;
+  if (!A || !B || !C) return set_error(NF_ERR_ARG, "nf_gemm_nt: null pointer");
+  if (lda < K || ldb < K || ldc < N) return set_error(NF_ERR_ARG, "nf_gemm_nt: bad leading dim");
+  if ((M + 127) / 128 > 0x7fffffffLL || (N + 127) / 128 > 65535)
+    return set_error(NF_ERR_ARG, "nf_gemm_nt: grid too large");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (dtype == NF_DTYPE_BF16)
+    return launch_gemm_store<MainCfg<bf16>>((const bf16 *)A, lda, (const bf16 *)B, ldb, C, ldc, M,
+                                            N, K, 0, s);
+  if (dtype == NF_DTYPE_F32)
+    return launch_gemm_store<MainCfg<float>>((const float *)A, lda, (const float *)B, ldb, C, ldc,
+                                             M, N, K, 0, s);
+  return set_error(NF_ERR_DTYPE, "nf_gemm_nt: dtype %d unsupported", dtype);
+}

@@ -1,0 +1,198 @@
+"""Memory-bounded cross entropy for the reasoning head, on MI355X MFMA.
+
+Drop-in for ``nuvla_forge/kernels/chunked_ce.py``: the same
+``_ChunkedCrossEntropy`` autograd Function (``forward(ctx, hidden, lm_weight,
+targets, chunk_size, ignore_index, force_reference) -> loss``; ``backward``
+returns 6 values, chunked_ce.py:120-182) and the same public
+``chunked_cross_entropy(hidden, lm_weight, targets, chunk_size=1024,
+ignore_index=-100, force_reference=False)`` (chunked_ce.py:185-208).
+
+Like the reference, the gradient is formed during the forward pass and the
+backward only scales it by ``grad_output`` and casts to the input dtypes.
+The device path is one call, ``nf_ce_fwd_bwd``: logits tiles are produced on
+bf16 (or fp32) MFMA, reduced to per-row log-sum-exp without being stored, and
+recomputed one vocabulary chunk at a time to form ``(softmax - onehot) / n``
+and both gradient GEMMs.  The valid-token count stays on the device, so the
+reference's ``.item()`` host sync is gone.
+
+``chunk_size`` keeps its meaning as the memory budget: the reference holds a
+[chunk_size, V] fp32 logits tile; this path holds an [M, vc] probability tile
+with vc = chunk_size * V / M rounded up to the 128-column MFMA tile (at most
+V).  Results do not depend on it beyond fp rounding.
+
+Element types: bf16 inputs run bf16 MFMA with fp32 accumulation; fp32 inputs
+run fp32 MFMA.  Mixed bf16/fp32 inputs compute in bf16 when autocast is on
+for the device (as the reference's autocast-ed ``F.linear`` does) and in fp32
+otherwise; fp16 inputs are widened to fp32.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from .. import _lib
+from .utils import device_of, require_device
+
+# Out-of-range targets (not ignore_index, outside [0, V)) raise ValueError.
+# The check reads one device int back to the host; it is skipped while a
+# stream is being captured into a graph (such rows count as ignored there).
+VALIDATE_TARGETS = True
+
+
+def vocab_chunk_for(chunk_size: int, m: int, v: int) -> int:
+    """Vocabulary columns per chunk holding the reference's [chunk_size, V] budget."""
+    if chunk_size <= 0:
+        raise ValueError(f"chunk_size must be positive, got {chunk_size}")
+    vc = -(-int(chunk_size) * v // max(m, 1))
+    vc = -(-vc // 128) * 128
+    return max(128, min(vc, -(-v // 8) * 8))
+
+
+def _compute_dtype(hidden: torch.Tensor, lm_weight: torch.Tensor) -> torch.dtype:
+    hd, wd = hidden.dtype, lm_weight.dtype
+    if hd == wd and hd in (torch.bfloat16, torch.float32):
+        return hd
+    if torch.bfloat16 in (hd, wd) and torch.is_autocast_enabled(hidden.device.type) and \
+            torch.get_autocast_dtype(hidden.device.type) == torch.bfloat16:
+        return torch.bfloat16
+    return torch.float32
+
+
+def _ce_chunk_torch(logits, targets, ignore_index, inv_count):
+    """One row chunk in ATen: (sum of row losses * inv, (softmax - onehot) * inv).
+
+    Same quantities as the reference's CPU chunk path (chunked_ce.py:101-117);
+    ignored rows get zero loss and a zero gradient row.
+    """
+    logits = logits.float()
+    keep = (targets != ignore_index).to(logits.dtype)
+    rows = torch.arange(targets.shape[0], device=logits.device)
+    cols = torch.where(targets != ignore_index, targets, torch.zeros_like(targets))
+    lse = torch.logsumexp(logits, dim=-1)
+    loss = (lse - logits[rows, cols]) * keep
+    grad = torch.exp(logits - lse.unsqueeze(1))
+    grad[rows, cols] -= 1.0
+    grad *= keep.unsqueeze(1)
+    return loss.sum() * inv_count, grad * inv_count
+
+
+def _forward_eager(hidden, lm_weight, targets, chunk_size, ignore_index):
+    """The reference's row-chunk loop in ATen (``force_reference=True``)."""
+    m = hidden.shape[0]
+    n_valid = int((targets != ignore_index).sum().item())
+    inv_count = 1.0 / max(n_valid, 1)
+    loss_total = hidden.new_zeros((), dtype=torch.float32)
+    d_hidden = torch.zeros_like(hidden, dtype=torch.float32)
+    d_weight = torch.zeros_like(lm_weight, dtype=torch.float32)
+    w = lm_weight.float()
+    for start in range(0, m, chunk_size):
+        stop = min(start + chunk_size, m)
+        h_chunk = hidden[start:stop].float()
+        logits = h_chunk @ w.T
+        chunk_loss, dlogits = _ce_chunk_torch(logits, targets[start:stop], ignore_index, inv_count)
+        loss_total = loss_total + chunk_loss
+        d_hidden[start:stop] = dlogits @ w
+        d_weight += dlogits.T @ h_chunk
+    return loss_total, d_hidden, d_weight
+
+
+def _forward_hip(hidden, lm_weight, targets, chunk_size, ignore_index):
+    m, d = hidden.shape
+    v = lm_weight.shape[0]
+    cdt = _compute_dtype(hidden, lm_weight)
+    h = hidden.to(cdt).contiguous()
+    w = lm_weight.to(cdt).contiguous()
+    tg = targets.to(torch.int64).contiguous()
+    dev = hidden.device
+    loss = torch.empty((), dtype=torch.float32, device=dev)
+    d_hidden = torch.empty((m, d), dtype=torch.float32, device=dev)
+    d_weight = torch.empty((v, d), dtype=torch.float32, device=dev)
+    bad = torch.empty(1, dtype=torch.int32, device=dev)
+    if m == 0:
+        loss.zero_(), d_hidden.zero_(), d_weight.zero_()
+        return loss, d_hidden, d_weight
+    vc = vocab_chunk_for(chunk_size, m, v)
+    L = _lib.lib()
+    code = _lib.dtype_code(cdt)
+    ws_bytes = L.nf_ce_workspace(m, d, v, vc, code)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+    with device_of(hidden):
+        _lib.check(
+            L.nf_ce_fwd_bwd(h.data_ptr(), w.data_ptr(), tg.data_ptr(), m, d, v, int(ignore_index),
+                            vc, code, loss.data_ptr(), d_hidden.data_ptr(), d_weight.data_ptr(),
+                            bad.data_ptr(), ws.data_ptr(), ws_bytes, _lib.stream_of(hidden)),
+            "nf_ce_fwd_bwd",
+        )
+    if VALIDATE_TARGETS and not torch.cuda.is_current_stream_capturing():
+        nbad = int(bad.item())
+        if nbad:
+            raise ValueError(f"chunked_cross_entropy: {nbad} target(s) outside [0, {v}) "
+                             f"and not ignore_index={ignore_index}")
+    return loss, d_hidden, d_weight
+
+
+class _ChunkedCrossEntropy(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, hidden, lm_weight, targets, chunk_size, ignore_index, force_reference):
+        if hidden.dim() != 2 or lm_weight.dim() != 2 or hidden.shape[1] != lm_weight.shape[1]:
+            raise ValueError(f"hidden [M, D] and lm_weight [V, D] expected, got "
+                             f"{tuple(hidden.shape)} and {tuple(lm_weight.shape)}")
+        if targets.shape != (hidden.shape[0],):
+            raise ValueError(f"targets must be [M={hidden.shape[0]}], got {tuple(targets.shape)}")
+        if force_reference:
+            loss, d_hidden, d_weight = _forward_eager(hidden, lm_weight, targets, chunk_size,
+                                                      ignore_index)
+        else:
+            loss, d_hidden, d_weight = _forward_hip(hidden, lm_weight, targets, chunk_size,
+                                                    ignore_index)
+        ctx.save_for_backward(d_hidden, d_weight)
+        ctx.hidden_dtype = hidden.dtype
+        ctx.weight_dtype = lm_weight.dtype
+        ctx.eager = force_reference
+        return loss
+
+    @staticmethod
+    def backward(ctx, grad_output):
+        d_hidden, d_weight = ctx.saved_tensors
+        if ctx.eager or not d_hidden.is_cuda:
+            g = grad_output
+            return ((d_hidden * g).to(ctx.hidden_dtype), (d_weight * g).to(ctx.weight_dtype),
+                    None, None, None, None)
+        g = grad_output.to(torch.float32).contiguous()
+        dh = torch.empty(d_hidden.shape, dtype=ctx.hidden_dtype, device=d_hidden.device)
+        dw = torch.empty(d_weight.shape, dtype=ctx.weight_dtype, device=d_weight.device)
+        L = _lib.lib()
+        with device_of(d_hidden):
+            s = _lib.stream_of(d_hidden)
+            _lib.check(L.nf_scale_cast(d_hidden.data_ptr(), g.data_ptr(), dh.data_ptr(),
+                                       d_hidden.numel(), _lib.dtype_code(dh), s), "nf_scale_cast")
+            _lib.check(L.nf_scale_cast(d_weight.data_ptr(), g.data_ptr(), dw.data_ptr(),
+                                       d_weight.numel(), _lib.dtype_code(dw), s), "nf_scale_cast")
+        return dh, dw, None, None, None, None
+
+
+def chunked_cross_entropy(
+    hidden: torch.Tensor,
+    lm_weight: torch.Tensor,
+    targets: torch.Tensor,
+    chunk_size: int = 1024,
+    ignore_index: int = -100,
+    force_reference: bool = False,
+) -> torch.Tensor:
+    """Mean cross entropy over ``hidden @ lm_weight.T`` without a full logit tensor.
+
+    Args:
+        hidden: [M, D] pre-projection hidden states.
+        lm_weight: [V, D] output embedding.
+        targets: [M] int64 class indices, ``ignore_index`` to mask.
+        chunk_size: memory budget in rows of a [chunk_size, V] logits tile.
+        ignore_index: target value that contributes no loss and no gradient.
+        force_reference: run the reference's eager row-chunk loop instead.
+
+    Returns:
+        Scalar fp32 loss, mean-reduced over non-ignored tokens (0 if none).
+    """
+    if not force_reference:
+        require_device(hidden, "chunked_cross_entropy")
+    return _ChunkedCrossEntropy.apply(hidden, lm_weight, targets, chunk_size, ignore_index,
+                                      force_reference)

@@ -1,0 +1,180 @@
+"""C ABI and host-side logic, CPU only (no kernel is launched here).
+
+Checks that libnf_hip.so loads, exports every function include/*.h declares,
+reports its ABI version, and rejects bad arguments with a status and a
+message before touching the GPU; and that the Python drop-in refuses CPU
+tensors on the fused path (no silent fallback) while ``force_reference=True``
+runs the eager formulation.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+from nuvla_forge_amd import _lib
+from nuvla_forge_amd import kernels as K
+from nuvla_forge_amd.kernels import chunked_ce, reference
+from oracle import numerics as on
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADERS = sorted((ROOT / "include").glob("*.h"))
+
+NF_OK, NF_ERR_ARG, NF_ERR_DTYPE, NF_ERR_WORKSPACE = 0, -1, -2, -3
+FAKE = 4096  # a non-null pointer value; every call below returns before using it
+
+
+def _declared() -> set[str]:
+    names: set[str] = set()
+    for h in HEADERS:
+        text = re.sub(r"/\*.*?\*/", "", h.read_text(), flags=re.S)
+        names |= set(re.findall(r"\b(nf_\w+)\s*\(", text))
+    return names
+
+
+def _err() -> str:
+    return _lib.lib().nf_last_error().decode()
+
+
+def test_library_exports_every_declared_symbol():
+    declared = _declared()
+    assert len(declared) >= 10, declared
+    raw = ctypes.CDLL(str(_lib.LIB_PATH))
+    missing = [n for n in sorted(declared) if not hasattr(raw, n)]
+    assert not missing, f"not exported: {missing}"
+    assert declared == set(_lib.SIGNATURES), "ctypes signature table out of sync with the header"
+
+
+def test_abi_version():
+    assert _lib.lib().nf_abi_version() == _lib.ABI_VERSION == 1
+    assert K.HAS_HIP and K.HAS_TRITON
+
+
+def test_swiglu_argument_validation():
+    L = _lib.lib()
+    assert L.nf_swiglu_fwd(FAKE, FAKE, FAKE, -1, 1, None) == NF_ERR_ARG
+    assert "n=-1" in _err()
+    assert L.nf_swiglu_fwd(None, FAKE, FAKE, 10, 1, None) == NF_ERR_ARG
+    assert "null" in _err()
+    assert L.nf_swiglu_fwd(FAKE, FAKE, FAKE, 10, 7, None) == NF_ERR_DTYPE
+    assert L.nf_swiglu_bwd(FAKE, FAKE, FAKE, FAKE, FAKE, 0, 1, None) == NF_OK  # empty: no launch
+
+
+def test_adaln_argument_validation():
+    L = _lib.lib()
+    args = [FAKE, 1024, FAKE, 1024, FAKE, 1024, FAKE, FAKE, 1024, FAKE, 1024, FAKE, FAKE, FAKE]
+    tail = [1e-6, 1, 1, 1, 1, 1, 1, None]
+    assert L.nf_adaln_fwd(*args, 100, 1024, 7, *tail) == NF_ERR_ARG  # M % T != 0
+    assert "multiple" in _err()
+    assert L.nf_adaln_fwd(*args, 64, 20000, 8, *tail) == NF_ERR_ARG  # N too large
+    assert "exceeds" in _err()
+    assert L.nf_adaln_fwd(*args, 64, 1024, 8, 1e-6, 1, 0, 1, 1, 1, 1, None) == NF_ERR_DTYPE  # bf16 x, f32 y
+    bad_ld = list(args)
+    bad_ld[1] = 512
+    assert L.nf_adaln_fwd(*bad_ld, 64, 1024, 8, *tail) == NF_ERR_ARG
+    assert L.nf_adaln_bwd_workspace(8192, 1024, 1024) > 8 * 1024 * 4
+    assert L.nf_adaln_bwd_workspace(10, 1024, 3) == 0
+    small = L.nf_adaln_bwd_workspace(64, 1024, 8)
+    bwd = [FAKE, FAKE, FAKE, 1024, FAKE, 1024, FAKE, 1024, FAKE, FAKE, 1024, FAKE, FAKE, FAKE,
+           None, None, None, None, FAKE, small - 1, 64, 1024, 8, 1, 1, 1, 1, 1, 1, None]
+    assert L.nf_adaln_bwd(*bwd) == NF_ERR_WORKSPACE
+    assert "workspace" in _err()
+
+
+def test_ce_argument_validation():
+    L = _lib.lib()
+    ws = L.nf_ce_workspace(4096, 2048, 32000, 4096, 1)
+    assert ws > 2048 * 32000 * 2  # holds W^T
+    assert L.nf_ce_workspace(4096, 2048, 32000, 4096, 2) == 0  # fp16 unsupported
+    base = [FAKE, FAKE, FAKE]
+    out = [FAKE, FAKE, FAKE, None, FAKE]
+    assert L.nf_ce_fwd_bwd(*base, 16, 8, 50, -100, 0, 1, *out, ws, None) == NF_ERR_ARG
+    assert L.nf_ce_fwd_bwd(*base, 16, 8, 50, -100, 64, 2, *out, ws, None) == NF_ERR_DTYPE
+    assert L.nf_ce_fwd_bwd(*base, 16, 8, 50, -100, 64, 1, *out, 16, None) == NF_ERR_WORKSPACE
+    assert L.nf_scale_cast(FAKE, FAKE, FAKE, -5, 1, None) == NF_ERR_ARG
+    assert L.nf_gemm_nt(FAKE, 4, FAKE, 4, FAKE, 2, 2, 2, 8, 1, None) == NF_ERR_ARG  # lda < K
+
+
+def test_vocab_chunk_budget():
+    assert chunked_ce.vocab_chunk_for(512, 4096, 32000) == 4096
+    assert chunked_ce.vocab_chunk_for(1024, 4096, 32000) == 8064
+    assert chunked_ce.vocab_chunk_for(4096, 512, 1000) == 1000
+    assert chunked_ce.vocab_chunk_for(1, 4096, 1000) == 128
+    with pytest.raises(ValueError):
+        chunked_ce.vocab_chunk_for(0, 10, 10)
+
+
+# ---------------------------------------------------------------------------
+# Python drop-in on the CPU
+# ---------------------------------------------------------------------------
+def test_fused_ops_refuse_cpu_tensors():
+    x = torch.randn(8, 16)
+    g = torch.zeros(2, 16)
+    with pytest.raises(RuntimeError, match="force_reference"):
+        K.fused_swiglu(x, x)
+    with pytest.raises(RuntimeError, match="force_reference"):
+        K.fused_adaln_residual_rmsnorm(x, x, g, torch.ones(16), g, g, 4)
+    with pytest.raises(RuntimeError, match="force_reference"):
+        K.chunked_cross_entropy(x, torch.randn(5, 16), torch.zeros(8, dtype=torch.long))
+
+
+def test_force_reference_adaln_matches_oracle():
+    gen = torch.Generator().manual_seed(0)
+    b, t, n = 2, 4, 32
+    x, y = (torch.randn(b * t, n, generator=gen, dtype=torch.float64, requires_grad=True)
+            for _ in range(2))
+    cond = [torch.randn(b, n, generator=gen, dtype=torch.float64, requires_grad=True)
+            for _ in range(3)]
+    w = torch.randn(n, generator=gen, dtype=torch.float64, requires_grad=True)
+    h, out = K.fused_adaln_residual_rmsnorm(x, y, cond[0], w, cond[1], cond[2], t,
+                                            force_reference=True)
+    dh, do = torch.randn_like(h), torch.randn_like(out)
+    torch.autograd.backward([h, out], [dh, do])
+    args = dict(x=x, y=y, gate=cond[0], weight=w, scale=cond[1], shift=cond[2])
+    npa = {k: v.detach().numpy() for k, v in args.items()}
+    hh, oo, _ = on.adaln_forward(**npa, t=t)
+    grads = on.adaln_backward(**npa, t=t, dh_up=dh.numpy(), dout=do.numpy())
+    assert on.rel_err(h.detach().numpy(), hh) < 1e-14
+    assert on.rel_err(out.detach().numpy(), oo) < 1e-6  # the eager path norms in fp32
+    for k, v in args.items():
+        assert on.rel_err(v.grad.numpy(), grads[k]) < 1e-6, k
+
+
+def test_force_reference_swiglu_and_ce():
+    gen = torch.Generator().manual_seed(1)
+    a = torch.randn(17, 33, generator=gen, requires_grad=True)
+    b = torch.randn(17, 33, generator=gen, requires_grad=True)
+    out = K.fused_swiglu(a, b, force_reference=True)
+    assert on.rel_err(out.detach().numpy(), on.swiglu_forward(a.detach().double().numpy(),
+                                                               b.detach().double().numpy())) < 1e-6
+    m, d, v = 64, 32, 200
+    hid = torch.randn(m, d, generator=gen, requires_grad=True)
+    w = (torch.randn(v, d, generator=gen) * 0.02).requires_grad_(True)
+    tgt = torch.randint(0, v, (m,), generator=gen)
+    tgt[::3] = -100
+    loss = K.chunked_cross_entropy(hid, w, tgt, chunk_size=16, force_reference=True)
+    loss.backward()
+    lo, dho, dwo = on.ce_forward_backward(hid.detach().double().numpy(),
+                                          w.detach().double().numpy(), tgt.numpy())
+    assert float(loss) == pytest.approx(lo, rel=1e-5)
+    assert on.rel_err(hid.grad.numpy(), dho) < 1e-5
+    assert on.rel_err(w.grad.numpy(), dwo) < 1e-5
+    assert torch.all(hid.grad[::3] == 0)
+    allign = torch.full((m,), -100)
+    z = K.chunked_cross_entropy(hid, w, allign, chunk_size=16, force_reference=True)
+    assert float(z) == 0.0
+
+
+def test_eager_reference_module_matches_textbook_ce():
+    gen = torch.Generator().manual_seed(2)
+    hid = torch.randn(32, 8, generator=gen)
+    w = torch.randn(40, 8, generator=gen)
+    tgt = torch.randint(0, 40, (32,), generator=gen)
+    lo, _, _ = on.ce_forward_backward(hid.double().numpy(), w.double().numpy(), tgt.numpy())
+    assert float(reference.chunked_cross_entropy_ref(hid, w, tgt)) == pytest.approx(lo, rel=1e-5)
+    assert np.isfinite(lo)

@@ -1,0 +1,216 @@
+"""adaLN seam HIP kernels vs the oracle (GPU).
+
+Covers BASELINE cfg1 (fp32 [2,64,256], all six gradients at 1e-5) and cfg2
+(bf16 [8,1024,1024], 10 bit-identical backward passes), the reference's test
+shapes (tests/test_kernels.py:85-115, incl. the N=1000 masked tail), odd N
+(element-wise kernel variant), wide N (multi-wavefront rows), mixed autocast
+dtypes, strided / broadcast conditioning views as the DiT block passes them
+(model/dit.py:146-166), missing upstream gradients, and the large seam stress
+shape [32,2048,2048] checked sample by sample.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from nuvla_forge_amd.kernels import fused_adaln_residual_rmsnorm
+from oracle import numerics as on
+from tests.helpers import TOL, gen, note, np64, randn
+
+pytestmark = pytest.mark.gpu
+
+NAMES = ("x", "y", "gate", "weight", "scale", "shift")
+
+
+def _inputs(b, t, n, dtype, dev, seed=0, cond_dtype=None, y_dtype=None):
+    """BASELINE distributions: x, y ~ N(0,1); cond ~ N(0, 0.1); w = 1 + N(0, 0.02)."""
+    g = gen(seed)
+    cd = cond_dtype or dtype
+    return {
+        "x": randn((b * t, n), g, dtype, dev),
+        "y": randn((b * t, n), g, y_dtype or dtype, dev),
+        "gate": randn((b, n), g, cd, dev, std=0.1),
+        "weight": randn((n,), g, cd, dev, std=0.02, mean=1.0),
+        "scale": randn((b, n), g, cd, dev, std=0.1),
+        "shift": randn((b, n), g, cd, dev, std=0.1),
+    }
+
+
+def _upstream(m, n, dtype, dev, seed=1):
+    g = gen(seed)
+    return randn((m, n), g, dtype, dev), randn((m, n), g, dtype, dev)
+
+
+def _run(inp, t, dh, dout):
+    leaves = {k: v.detach().requires_grad_(True) for k, v in inp.items()}
+    h, out = fused_adaln_residual_rmsnorm(**leaves, tokens_per_sample=t)
+    torch.autograd.backward([h, out], [dh, dout])
+    torch.cuda.synchronize()
+    return h.detach(), out.detach(), {k: v.grad for k, v in leaves.items()}
+
+
+def _check(inp, t, dh, dout, h, out, grads, tol, label, eps=1e-6):
+    a = {k: np64(v) for k, v in inp.items()}
+    hw, ow, _ = on.adaln_forward(**a, t=t, eps=eps)
+    gw = on.adaln_backward(**a, t=t, dh_up=np64(dh), dout=np64(dout), eps=eps)
+    errs = {"h": on.rel_err(np64(h), hw), "out": on.rel_err(np64(out), ow)}
+    for k in NAMES:
+        errs["d" + k] = on.rel_err(np64(grads[k]), gw[k])
+    bad = {k: v for k, v in errs.items() if not v <= tol}
+    assert not bad, f"{label}: rel err above {tol}: {bad}"
+    return errs
+
+
+def test_cfg1_fp32_all_six_gradients(cuda):
+    note("adaln cfg1 fp32 [2,64,256]")
+    b, t, n = 2, 64, 256
+    inp = _inputs(b, t, n, torch.float32, cuda)
+    dh, dout = _upstream(b * t, n, torch.float32, cuda)
+    h, out, grads = _run(inp, t, dh, dout)
+    _check(inp, t, dh, dout, h, out, grads, 1e-5, "cfg1")
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("b,t,n", [(2, 16, 256), (4, 32, 1024), (3, 7, 768), (1, 64, 1536),
+                                   (2, 8, 1000), (2, 3, 333), (1, 5, 8), (2, 4, 4096),
+                                   (1, 2, 16384)])
+def test_adaln_matches_oracle(cuda, dtype, b, t, n):
+    note(f"adaln dtype={dtype} b={b} t={t} n={n}")
+    inp = _inputs(b, t, n, dtype, cuda)
+    dh, dout = _upstream(b * t, n, dtype, cuda)
+    h, out, grads = _run(inp, t, dh, dout)
+    assert h.dtype == dtype and out.dtype == dtype
+    for k in NAMES:
+        assert grads[k].dtype == inp[k].dtype and grads[k].shape == inp[k].shape
+    _check(inp, t, dh, dout, h, out, grads, TOL[dtype], f"{dtype} ({b},{t},{n})")
+
+
+def test_cfg2_bf16_and_bitwise_deterministic_backward(cuda):
+    note("adaln cfg2 bf16 [8,1024,1024] x10 backward")
+    b, t, n = 8, 1024, 1024
+    inp = _inputs(b, t, n, torch.bfloat16, cuda)
+    dh, dout = _upstream(b * t, n, torch.bfloat16, cuda)
+    h, out, grads = _run(inp, t, dh, dout)
+    _check(inp, t, dh, dout, h, out, grads, 2e-2, "cfg2")
+    for _ in range(9):
+        _, _, again = _run(inp, t, dh, dout)
+        for k in NAMES:
+            assert torch.equal(again[k], grads[k]), f"d{k} differs between runs"
+
+
+def test_mixed_autocast_dtypes(cuda):
+    """x fp32 residual, y bf16 branch output, bf16 conditioning, fp32 weight."""
+    note("adaln mixed dtypes")
+    b, t, n = 2, 32, 512
+    inp = _inputs(b, t, n, torch.float32, cuda, cond_dtype=torch.bfloat16, y_dtype=torch.bfloat16)
+    inp["weight"] = inp["weight"].float()
+    dh, dout = _upstream(b * t, n, torch.float32, cuda)
+    h, out, grads = _run(inp, t, dh, dout)
+    assert h.dtype == torch.float32 and grads["y"].dtype == torch.bfloat16
+    assert grads["gate"].dtype == torch.bfloat16 and grads["weight"].dtype == torch.float32
+    _check(inp, t, dh, dout, h, out, grads, 2e-2, "mixed")
+
+
+def test_strided_and_broadcast_conditioning(cuda):
+    """chunk(6) views (row stride 6N) and expand()-ed zeros/ones (row stride 0)."""
+    note("adaln strided cond")
+    b, t, n = 4, 16, 256
+    g = gen(5)
+    x = randn((b * t, n), g, torch.float32, cuda)
+    y = randn((b * t, n), g, torch.float32, cuda)
+    w = randn((n,), g, torch.float32, cuda, std=0.02, mean=1.0)
+    cond = randn((b, 6 * n), g, torch.float32, cuda, std=0.1).requires_grad_(True)
+    shift1, scale1, gate1, shift2, scale2, gate2 = cond.chunk(6, dim=-1)
+    zeros = torch.zeros(1, n, device=cuda).expand(b, n)
+    ones = torch.ones(1, n, device=cuda).expand(b, n)
+    dh, dout = _upstream(b * t, n, torch.float32, cuda)
+    for gate, scale, shift in ((gate1, zeros, zeros), (ones, scale2, shift2)):
+        cond.grad = None
+        xs = x.detach().requires_grad_(True)
+        ws = w.detach().requires_grad_(True)
+        h, out = fused_adaln_residual_rmsnorm(xs, y, gate, ws, scale, shift, tokens_per_sample=t)
+        torch.autograd.backward([h, out], [dh, dout])
+        a = dict(x=np64(x), y=np64(y), gate=np64(gate), weight=np64(w), scale=np64(scale),
+                 shift=np64(shift))
+        hw, ow, _ = on.adaln_forward(**a, t=t)
+        gw = on.adaln_backward(**a, t=t, dh_up=np64(dh), dout=np64(dout))
+        assert on.rel_err(np64(out), ow) < 1e-5 and on.rel_err(np64(h), hw) < 1e-5
+        assert on.rel_err(np64(xs.grad), gw["x"]) < 1e-5
+        assert on.rel_err(np64(ws.grad), gw["weight"]) < 1e-5
+        # gradients land in the right sixth of the cond projection
+        cg = np64(cond.grad).reshape(b, 6, n)
+        if gate is gate1:
+            assert on.rel_err(cg[:, 2], gw["gate"]) < 1e-5
+            assert not cg[:, [0, 1, 3, 4, 5]].any()
+        else:
+            assert on.rel_err(cg[:, 4], gw["scale"]) < 1e-5
+            assert on.rel_err(cg[:, 3], gw["shift"]) < 1e-5
+            assert not cg[:, [0, 1, 2, 5]].any()
+
+
+@pytest.mark.parametrize("which", ["h_only", "out_only"])
+def test_missing_upstream_gradient(cuda, which):
+    note(f"adaln upstream {which}")
+    b, t, n = 2, 8, 512
+    inp = _inputs(b, t, n, torch.float32, cuda)
+    leaves = {k: v.detach().requires_grad_(True) for k, v in inp.items()}
+    h, out = fused_adaln_residual_rmsnorm(**leaves, tokens_per_sample=t)
+    g = randn((b * t, n), gen(3), torch.float32, cuda)
+    (h if which == "h_only" else out).backward(g)
+    torch.cuda.synchronize()
+    a = {k: np64(v) for k, v in inp.items()}
+    gw = on.adaln_backward(**a, t=t, dh_up=np64(g) if which == "h_only" else None,
+                           dout=np64(g) if which == "out_only" else None)
+    for k in NAMES:
+        got = leaves[k].grad
+        want = gw[k]
+        if got is None:
+            assert not np.any(want), k
+        else:
+            assert on.rel_err(np64(got), want) < 1e-5, k
+
+
+def test_zero_gate_keeps_residual_exact(cuda):
+    note("adaln zero gate")
+    b, t, n = 2, 16, 1024
+    inp = _inputs(b, t, n, torch.bfloat16, cuda)
+    inp["gate"] = torch.zeros_like(inp["gate"])
+    h, _ = fused_adaln_residual_rmsnorm(**inp, tokens_per_sample=t)
+    assert torch.equal(h, inp["x"])
+
+
+def test_rejects_bad_shapes(cuda):
+    x = torch.zeros(10, 64, device=cuda)
+    c = torch.zeros(2, 64, device=cuda)
+    with pytest.raises(ValueError):
+        fused_adaln_residual_rmsnorm(x, x, c, torch.ones(64, device=cuda), c, c, 3)
+    c3 = torch.zeros(3, 64, device=cuda)
+    with pytest.raises(ValueError):  # T = 5 gives B = 2, not 3
+        fused_adaln_residual_rmsnorm(x, x, c3, torch.ones(64, device=cuda), c3, c3, 5)
+    big = torch.zeros(2, 16385, device=cuda)
+    cb = torch.zeros(1, 16385, device=cuda)
+    with pytest.raises(ValueError):
+        fused_adaln_residual_rmsnorm(big, big, cb, torch.ones(16385, device=cuda), cb, cb, 2)
+
+
+def test_stress_shape(cuda):
+    """BASELINE cfg5 seam: bf16 [32, 2048, 2048], oracle evaluated in fp32 on the host."""
+    note("adaln stress bf16 [32,2048,2048]")
+    b, t, n = 32, 2048, 2048
+    inp = _inputs(b, t, n, torch.bfloat16, cuda, seed=7)
+    dh, dout = _upstream(b * t, n, torch.bfloat16, cuda, seed=8)
+    h, out, grads = _run(inp, t, dh, dout)
+
+    def f32(v):
+        return v.to("cpu", torch.float32).numpy()
+
+    a = {k: f32(v) for k, v in inp.items()}
+    hw, ow, _ = on.adaln_forward(**a, t=t)
+    gw = on.adaln_backward(**a, t=t, dh_up=f32(dh), dout=f32(dout))
+    errs = {"h": on.rel_err(f32(h), hw), "out": on.rel_err(f32(out), ow)}
+    for k in NAMES:
+        errs["d" + k] = on.rel_err(f32(grads[k]), gw[k])
+    bad = {k: v for k, v in errs.items() if not v <= 2e-2}
+    assert not bad, bad

@@ -1,0 +1,160 @@
+"""Chunked cross entropy and its MFMA GEMM core vs the oracle (GPU).
+
+nf_gemm_nt is driven directly through the C ABI at ragged sizes first: it
+checks the MFMA operand/accumulator lane layouts the cross entropy relies on.
+Then the op through the autograd Function: the reference's test cases
+(tests/test_kernels.py:182-237: M512 H64 V1000 at chunk 128/4096, every 3rd
+row ignored, all rows ignored), ragged shapes (non-multiple-of-8 D and V),
+bad targets, grad_output scaling, and BASELINE cfg4 (bf16 M4096 D2048 V32000,
+10% ignored) against an fp32 host oracle, with a bit-identical rerun.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from nuvla_forge_amd import _lib
+from nuvla_forge_amd.kernels import chunked_cross_entropy
+from oracle import numerics as on
+from tests.helpers import TOL, gen, note, np64, randn
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("m,n,k", [(128, 128, 64), (32, 32, 16), (200, 130, 72), (1, 1, 8),
+                                   (257, 383, 1000), (64, 96, 36), (96, 64, 1), (512, 256, 2048)])
+def test_gemm_nt_matches_numpy(cuda, dtype, m, n, k):
+    note(f"gemm_nt dtype={dtype} m={m} n={n} k={k}")
+    g = gen(0)
+    a = randn((m, k), g, dtype, cuda)
+    b = randn((n, k), g, dtype, cuda)
+    c = torch.full((m, n), float("nan"), device=cuda)
+    L = _lib.lib()
+    _lib.check(L.nf_gemm_nt(a.data_ptr(), k, b.data_ptr(), k, c.data_ptr(), n, m, n, k,
+                            _lib.dtype_code(dtype), _lib.stream_of(a)), "nf_gemm_nt")
+    torch.cuda.synchronize()
+    want = np64(a) @ np64(b).T
+    assert on.rel_err(np64(c), want) < 1e-5
+
+
+def test_gemm_nt_leading_dimensions(cuda):
+    note("gemm_nt strided operands")
+    g = gen(1)
+    base_a = randn((100, 96), g, torch.bfloat16, cuda)
+    base_b = randn((70, 80), g, torch.bfloat16, cuda)
+    c = torch.zeros(100, 90, device=cuda)
+    L = _lib.lib()
+    # A = base_a[:, 8:72] (lda 96), B = base_b[:, 16:80] (ldb 80), C = c[:, :70] (ldc 90)
+    _lib.check(L.nf_gemm_nt(base_a[:, 8:].data_ptr(), 96, base_b[:, 16:].data_ptr(), 80,
+                            c.data_ptr(), 90, 100, 70, 64, 1, _lib.stream_of(c)), "nf_gemm_nt")
+    torch.cuda.synchronize()
+    want = np64(base_a[:, 8:72]) @ np64(base_b[:, 16:80]).T
+    assert on.rel_err(np64(c[:, :70]), want) < 1e-5
+    assert not c[:, 70:].any()
+
+
+def _ce_inputs(m, d, v, dtype, dev, seed=0, w_std=0.02, ignore=None):
+    g = gen(seed)
+    hid = randn((m, d), g, dtype, dev)
+    w = randn((v, d), g, dtype, dev, std=w_std)
+    tgt = torch.randint(0, v, (m,), generator=g)
+    if ignore is not None:
+        tgt[ignore] = -100
+    return hid, w, tgt.to(dev)
+
+
+def _run_ce(hid, w, tgt, chunk, scale=1.0):
+    h = hid.detach().requires_grad_(True)
+    ww = w.detach().requires_grad_(True)
+    loss = chunked_cross_entropy(h, ww, tgt, chunk_size=chunk)
+    (loss * scale).backward()
+    torch.cuda.synchronize()
+    return loss.detach(), h.grad, ww.grad
+
+
+def _check_ce(hid, w, tgt, loss, dh, dw, tol, label, scale=1.0):
+    lo, dho, dwo = on.ce_forward_backward(np64(hid), np64(w), tgt.cpu().numpy())
+    errs = {"loss": abs(float(loss) - lo) / max(abs(lo), 1e-30) if lo else abs(float(loss)),
+            "dh": on.rel_err(np64(dh), scale * dho), "dw": on.rel_err(np64(dw), scale * dwo)}
+    bad = {k: v for k, v in errs.items() if not v <= tol}
+    assert not bad, f"{label}: {bad}"
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("chunk", [128, 4096])
+def test_ce_reference_case(cuda, dtype, chunk):
+    """m, h, v = 512, 64, 1000 (reference tests/test_kernels.py:182-201)."""
+    note(f"ce ref case dtype={dtype} chunk={chunk}")
+    hid, w, tgt = _ce_inputs(512, 64, 1000, dtype, cuda)
+    loss, dh, dw = _run_ce(hid, w, tgt, chunk)
+    assert dh.dtype == dtype and dw.dtype == dtype and loss.dtype == torch.float32
+    _check_ce(hid, w, tgt, loss, dh, dw, TOL[dtype], f"{dtype} chunk {chunk}")
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_ce_respects_ignore_index(cuda, dtype):
+    note(f"ce ignore_index dtype={dtype}")
+    hid, w, tgt = _ce_inputs(64, 32, 200, dtype, cuda, seed=3, ignore=slice(None, None, 3))
+    loss, dh, dw = _run_ce(hid, w, tgt, 16)
+    _check_ce(hid, w, tgt, loss, dh, dw, TOL[dtype], "ignore")
+    assert torch.all(dh[::3] == 0)
+
+
+def test_ce_all_ignored_is_zero(cuda):
+    note("ce all ignored")
+    hid, w, _ = _ce_inputs(16, 8, 50, torch.float32, cuda)
+    tgt = torch.full((16,), -100, device=cuda)
+    loss, dh, dw = _run_ce(hid, w, tgt, 4)
+    assert float(loss) == 0.0
+    assert not dh.any() and not dw.any()
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("m,d,v,chunk", [(17, 36, 333, 7), (300, 40, 1030, 1000), (9, 4, 6, 1),
+                                         (130, 264, 129, 64)])
+def test_ce_ragged_shapes(cuda, dtype, m, d, v, chunk):
+    note(f"ce ragged dtype={dtype} m={m} d={d} v={v} chunk={chunk}")
+    hid, w, tgt = _ce_inputs(m, d, v, dtype, cuda, seed=4, w_std=0.3,
+                             ignore=slice(None, None, 4))
+    loss, dh, dw = _run_ce(hid, w, tgt, chunk)
+    _check_ce(hid, w, tgt, loss, dh, dw, TOL[dtype], f"ragged {m},{d},{v}")
+
+
+def test_ce_grad_output_scaling(cuda):
+    note("ce grad scaling")
+    hid, w, tgt = _ce_inputs(128, 64, 500, torch.float32, cuda, seed=5)
+    loss, dh, dw = _run_ce(hid, w, tgt, 64, scale=3.0)
+    _check_ce(hid, w, tgt, loss, dh, dw, 1e-5, "scaled", scale=3.0)
+
+
+def test_ce_rejects_out_of_range_targets(cuda):
+    note("ce bad target")
+    hid, w, tgt = _ce_inputs(32, 16, 40, torch.float32, cuda)
+    tgt[5] = 40
+    with pytest.raises(ValueError, match="outside"):
+        chunked_cross_entropy(hid, w, tgt)
+
+
+def test_ce_cfg4_bf16_full_size_and_deterministic(cuda):
+    """BASELINE cfg4: bf16 M4096 D2048 V32000, 409 rows ignored (M_valid 3687)."""
+    note("ce cfg4 bf16 M4096 D2048 V32000")
+    m, d, v = 4096, 2048, 32000
+    g = gen(2)
+    hid = randn((m, d), gen(0), torch.bfloat16, cuda)
+    w = randn((v, d), gen(1), torch.bfloat16, cuda, std=0.02)
+    tgt = torch.randint(0, v, (m,), generator=g)
+    tgt[torch.randperm(m, generator=g)[:409]] = -100
+    tgt = tgt.to(cuda)
+    loss, dh, dw = _run_ce(hid, w, tgt, 512)  # 512 rows of budget -> 4096-column vocab chunks
+    loss2, dh2, dw2 = _run_ce(hid, w, tgt, 512)
+    assert torch.equal(loss, loss2) and torch.equal(dh, dh2) and torch.equal(dw, dw2)
+    H = hid.float().cpu().numpy()
+    W = w.float().cpu().numpy()
+    lo, dho, dwo = on.ce_forward_backward(H, W, tgt.cpu().numpy())
+    assert abs(float(loss) - lo) / lo < 2e-2
+    assert on.rel_err(dh.float().cpu().numpy(), dho) < 2e-2
+    assert on.rel_err(dw.float().cpu().numpy(), dwo) < 2e-2
+    assert np.all(dh.float().cpu().numpy()[(tgt == -100).cpu().numpy()] == 0)

@@ -1,0 +1,93 @@
+"""SwiGLU HIP kernels vs the oracle (GPU).
+
+Shapes follow the reference's tests/test_kernels.py:141-159 plus BASELINE's
+[8192, 4096] bf16 config, a one-element tensor and misaligned views (the
+scalar-load kernel variant).
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from nuvla_forge_amd.kernels import fused_swiglu
+from oracle import numerics as on
+from tests.helpers import TOL, gen, note, np64, randn
+
+pytestmark = pytest.mark.gpu
+
+SHAPES = [(64, 512), (128, 2048), (17, 333), (1, 1), (8192, 4096)]
+
+
+def _run(a, b, dout):
+    a = a.detach().requires_grad_(True)
+    b = b.detach().requires_grad_(True)
+    out = fused_swiglu(a, b)
+    out.backward(dout)
+    torch.cuda.synchronize()
+    return out.detach(), a.grad, b.grad
+
+
+def _check(a, b, dout, out, da, db, dtype, label):
+    A, B, G = np64(a), np64(b), np64(dout)
+    want_da, want_db = on.swiglu_backward(A, B, G)
+    tol = TOL[dtype]
+    for name, got, want in (("out", out, on.swiglu_forward(A, B)), ("da", da, want_da),
+                            ("db", db, want_db)):
+        err = on.rel_err(np64(got), want)
+        assert err <= tol, f"{label} {name}: rel err {err:.3e} > {tol}"
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("shape", SHAPES)
+def test_swiglu_matches_oracle(cuda, dtype, shape):
+    note(f"swiglu dtype={dtype} shape={shape}")
+    g = gen(0)
+    a, b, dout = (randn(shape, g, dtype, cuda) for _ in range(3))
+    out, da, db = _run(a, b, dout)
+    assert out.dtype == dtype and da.dtype == dtype and db.dtype == dtype
+    _check(a, b, dout, out, da, db, dtype, f"{dtype} {shape}")
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_swiglu_misaligned_views(cuda, dtype):
+    """Storage offsets of one element force the element-wise (non-vector) kernel."""
+    note(f"swiglu misaligned dtype={dtype}")
+    g = gen(1)
+    n = 4099
+    base = [randn((n + 1,), g, dtype, cuda) for _ in range(3)]
+    a, b, dout = (t[1:] for t in base)
+    out, da, db = _run(a, b, dout)
+    _check(a, b, dout, out, da, db, dtype, "misaligned")
+
+
+def test_swiglu_saturation_and_zero(cuda):
+    note("swiglu saturation")
+    a = torch.tensor([0.0, 80.0, -80.0, 1e-30, -1e-30, 20.0, -20.0], device=cuda)
+    b = torch.full_like(a, 2.0)
+    dout = torch.ones_like(a)
+    out, da, db = _run(a, b, dout)
+    assert torch.isfinite(out).all() and torch.isfinite(da).all() and torch.isfinite(db).all()
+    assert out[0].item() == 0.0 and out[1].item() == pytest.approx(160.0)
+    assert abs(out[2].item()) < 1e-20
+    assert da[0].item() == pytest.approx(1.0)  # b * silu'(0) = 2 * 0.5
+    _check(a, b, dout, out, da, db, torch.float32, "saturation")
+
+
+def test_swiglu_is_deterministic(cuda):
+    note("swiglu determinism")
+    g = gen(2)
+    a, b, dout = (randn((1024, 1000), g, torch.bfloat16, cuda) for _ in range(3))
+    first = _run(a, b, dout)
+    for _ in range(3):
+        again = _run(a, b, dout)
+        for x, y in zip(first, again):
+            assert torch.equal(x, y)
+
+
+def test_swiglu_rejects_mismatched_inputs(cuda):
+    a = torch.zeros(4, 4, device=cuda)
+    with pytest.raises(ValueError):
+        fused_swiglu(a, torch.zeros(4, 5, device=cuda))
+    with pytest.raises(TypeError):
+        fused_swiglu(a, torch.zeros(4, 4, device=cuda, dtype=torch.bfloat16))
