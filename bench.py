@@ -1,0 +1,529 @@
+#!/usr/bin/env python3
+"""Benchmark of the fused adaLN-RMSNorm / SwiGLU / chunked-CE path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps 50] [--warmup 10] [--no-extra] [--no-cpu]
+
+Prints ONE JSON line (the driver's contract).  The headline workload is
+fused_adaln_residual_rmsnorm forward + backward in bf16 at
+the DiT-block shape B=8, T=1024, N=1024 (synthetic N(0,1) activations, N(0,0.1)
+conditioning, weight 1+N(0,0.02)).  A "step" is one forward plus one autograd
+backward through the drop-in Function, all inputs resident in HBM.
+
+Timing:
+  * value / ms_per_step: K steps as K/10 replays of a HIP graph holding 10
+    consecutive steps (fresh leaves; warmup and capture on one side stream),
+    bracketed by events + synchronize -- one graph launch per 10 steps, as a
+    training loop's graph amortises it; the one-step-per-graph time is
+    reported beside it;
+    value = algorithmic bytes (10*M*N + 6*B*N + 2*N) * 2 / ms_per_step.
+    The graph's outputs are compared bitwise with an eager step.
+  * roofline: the dominant kernel (the backward row kernel, nf_adaln_bwd) on
+    the step's inputs: 20 back-to-back launches captured in a HIP graph,
+    replayed K times between two events on its launch stream; achieved = its
+    algorithmic bytes (6*M*N + 2*B*N + N) * 2 per launch / mean launch time;
+    peak = 8 TB/s HBM.
+  * cpu_baseline: oracle/torch_cpu.py (the reference's eager PyTorch path,
+    forward + autograd backward) on the host cores for the same workload.
+  * extra: SwiGLU bf16 [8192, 4096], chunked CE bf16 M4096 D2048
+    V32000 with 409 ignored rows (configs[3], tokens/s and MFMA fraction of
+    2.5 PFLOP/s on 6*M_valid*V*D), the cfg5 stress chain, their CPU baselines.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
+STEPS_PER_GRAPH = 10            # consecutive steps captured in one HIP graph
+MFMA_BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16
+
+
+def log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+def parse() -> argparse.Namespace:
+    ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--no-extra", action="store_true", help="headline workload only")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baselines")
+    ap.add_argument("--json-out", default=None, help="also write the JSON record here")
+    return ap.parse_args()
+
+
+# ---------------------------------------------------------------------------
+# timing helpers
+# ---------------------------------------------------------------------------
+def _sync():
+    import torch
+
+    torch.cuda.synchronize()
+
+
+def time_eager(step, steps: int, warmup: int) -> float:
+    import torch
+
+    for _ in range(warmup):
+        step()
+    _sync()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        step()
+    e1.record()
+    _sync()
+    return e0.elapsed_time(e1) / steps
+
+
+def time_graph(make_step, steps: int, warmup: int, per_graph: int = 1):
+    """Capture `per_graph` consecutive steps in one HIP graph and time
+    `steps` steps (steps / per_graph replays).
+
+    `make_step()` must build the step around fresh leaf tensors: their
+    AccumulateGrad nodes are then created on the side stream that both warms
+    up and captures the step, so autograd never has to synchronise the
+    (non-capturing) default stream with the capture.  Returns (ms per step,
+    outputs of the last captured step, graph).
+    """
+    import torch
+
+    per_graph = max(1, min(per_graph, steps))
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        step = make_step()
+        for _ in range(max(warmup, 2)):
+            step()
+    side.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=side):
+        for _ in range(per_graph):
+            outs = step()
+    torch.cuda.current_stream().wait_stream(side)
+    for _ in range(max(1, warmup // per_graph)):
+        graph.replay()
+    _sync()
+    replays = max(1, steps // per_graph)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(replays):
+        graph.replay()
+    e1.record()
+    _sync()
+    return e0.elapsed_time(e1) / (replays * per_graph), outs, graph
+
+
+def same(a, b) -> bool:
+    import torch
+
+    return all(torch.equal(x, y) for x, y in zip(a, b))
+
+
+def cpu_threads() -> int:
+    # the GPU box's CPU share is 16 cores per GPU, whatever the affinity mask says
+    return max(1, min(16, len(os.sched_getaffinity(0))))
+
+
+def time_cpu(fn, budget_s: float = 20.0, min_reps: int = 1, max_reps: int = 3) -> float:
+    """1 warmup, then up to max_reps timed reps within budget; median seconds."""
+    t0 = time.perf_counter()
+    fn()
+    first = time.perf_counter() - t0
+    reps = []
+    while len(reps) < max_reps and (len(reps) < min_reps or sum(reps) + first < budget_s):
+        t0 = time.perf_counter()
+        fn()
+        reps.append(time.perf_counter() - t0)
+    return statistics.median(reps)
+
+
+# ---------------------------------------------------------------------------
+# workloads
+# ---------------------------------------------------------------------------
+def adaln_inputs(b, t, n, dev, seed=0):
+    import torch
+
+    g = torch.Generator().manual_seed(seed)
+    bf = torch.bfloat16
+
+    def r(*shape, std=1.0, mean=0.0):
+        return (torch.randn(*shape, generator=g) * std + mean).to(bf).to(dev)
+
+    inp = {"x": r(b * t, n), "y": r(b * t, n), "gate": r(b, n, std=0.1),
+           "weight": r(n, std=0.02, mean=1.0), "scale": r(b, n, std=0.1),
+           "shift": r(b, n, std=0.1)}
+    g1 = torch.Generator().manual_seed(seed + 1)
+    dh = torch.randn(b * t, n, generator=g1).to(bf).to(dev)
+    dout = torch.randn(b * t, n, generator=g1).to(bf).to(dev)
+    return inp, dh, dout
+
+
+def adaln_step_fn(inp, t, dh, dout):
+    """A fwd + autograd-bwd step over fresh leaves sharing `inp`'s storage."""
+    import torch
+
+    from nuvla_forge_amd.kernels import fused_adaln_residual_rmsnorm
+
+    leaves = [v.detach().requires_grad_(True) for v in inp.values()]
+
+    def step():
+        h, out = fused_adaln_residual_rmsnorm(*leaves, tokens_per_sample=t)
+        grads = torch.autograd.grad([h, out], leaves, [dh, dout])
+        return (h, out, *grads)
+
+    return step
+
+
+def adaln_alg_bytes(b, t, n, e=2):
+    m = b * t
+    return (10 * m * n + 6 * b * n + 2 * n) * e
+
+
+def per_launch_ms(launch, steps: int, reps: int = 20) -> float:
+    """Mean duration of one launch: `reps` back-to-back launches captured in a
+    HIP graph (on a side stream), replayed `steps` times between two events on
+    the stream the kernels run on."""
+    import torch
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        launch()
+    side.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=side):
+        for _ in range(reps):
+            launch()
+    torch.cuda.current_stream().wait_stream(side)
+    graph.replay()
+    _sync()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        graph.replay()
+    e1.record()
+    _sync()
+    return e0.elapsed_time(e1) / (steps * reps)
+
+
+def adaln_kernel_ms(inp, t, dh, dout, steps):
+    """Per-launch time of nf_adaln_fwd / nf_adaln_bwd / nf_adaln_bwd_reduce on
+    the step's own inputs."""
+    import torch
+
+    from nuvla_forge_amd import _lib
+
+    L, dc = _lib.lib(), _lib.dtype_code
+    x, y, gate, w, scale, shift = (inp[k] for k in ("x", "y", "gate", "weight", "scale", "shift"))
+    m, n = x.shape
+    b = m // t
+    h, out, dx, dy = (torch.empty_like(x) for _ in range(4))
+    rstd = torch.empty(m, dtype=torch.float32, device=x.device)
+    dgate, dscale, dshift = (torch.empty_like(gate) for _ in range(3))
+    dweight = torch.empty_like(w)
+    ws_bytes = L.nf_adaln_bwd_workspace(m, n, t)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=x.device)
+
+    def fwd():
+        _lib.check(L.nf_adaln_fwd(
+            x.data_ptr(), n, y.data_ptr(), n, gate.data_ptr(), n, w.data_ptr(), scale.data_ptr(),
+            n, shift.data_ptr(), n, h.data_ptr(), out.data_ptr(), rstd.data_ptr(), m, n, t, 1e-6,
+            dc(x), dc(y), dc(gate), dc(w), dc(scale), dc(shift), _lib.stream_of(x)), "fwd")
+
+    def bwd():
+        _lib.check(L.nf_adaln_bwd(
+            dh.data_ptr(), dout.data_ptr(), x.data_ptr(), n, y.data_ptr(), n, gate.data_ptr(), n,
+            w.data_ptr(), scale.data_ptr(), n, rstd.data_ptr(), dx.data_ptr(), dy.data_ptr(),
+            ws.data_ptr(), ws_bytes, m, n, t, dc(x), dc(y), dc(gate), dc(w), dc(scale),
+            _lib.stream_of(x)), "bwd")
+
+    def red():
+        _lib.check(L.nf_adaln_bwd_reduce(
+            ws.data_ptr(), ws_bytes, w.data_ptr(), scale.data_ptr(), n, dgate.data_ptr(),
+            dweight.data_ptr(), dscale.data_ptr(), dshift.data_ptr(), m, n, t, dc(gate), dc(w),
+            dc(scale), dc(shift), _lib.stream_of(x)), "reduce")
+
+    fwd()
+    bwd()
+    _sync()
+    assert b * t == m
+    return {"nf_adaln_fwd": per_launch_ms(fwd, steps), "nf_adaln_bwd": per_launch_ms(bwd, steps),
+            "nf_adaln_bwd_reduce": per_launch_ms(red, steps)}
+
+
+def bench_adaln(args, dev):
+    b, t, n = 8, 1024, 1024
+    m = b * t
+    inp, dh, dout = adaln_inputs(b, t, n, dev)
+    make = lambda: adaln_step_fn(inp, t, dh, dout)  # noqa: E731
+    eager_step = make()
+    eager_ms = time_eager(eager_step, args.steps, args.warmup)
+    ref = [x.clone() for x in eager_step()]
+    graph_ms, outs, graph = time_graph(make, args.steps, args.warmup, STEPS_PER_GRAPH)
+    graph_ok = same(ref, outs)
+    graph.replay()
+    _sync()
+    graph_ok = graph_ok and same(ref, outs)
+    del graph, outs
+    graph1_ms, _, _ = time_graph(make, args.steps, args.warmup, 1)
+
+    # per-kernel durations: back-to-back launches of each C-ABI entry point
+    kern_ms = adaln_kernel_ms(inp, t, dh, dout, args.steps)
+
+    alg = adaln_alg_bytes(b, t, n)
+    bwd_alg = (6 * m * n + 2 * b * n + n) * 2
+    fwd_alg = (4 * m * n + 3 * b * n + n) * 2
+    bwd_gbs = bwd_alg / (kern_ms["nf_adaln_bwd"] * 1e-3) / 1e9
+    fwd_gbs = fwd_alg / (kern_ms["nf_adaln_fwd"] * 1e-3) / 1e9
+    return {
+        "b": b, "t": t, "n": n, "alg_bytes": alg, "graph_ms": graph_ms, "eager_ms": eager_ms,
+        "graph1_ms": graph1_ms,
+        "graph_matches_eager": graph_ok, "kernel_ms": kern_ms,
+        "bwd_alg_bytes": bwd_alg, "bwd_gbs": bwd_gbs, "fwd_alg_bytes": fwd_alg, "fwd_gbs": fwd_gbs,
+        "gbs": alg / (graph_ms * 1e-3) / 1e9, "gbs_eager": alg / (eager_ms * 1e-3) / 1e9,
+        "ref_style_gbs_11MNe": 11 * m * n * 2 / (graph_ms * 1e-3) / 1e9,
+    }
+
+
+def bench_swiglu(args, dev, m=8192, h=4096):
+    import torch
+
+    from nuvla_forge_amd.kernels import fused_swiglu
+
+    g = torch.Generator().manual_seed(10)
+    a, b, dout = (torch.randn(m, h, generator=g).to(torch.bfloat16).to(dev) for _ in range(3))
+
+    def make():
+        la, lb = a.detach().requires_grad_(True), b.detach().requires_grad_(True)
+
+        def step():
+            out = fused_swiglu(la, lb)
+            return (out, *torch.autograd.grad(out, [la, lb], dout))
+
+        return step
+
+    eager_step = make()
+    eager_ms = time_eager(eager_step, args.steps, args.warmup)
+    ref = [x.clone() for x in eager_step()]
+    ms, outs, _ = time_graph(make, args.steps, args.warmup, STEPS_PER_GRAPH)
+    alg = 8 * m * h * 2
+    return {"m": m, "h": h, "alg_bytes": alg, "graph_ms": ms, "eager_ms": eager_ms,
+            "graph_matches_eager": same(ref, outs), "gbs": alg / (ms * 1e-3) / 1e9,
+            "hbm_frac": alg / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS}
+
+
+def ce_inputs(dev, m=4096, d=2048, v=32000, n_ignore=409):
+    import torch
+
+    g = torch.Generator().manual_seed(20)
+    hid = torch.randn(m, d, generator=g).to(torch.bfloat16).to(dev)
+    w = (torch.randn(v, d, generator=g) * 0.02).to(torch.bfloat16).to(dev)
+    tgt = torch.randint(0, v, (m,), generator=g)
+    tgt[torch.randperm(m, generator=g)[:n_ignore]] = -100
+    return hid, w, tgt.to(dev)
+
+
+def bench_ce(args, dev):
+    import torch
+
+    from nuvla_forge_amd.kernels import chunked_cross_entropy
+
+    m, d, v = 4096, 2048, 32000
+    hid, w, tgt = ce_inputs(dev, m, d, v)
+    m_valid = int((tgt != -100).sum())
+    chunk = 512  # rows of budget -> 4096-column vocabulary chunks at this M, V
+
+    def make():
+        lh, lw = hid.detach().requires_grad_(True), w.detach().requires_grad_(True)
+
+        def step():
+            loss = chunked_cross_entropy(lh, lw, tgt, chunk_size=chunk)
+            return (loss, *torch.autograd.grad(loss, [lh, lw]))
+
+        return step
+
+    steps = max(5, args.steps // 5)
+    eager_step = make()
+    eager_ms = time_eager(eager_step, steps, max(2, args.warmup // 5))
+    ref = [x.clone() for x in eager_step()]
+    ms, outs, _ = time_graph(make, steps, max(2, args.warmup // 5))
+    flops = 6 * m_valid * v * d
+    tflops = flops / (ms * 1e-3) / 1e12
+    return {"m": m, "d": d, "v": v, "m_valid": m_valid, "vocab_chunk": 4096,
+            "graph_ms": ms, "eager_ms": eager_ms, "graph_matches_eager": same(ref, outs),
+            "tokens_per_s": m / (ms * 1e-3), "alg_flops": flops, "tflops": tflops,
+            "mfma_frac": tflops / MFMA_BF16_PEAK_TFLOPS}
+
+
+def bench_stress(args, dev):
+    import torch
+
+    from nuvla_forge_amd.kernels import fused_swiglu
+
+    b, t, n = 32, 2048, 2048
+    sm, sh = 65536, 5632
+    inp, dh, dout = adaln_inputs(b, t, n, dev, seed=30)
+    g = torch.Generator().manual_seed(31)
+    a, bb, gout = (torch.randn(sm, sh, generator=g).to(torch.bfloat16).to(dev) for _ in range(3))
+
+    def make():
+        ad_step = adaln_step_fn(inp, t, dh, dout)
+        la, lb = a.detach().requires_grad_(True), bb.detach().requires_grad_(True)
+
+        def step():
+            r1 = ad_step()
+            out = fused_swiglu(la, lb)
+            return (*r1, out, *torch.autograd.grad(out, [la, lb], gout))
+
+        return step
+
+    steps = max(5, args.steps // 5)
+    ms, _, _ = time_graph(make, steps, max(2, args.warmup // 5))
+    alg = adaln_alg_bytes(b, t, n) + 8 * sm * sh * 2
+    return {"alg_bytes": alg, "graph_ms": ms, "gbs": alg / (ms * 1e-3) / 1e9,
+            "hbm_frac": alg / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS}
+
+
+# ---------------------------------------------------------------------------
+# CPU baselines (the reference's eager PyTorch path, oracle/torch_cpu.py)
+# ---------------------------------------------------------------------------
+def cpu_baselines(extra: bool):
+    import torch
+
+    from oracle import torch_cpu as tc
+
+    threads = cpu_threads()
+    torch.set_num_threads(threads)
+    out = {}
+    b, t, n = 8, 1024, 1024
+    inp, dh, dout = adaln_inputs(b, t, n, "cpu")
+    s = time_cpu(lambda: tc.adaln_fwd_bwd(**inp, t=t, dh_up=dh, dout=dout))
+    out["adaln"] = {"value": adaln_alg_bytes(b, t, n) / s / 1e9, "unit": "GB/s", "cores": threads,
+                    "kind": "port", "seconds_per_step": s,
+                    "sample": "full cfg2 workload (bf16 [8,1024,1024] fwd + autograd bwd), "
+                              "median of timed reps after 1 warmup"}
+    if extra:
+        g = torch.Generator().manual_seed(10)
+        m, h = 8192, 4096
+        a, bb, gd = (torch.randn(m, h, generator=g).to(torch.bfloat16) for _ in range(3))
+        s = time_cpu(lambda: tc.swiglu_fwd_bwd(a, bb, gd))
+        out["swiglu"] = {"value": 8 * m * h * 2 / s / 1e9, "unit": "GB/s", "cores": threads,
+                         "kind": "port", "seconds_per_step": s,
+                         "sample": "full cfg3 workload (bf16 [8192,4096])"}
+        hid, w, tgt = ce_inputs("cpu")
+        rows = 1024
+        s = time_cpu(lambda: tc.chunked_ce_fwd_bwd(hid[:rows], w, tgt[:rows], chunk_size=1024),
+                     max_reps=2)
+        out["ce"] = {"value": rows / s, "unit": "tokens/s", "cores": threads, "kind": "port",
+                     "seconds_per_step": s,
+                     "sample": "first 1024 of the 4096 cfg4 rows (one 1024-row chunk of the "
+                               "reference's CPU loop, fp32 GEMMs), tokens/s of that sample"}
+    out["torch"] = torch.__version__
+    try:
+        with open("/proc/cpuinfo") as f:
+            out["cpu_model"] = next(ln.split(":", 1)[1].strip() for ln in f
+                                    if ln.startswith("model name"))
+    except (OSError, StopIteration):
+        out["cpu_model"] = "unknown"
+    return out
+
+
+def main() -> int:
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU only (got --gpus {args.gpus}); the path "
+              "has no multi-GPU leg. Run with --gpus 1.", file=sys.stderr)
+        return 2
+    import torch
+
+    if not torch.cuda.is_available():
+        print("bench.py: no ROCm GPU visible", file=sys.stderr)
+        return 1
+    dev = torch.device("cuda", 0)
+    log(f"device: {torch.cuda.get_device_name(0)}  torch {torch.__version__}")
+
+    log("adaLN cfg2 ...")
+    ad = bench_adaln(args, dev)
+    log(f"  graph {ad['graph_ms'] * 1e3:.1f} us ({ad['gbs']:.0f} GB/s), eager "
+        f"{ad['eager_ms'] * 1e3:.1f} us; kernels {ad['kernel_ms']}")
+    extra = {}
+    if not args.no_extra:
+        log("SwiGLU cfg3 ...")
+        extra["swiglu_cfg3"] = bench_swiglu(args, dev)
+        log(f"  {extra['swiglu_cfg3']}")
+        log("chunked CE cfg4 ...")
+        extra["ce_cfg4"] = bench_ce(args, dev)
+        log(f"  {extra['ce_cfg4']}")
+        log("stress chain cfg5 ...")
+        extra["stress_cfg5"] = bench_stress(args, dev)
+        log(f"  {extra['stress_cfg5']}")
+
+    cpu = None
+    if not args.no_cpu:
+        log("CPU baselines ...")
+        cpu = cpu_baselines(not args.no_extra)
+        log(f"  {cpu}")
+        for k in ("swiglu", "ce"):
+            if k in cpu:
+                extra.setdefault("cpu_baselines", {})[k] = cpu[k]
+
+    bwd_ms = ad["kernel_ms"]["nf_adaln_bwd"]
+    record = {
+        "metric": "adaLN-RMSNorm fwd+bwd HBM GB/s & % of peak; chunked-CE tokens/s",
+        "value": round(ad["gbs"], 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ad["graph_ms"], 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) activations, N(0,0.1) conditioning)",
+        "config": {
+            "workload": "fused_adaln_residual_rmsnorm fwd+bwd bf16 B=8 T=1024 N=1024 "
+                        "(BASELINE configs[1]); forward + autograd backward through the "
+                        f"Function, {STEPS_PER_GRAPH} steps per HIP graph replay",
+            "alg_bytes_per_step": ad["alg_bytes"],
+            "hbm_frac_whole_step": round(ad["gbs"] / HBM_PEAK_GBS, 4),
+            "eager_ms_per_step": round(ad["eager_ms"], 5),
+            "graph1_ms_per_step": round(ad["graph1_ms"], 5),
+            "graph_matches_eager": ad["graph_matches_eager"],
+            "kernel_ms": {k: round(v, 5) for k, v in ad["kernel_ms"].items()},
+            "fwd_kernel_gbs": round(ad["fwd_gbs"], 1),
+            "ref_style_gbs_11MNe": round(ad["ref_style_gbs_11MNe"], 1),
+        },
+        "roofline": {
+            "kernel": "adaln_bwd_kernel (nf_adaln_bwd)",
+            "bound": "hbm",
+            "achieved": round(ad["bwd_gbs"], 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(ad["bwd_gbs"] / HBM_PEAK_GBS, 4),
+            "traffic": None,
+            "alg_bytes_per_launch": ad["bwd_alg_bytes"],
+            "mean_launch_ms": round(bwd_ms, 5),
+        },
+        "cpu_baseline": None if cpu is None else {
+            k: cpu["adaln"][k] for k in ("value", "unit", "cores", "kind", "sample")
+        } | {"cpu_model": cpu["cpu_model"], "torch": cpu["torch"]},
+        "extra": extra,
+    }
+    line = json.dumps(record)
+    if args.json_out:
+        with open(args.json_out, "w") as f:
+            f.write(line + "\n")
+    print(line, flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

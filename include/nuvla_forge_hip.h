@@ -84,34 +84,45 @@ int nf_adaln_fwd(const void *x, int64_t ld_x, const void *y, int64_t ld_y,
                  int dt_gate, int dt_weight, int dt_scale, int dt_shift,
                  void *stream);
 
-/* Bytes of fp32 workspace nf_adaln_bwd needs for this shape (per-block
- * partial rows of the M-axis reductions). */
+/* Bytes of fp32 workspace the backward pair below needs for this shape
+ * (per-block partial rows of the M-axis reductions). */
 size_t nf_adaln_bwd_workspace(int64_t M, int64_t N, int64_t T);
 
-/* adaLN seam backward.  h is recomputed in fp32 from x and y; rstd is the
- * forward's.  With dxhat = dout * weight * (1 + scale[b]) and
+/* adaLN seam backward, row part.  h is recomputed in fp32 from x and y;
+ * rstd is the forward's.  With dxhat = dout * weight * (1 + scale[b]) and
  * xhat = h * rstd:
- *   dh     = dh_up + rstd * (dxhat - xhat * mean(dxhat * xhat))
- *   dx     = dh                          (contiguous [M, N], dt_x)
- *   dy     = dh * gate[b]                (contiguous [M, N], dt_y)
- *   dgate  = sum_t dh * y                ([B, N], dt_gate)
- *   dscale = sum_t dout * xhat * weight  ([B, N], dt_scale)
- *   dshift = sum_t dout                  ([B, N], dt_shift)
- *   dweight= sum_m dout * xhat * (1 + scale[b])   ([N], dt_weight)
- * The M-axis sums are deterministic: per-block partials reduced in LDS, then
- * a fixed-order second pass; no atomics.
- * Replaces the `_adaln_rmsnorm_bwd` launch and the partial `.sum` reductions
- * in nuvla_forge/kernels/adaln_rmsnorm.py:97-162 and :194-236.
- * dh_up / dout are contiguous [M, N] of dt_x; either may be NULL (= zero).
- * dgate / dweight / dscale / dshift may each be NULL (not computed). */
+ *   dh = dh_up + rstd * (dxhat - xhat * mean(dxhat * xhat))
+ *   dx = dh                          (contiguous [M, N], dt_x)
+ *   dy = dh * gate[b]                (contiguous [M, N], dt_y)
+ * and, per block of rows of one sample, the partial column sums
+ *   sum dout * xhat,  sum dout,  sum dh * y
+ * written to `workspace` for nf_adaln_bwd_reduce.
+ * Replaces the `_adaln_rmsnorm_bwd` kernel and its launch,
+ * nuvla_forge/kernels/adaln_rmsnorm.py:97-162 and :207-229.
+ * dh_up / dout are contiguous [M, N] of dt_x; either may be NULL (= zero). */
 int nf_adaln_bwd(const void *dh_up, const void *dout, const void *x,
                  int64_t ld_x, const void *y, int64_t ld_y, const void *gate,
                  int64_t ld_gate, const void *weight, const void *scale,
                  int64_t ld_scale, const float *rstd, void *dx, void *dy,
-                 void *dgate, void *dweight, void *dscale, void *dshift,
-                 void *workspace, size_t workspace_bytes, int64_t M,
-                 int64_t N, int64_t T, int dt_x, int dt_y, int dt_gate,
-                 int dt_weight, int dt_scale, int dt_shift, void *stream);
+                 void *workspace, size_t workspace_bytes, int64_t M, int64_t N,
+                 int64_t T, int dt_x, int dt_y, int dt_gate, int dt_weight,
+                 int dt_scale, void *stream);
+
+/* adaLN seam backward, reductions over M of the partials nf_adaln_bwd left
+ * in `workspace` (same shape arguments), in a fixed order with no atomics:
+ *   dgate  = sum_t dh * y                ([B, N], dt_gate)
+ *   dscale = weight * sum_t dout * xhat  ([B, N], dt_scale)
+ *   dshift = sum_t dout                  ([B, N], dt_shift)
+ *   dweight= sum_b (1 + scale[b]) * sum_t dout * xhat   ([N], dt_weight)
+ * Replaces the partial `.sum` reductions and casts of
+ * nuvla_forge/kernels/adaln_rmsnorm.py:231-234.  Outputs may each be NULL
+ * (not computed).  Must follow nf_adaln_bwd on the same stream. */
+int nf_adaln_bwd_reduce(void *workspace, size_t workspace_bytes,
+                        const void *weight, const void *scale, int64_t ld_scale,
+                        void *dgate, void *dweight, void *dscale, void *dshift,
+                        int64_t M, int64_t N, int64_t T, int dt_gate,
+                        int dt_weight, int dt_scale, int dt_shift,
+                        void *stream);
 
 /* ------------------------------------------------------------------------
  * Chunked cross entropy with the gradient formed during the forward pass.

@@ -39,8 +39,12 @@ SIGNATURES = {
     "nf_adaln_bwd": (
         _I32,
         [_P, _P, _P, _I64, _P, _I64, _P, _I64, _P, _P, _I64, _P, _P, _P,
-         _P, _P, _P, _P, _P, _SZ, _I64, _I64, _I64,
-         _I32, _I32, _I32, _I32, _I32, _I32, _P],
+         _P, _SZ, _I64, _I64, _I64, _I32, _I32, _I32, _I32, _I32, _P],
+    ),
+    "nf_adaln_bwd_reduce": (
+        _I32,
+        [_P, _SZ, _P, _P, _I64, _P, _P, _P, _P, _I64, _I64, _I64,
+         _I32, _I32, _I32, _I32, _P],
     ),
     "nf_ce_workspace": (_SZ, [_I64, _I64, _I64, _I64, _I32]),
     "nf_ce_fwd_bwd": (

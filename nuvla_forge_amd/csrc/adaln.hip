@@ -19,7 +19,7 @@ NF_ADALN_EXTERN(float, f16)
 #undef NF_ADALN_EXTERN
 
 // ---------------------------------------------------------------------------
-// fixed-order reductions of the partial rows
+// fixed-order reduction of the partial rows
 // ---------------------------------------------------------------------------
 struct ReduceArgs {
   const float *partial;  // [B * J, 3, N]
@@ -28,67 +28,95 @@ struct ReduceArgs {
   void *dgate;
   void *dscale;
   void *dshift;
-  float *q;  // [B, N]: (1 + scale_b) * A_b, for dweight
+  void *dweight;
   int64_t ld_scale;
   int N, J, B;
   int dt_weight, dt_scale, dt_gate, dt_shift;
 };
 
-constexpr int kRedCols = 64;
-constexpr int kRedSplit = 4;
+constexpr int kRcCols = 8;                     // columns per block
+constexpr int kRcThreads = 1024;
+constexpr int kRcQ = kRcThreads / kRcCols;     // threads per column (128)
+constexpr int kRcSlots = 1024;                 // partial rows staged per round
 
-// grid (ceil(N / 64), B); thread (c, s) sums partial rows j = s, s+4, ...
-__global__ __launch_bounds__(kRedCols *kRedSplit) void adaln_reduce_samples(
-    ReduceArgs p) {
-  __shared__ float part[3][kRedSplit][kRedCols];
-  const int c = threadIdx.x % kRedCols;
-  const int s = threadIdx.x / kRedCols;
-  const int col = blockIdx.x * kRedCols + c;
-  const int64_t b = blockIdx.y;
-  float a0 = 0.f, a1 = 0.f, a2 = 0.f;
-  if (col < p.N) {
-    for (int j = s; j < p.J; j += kRedSplit) {
-      const float *src = p.partial + ((b * p.J + j) * 3) * (int64_t)p.N + col;
-      a0 += src[0];
-      a1 += src[p.N];
-      a2 += src[2 * (int64_t)p.N];
+// One block per 8-column slice.  A round stages the partial rows of up to
+// 128 whole samples (<= 1024 rows) in LDS with one wave of loads (24 per
+// thread at most); S = 128 / samples threads per (sample, column) each sum
+// every S-th of the sample's J rows, one thread per (sample, column) adds the
+// S results, and one thread per column folds the samples into dweight.  All
+// orders are fixed, so the sums are bit-reproducible.
+__global__ __launch_bounds__(kRcThreads) void adaln_reduce_kernel(ReduceArgs p) {
+  __shared__ float buf[3][kRcSlots][kRcCols];
+  __shared__ float part[3][kRcQ][kRcCols];
+  __shared__ float qbuf[kRcQ][kRcCols];
+  const int c = threadIdx.x % kRcCols;
+  const int q = threadIdx.x / kRcCols;
+  const int col = blockIdx.x * kRcCols + c;
+  const bool cv = col < p.N;
+  const int64_t N = p.N;
+  int per_round = kRcSlots / p.J;  // J <= 1024 by construction of the plan
+  if (per_round > kRcQ) per_round = kRcQ;
+  if (per_round < 1) per_round = 1;
+  float dw = 0.f;
+  for (int b0 = 0; b0 < p.B; b0 += per_round) {
+    const int nb = p.B - b0 < per_round ? p.B - b0 : per_round;
+    const int nslots = nb * p.J;
+    const int64_t slot0 = (int64_t)b0 * p.J;
+    for (int s = q; s < nslots; s += kRcQ) {
+      const float *src = p.partial + (slot0 + s) * 3 * N + col;
+      buf[0][s][c] = cv ? src[0] : 0.f;
+      buf[1][s][c] = cv ? src[N] : 0.f;
+      buf[2][s][c] = cv ? src[2 * N] : 0.f;
     }
-  }
-  part[0][s][c] = a0;
-  part[1][s][c] = a1;
-  part[2][s][c] = a2;
-  __syncthreads();
-  if (s == 0 && col < p.N) {
-    float A = 0.f, Sh = 0.f, G = 0.f;
-#pragma unroll
-    for (int i = 0; i < kRedSplit; ++i) {
-      A += part[0][i][c];
-      Sh += part[1][i][c];
-      G += part[2][i][c];
-    }
-    const int64_t o = b * p.N + col;
-    if (p.dgate) store_dyn(p.dgate, p.dt_gate, o, G);
-    if (p.dshift) store_dyn(p.dshift, p.dt_shift, o, Sh);
-    if (p.dscale || p.q) {
-      float w[8], sc[8];
-      load8_dyn<false>(p.weight, p.dt_weight, col, 1, w);
-      if (p.dscale) store_dyn(p.dscale, p.dt_scale, o, w[0] * A);
-      if (p.q) {
-        load8_dyn<false>(p.scale, p.dt_scale, b * p.ld_scale + col, 1, sc);
-        p.q[o] = (1.f + sc[0]) * A;
+    __syncthreads();
+    const int S = kRcQ / nb;  // splits per sample, >= 1
+    {
+      const int sb = q / S, sp = q % S;
+      float A = 0.f, Sh = 0.f, G = 0.f;
+      if (sb < nb) {
+        for (int jj = sp; jj < p.J; jj += S) {
+          A += buf[0][sb * p.J + jj][c];
+          Sh += buf[1][sb * p.J + jj][c];
+          G += buf[2][sb * p.J + jj][c];
+        }
       }
+      part[0][q][c] = A;
+      part[1][q][c] = Sh;
+      part[2][q][c] = G;
     }
+    __syncthreads();
+    if (q < nb) {
+      float A = 0.f, Sh = 0.f, G = 0.f;
+      for (int sp = 0; sp < S; ++sp) {
+        A += part[0][q * S + sp][c];
+        Sh += part[1][q * S + sp][c];
+        G += part[2][q * S + sp][c];
+      }
+      float qv = 0.f;
+      if (cv) {
+        const int64_t b = b0 + q;
+        const int64_t o = b * N + col;
+        if (p.dgate) store_dyn(p.dgate, p.dt_gate, o, G);
+        if (p.dshift) store_dyn(p.dshift, p.dt_shift, o, Sh);
+        if (p.dscale) {
+          float w[8];
+          load8_dyn<false>(p.weight, p.dt_weight, col, 1, w);
+          store_dyn(p.dscale, p.dt_scale, o, w[0] * A);
+        }
+        if (p.dweight) {
+          float sc[8];
+          load8_dyn<false>(p.scale, p.dt_scale, b * p.ld_scale + col, 1, sc);
+          qv = (1.f + sc[0]) * A;
+        }
+      }
+      qbuf[q][c] = qv;
+    }
+    __syncthreads();
+    if (q == 0)
+      for (int sb = 0; sb < nb; ++sb) dw += qbuf[sb][c];
+    __syncthreads();
   }
-}
-
-// dweight[n] = sum_b q[b, n], b ascending
-__global__ __launch_bounds__(256) void adaln_reduce_weight(
-    const float *__restrict__ q, void *dweight, int dt_weight, int N, int B) {
-  const int col = blockIdx.x * 256 + threadIdx.x;
-  if (col >= N) return;
-  float acc = 0.f;
-  for (int b = 0; b < B; ++b) acc += q[(int64_t)b * N + col];
-  store_dyn(dweight, dt_weight, col, acc);
+  if (q == 0 && cv && p.dweight) store_dyn(p.dweight, p.dt_weight, col, dw);
 }
 
 }  // namespace adaln
@@ -118,10 +146,10 @@ extern "C" int nf_adaln_fwd(const void *x, int64_t ld_x, const void *y,
                    aligned16(x) && aligned16(y) && aligned16(gate) &&
                    aligned16(weight) && aligned16(scale) && aligned16(shift) &&
                    aligned16(h) && aligned16(out);
-  FwdArgs a{x, y, gate, weight, scale, shift, h, out, rstd,
-            ld_x, ld_y, ld_gate, ld_scale, ld_shift, M, T, (int)N, eps,
-            dt_gate, dt_weight, dt_scale, dt_shift};
   const Plan pl = make_plan(M, N, T);
+  FwdArgs a{x, y, gate, weight, scale, shift, h, out, rstd,
+            ld_x, ld_y, ld_gate, ld_scale, ld_shift, M, T, (int)N, pl.fwd_rpg, eps,
+            dt_gate, dt_weight, dt_scale, dt_shift};
   hipStream_t s = static_cast<hipStream_t>(stream);
   return dispatch_xy(dt_x, dt_y, "nf_adaln_fwd", [&](auto tx, auto ty) {
     return fwd_v<decltype(tx), decltype(ty)>(a, pl, vec, s);
@@ -138,20 +166,17 @@ extern "C" int nf_adaln_bwd(const void *dh_up, const void *dout, const void *x,
                             const void *gate, int64_t ld_gate,
                             const void *weight, const void *scale,
                             int64_t ld_scale, const float *rstd, void *dx,
-                            void *dy, void *dgate, void *dweight, void *dscale,
-                            void *dshift, void *workspace,
+                            void *dy, void *workspace,
                             size_t workspace_bytes_given, int64_t M, int64_t N,
                             int64_t T, int dt_x, int dt_y, int dt_gate,
-                            int dt_weight, int dt_scale, int dt_shift,
-                            void *stream) {
+                            int dt_weight, int dt_scale, void *stream) {
   if (int e = check_shape("nf_adaln_bwd", M, N, T)) return e;
   if (M == 0) return NF_OK;
   if (!x || !y || !gate || !weight || !scale || !rstd || !dx || !dy)
     return set_error(NF_ERR_ARG, "nf_adaln_bwd: null pointer");
   if (ld_x < N || ld_y < N || ld_gate < 0 || ld_scale < 0)
     return set_error(NF_ERR_ARG, "nf_adaln_bwd: bad row stride");
-  if (!is_dtype(dt_gate) || !is_dtype(dt_weight) || !is_dtype(dt_scale) ||
-      !is_dtype(dt_shift))
+  if (!is_dtype(dt_gate) || !is_dtype(dt_weight) || !is_dtype(dt_scale))
     return set_error(NF_ERR_DTYPE, "nf_adaln_bwd: bad conditioning dtype");
   const Plan pl = make_plan(M, N, T);
   const size_t need = workspace_bytes(pl, N);
@@ -165,27 +190,44 @@ extern "C" int nf_adaln_bwd(const void *dh_up, const void *dout, const void *x,
                    aligned16(scale) && aligned16(dx) && aligned16(dy) &&
                    aligned16(workspace) && (!dh_up || aligned16(dh_up)) &&
                    (!dout || aligned16(dout));
-  float *partial = static_cast<float *>(workspace);
-  float *q = partial + pl.B * pl.J * 3 * N;
-  BwdArgs a{dh_up, dout, x, y, gate, weight, scale, rstd, dx, dy, partial,
-            ld_x, ld_y, ld_gate, ld_scale, M, T, (int)N, pl.J,
-            pl.rows_per_block, dt_gate, dt_weight, dt_scale};
+  BwdArgs a{dh_up, dout, x, y, gate, weight, scale, rstd, dx, dy,
+            static_cast<float *>(workspace), ld_x, ld_y, ld_gate, ld_scale,
+            M, T, (int)N, pl.J, pl.rows_per_block, dt_gate, dt_weight, dt_scale};
   hipStream_t s = static_cast<hipStream_t>(stream);
-  int e = dispatch_xy(dt_x, dt_y, "nf_adaln_bwd", [&](auto tx, auto ty) {
+  return dispatch_xy(dt_x, dt_y, "nf_adaln_bwd", [&](auto tx, auto ty) {
     return bwd_v<decltype(tx), decltype(ty)>(a, pl, vec, s);
   });
-  if (e) return e;
+}
+
+extern "C" int nf_adaln_bwd_reduce(void *workspace,
+                                   size_t workspace_bytes_given,
+                                   const void *weight, const void *scale,
+                                   int64_t ld_scale, void *dgate, void *dweight,
+                                   void *dscale, void *dshift, int64_t M,
+                                   int64_t N, int64_t T, int dt_gate,
+                                   int dt_weight, int dt_scale, int dt_shift,
+                                   void *stream) {
+  if (int e = check_shape("nf_adaln_bwd_reduce", M, N, T)) return e;
   if (!dgate && !dscale && !dshift && !dweight) return NF_OK;
-  ReduceArgs r{partial, weight, scale, dgate, dscale, dshift,
-               dweight ? q : nullptr, ld_scale, (int)N, pl.J, (int)pl.B,
-               dt_weight, dt_scale, dt_gate, dt_shift};
-  dim3 g1((unsigned)((N + kRedCols - 1) / kRedCols), (unsigned)pl.B);
-  adaln_reduce_samples<<<g1, kRedCols * kRedSplit, 0, s>>>(r);
-  if ((e = check_launch("nf_adaln_bwd(reduce_samples)"))) return e;
-  if (dweight) {
-    adaln_reduce_weight<<<(unsigned)((N + 255) / 256), 256, 0, s>>>(
-        q, dweight, dt_weight, (int)N, (int)pl.B);
-    if ((e = check_launch("nf_adaln_bwd(reduce_weight)"))) return e;
+  if (!weight || !scale)
+    return set_error(NF_ERR_ARG, "nf_adaln_bwd_reduce: null pointer");
+  if (ld_scale < 0) return set_error(NF_ERR_ARG, "nf_adaln_bwd_reduce: bad row stride");
+  if (!is_dtype(dt_gate) || !is_dtype(dt_weight) || !is_dtype(dt_scale) ||
+      !is_dtype(dt_shift))
+    return set_error(NF_ERR_DTYPE, "nf_adaln_bwd_reduce: bad dtype");
+  const Plan pl = make_plan(M, N, T);
+  if (M > 0) {
+    const size_t need = workspace_bytes(pl, N);
+    if (!workspace || workspace_bytes_given < need)
+      return set_error(NF_ERR_WORKSPACE,
+                       "nf_adaln_bwd_reduce: workspace %zu bytes < required %zu",
+                       workspace_bytes_given, need);
   }
-  return NF_OK;
+  // M == 0: no sample, every sum is empty; the kernel writes dweight = 0
+  ReduceArgs r{static_cast<const float *>(workspace), weight, scale, dgate, dscale, dshift,
+               dweight, ld_scale, (int)N, M > 0 ? pl.J : 1, M > 0 ? (int)pl.B : 0,
+               dt_weight, dt_scale, dt_gate, dt_shift};
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  adaln_reduce_kernel<<<(unsigned)((N + kRcCols - 1) / kRcCols), kRcThreads, 0, s>>>(r);
+  return check_launch("nf_adaln_bwd_reduce");
 }

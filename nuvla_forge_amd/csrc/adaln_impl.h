@@ -11,21 +11,27 @@
 // WPR == 1 the row's sum of squares is a pure DPP wavefront reduction; with
 // WPR > 1 the per-wave sums meet in LDS.
 //
-// Backward.  Block (b, j) owns a contiguous run of rows of sample b.  Each
-// thread accumulates three per-column partials over its rows:
-//   A  = sum dout * xhat,  S = sum dout,  G = sum dh * y
-// (dscale = weight * A, dshift = S, dgate = G, dweight = sum_b (1+scale_b) A_b),
-// the row groups of the block combine them in LDS in a fixed order, and the
-// block writes one [3, N] fp32 partial row.  adaln_reduce_samples then sums
-// each sample's J partial rows in a fixed order and adaln_reduce_weight sums
-// samples in order: no atomics, bit-identical from run to run.
+// Forward.  Each row group walks a contiguous run of rows, issuing the loads
+// of row r+1 before working on row r (two rows of x, y in flight per
+// wavefront) and keeping the per-sample conditioning in registers while the
+// sample does not change.
+//
+// Backward.  Block (b, j) owns a contiguous run of rows of sample b; its G row
+// groups take every G-th row, again with the next row's four inputs loaded
+// before the current row is processed.  Each thread accumulates three
+// per-column partials over its rows:
+//   A = sum dout * xhat,  S = sum dout,  G = sum dh * y
+// (dscale = weight * A, dshift = S, dgate = G, dweight = sum_b (1+scale_b) A_b);
+// the row groups combine them in LDS in a fixed order and the block writes
+// one [3, N] fp32 partial row.  adaln_reduce_kernel (adaln.hip) then sums the
+// partial rows in a fixed order: no atomics, bit-identical run to run.
 #pragma once
 #include "nf_device.h"
 
 namespace nf {
 namespace adaln {
 
-constexpr int kMaxN = 16384;  // 64 lanes * 8 waves * 8 elems * 4 chunks
+constexpr int kMaxN = 16384;  // 64 lanes * 16 waves * 8 elems * 2 chunks
 
 struct FwdArgs {
   const void *x;
@@ -40,6 +46,7 @@ struct FwdArgs {
   int64_t ld_x, ld_y, ld_gate, ld_scale, ld_shift;
   int64_t M, T;
   int N;
+  int rows_per_group;  // contiguous rows walked by one row group
   float eps;
   int dt_gate, dt_weight, dt_scale, dt_shift;
 };
@@ -103,65 +110,104 @@ __device__ __forceinline__ float row_sum(float v, float *red, int g, int rt) {
 // ---------------------------------------------------------------------------
 // forward
 // ---------------------------------------------------------------------------
-template <typename TX, typename TY, int K, int WPR, bool VEC>
+template <typename TX, typename TY, int K, int WPR, bool VEC, bool NT>
 __global__ __launch_bounds__(FwdShape<WPR>::BLK) void adaln_fwd_kernel(
     FwdArgs p) {
   using S = FwdShape<WPR>;
   __shared__ float red[S::G * WPR];
   const int g = threadIdx.x / S::R;
   const int rt = threadIdx.x % S::R;
-  const int64_t row = (int64_t)blockIdx.x * S::G + g;
-  const bool active = row < p.M;
-  const int64_t b = active ? row / p.T : 0;
+  const int64_t first = ((int64_t)blockIdx.x * S::G + g) * p.rows_per_group;
+  const int64_t last = first + p.rows_per_group < p.M ? first + p.rows_per_group : p.M;
+  const TX *const xp = static_cast<const TX *>(p.x);
+  const TY *const yp = static_cast<const TY *>(p.y);
 
-  const TX *xr = static_cast<const TX *>(p.x) + row * p.ld_x;
-  const TY *yr = static_cast<const TY *>(p.y) + row * p.ld_y;
-
-  float hv[K][8];
-  float ss = 0.f;
+  float wv[K][8];
 #pragma unroll
   for (int k = 0; k < K; ++k) {
     const int col = (k * S::R + rt) * 8;
-    const int valid = active ? chunk_valid(p.N, col) : 0;
-    float xv[8], yv[8], gv[8];
-    if (valid > 0) {
-      load8<TX, VEC>(xr + col, valid, xv);
-      load8<TY, VEC>(yr + col, valid, yv);
-      load8_dyn<VEC>(p.gate, p.dt_gate, b * p.ld_gate + col, valid, gv);
-    } else {
-#pragma unroll
-      for (int i = 0; i < 8; ++i) xv[i] = yv[i] = gv[i] = 0.f;
-    }
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      hv[k][i] = xv[i] + gv[i] * yv[i];
-      ss += hv[k][i] * hv[k][i];
-    }
-    if (valid > 0)
-      store8<TX, VEC>(static_cast<TX *>(p.h) + row * (int64_t)p.N + col,
-                      valid, hv[k]);
+    const int valid = chunk_valid(p.N, col);
+    if (valid > 0) load8_dyn<VEC>(p.weight, p.dt_weight, col, valid, wv[k]);
   }
 
-  ss = row_sum<WPR>(ss, red, g, rt);
-  const float rstd = 1.f / __builtin_sqrtf(ss / (float)p.N + p.eps);
-  if (active && rt == 0) p.rstd[row] = rstd;
-
+  Raw8<TX> xc[K], xn[K];
+  Raw8<TY> yc[K], yn[K];
+  auto load_row = [&](int64_t row, Raw8<TX>(&xa)[K], Raw8<TY>(&ya)[K]) {
 #pragma unroll
-  for (int k = 0; k < K; ++k) {
-    const int col = (k * S::R + rt) * 8;
-    const int valid = active ? chunk_valid(p.N, col) : 0;
-    if (valid > 0) {
-      float wv[8], sv[8], shv[8], o[8];
-      load8_dyn<VEC>(p.weight, p.dt_weight, col, valid, wv);
-      load8_dyn<VEC>(p.scale, p.dt_scale, b * p.ld_scale + col, valid, sv);
-      load8_dyn<VEC>(p.shift, p.dt_shift, b * p.ld_shift + col, valid, shv);
+    for (int k = 0; k < K; ++k) {
+      const int col = (k * S::R + rt) * 8;
+      const int valid = chunk_valid(p.N, col);
+      if (valid > 0) {
+        xa[k].template load<VEC>(xp + row * p.ld_x + col, valid);
+        ya[k].template load<VEC>(yp + row * p.ld_y + col, valid);
+      } else {
+        xa[k].zero();
+        ya[k].zero();
+      }
+    }
+  };
+  if (first < last) load_row(first, xc, yc);
+
+  float gv[K][8], wo[K][8], shv[K][8];
+  int64_t cur_b = -1;
+  for (int r = 0; r < p.rows_per_group; ++r) {
+    const int64_t row = first + r;
+    const bool active = row < last;
+    if (row + 1 < last) load_row(row + 1, xn, yn);
+    if (active) {
+      const int64_t b = row / p.T;
+      if (b != cur_b) {  // uniform across the row group
+        cur_b = b;
+#pragma unroll
+        for (int k = 0; k < K; ++k) {
+          const int col = (k * S::R + rt) * 8;
+          const int valid = chunk_valid(p.N, col);
+          float sv[8];
+          if (valid > 0) {
+            load8_dyn<VEC>(p.gate, p.dt_gate, b * p.ld_gate + col, valid, gv[k]);
+            load8_dyn<VEC>(p.scale, p.dt_scale, b * p.ld_scale + col, valid, sv);
+            load8_dyn<VEC>(p.shift, p.dt_shift, b * p.ld_shift + col, valid, shv[k]);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) wo[k][i] = wv[k][i] * (1.f + sv[i]);
+          }
+        }
+      }
+    }
+
+    float hv[K][8];
+    float ss = 0.f;
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+      const int col = (k * S::R + rt) * 8;
+      const int valid = active ? chunk_valid(p.N, col) : 0;
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
-        const float xhat = hv[k][i] * rstd;
-        o[i] = xhat * wv[i] * (1.f + sv[i]) + shv[i];
+        hv[k][i] = valid > 0 ? xc[k][i] + gv[k][i] * yc[k][i] : 0.f;
+        ss += hv[k][i] * hv[k][i];
       }
-      store8<TX, VEC>(static_cast<TX *>(p.out) + row * (int64_t)p.N + col,
-                      valid, o);
+      if (valid > 0)
+        store8_hint<TX, VEC, NT>(static_cast<TX *>(p.h) + row * (int64_t)p.N + col, valid,
+                                 hv[k]);
+    }
+    ss = row_sum<WPR>(ss, red, g, rt);
+    const float rstd = 1.f / __builtin_sqrtf(ss / (float)p.N + p.eps);
+    if (active && rt == 0) p.rstd[row] = rstd;
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+      const int col = (k * S::R + rt) * 8;
+      const int valid = active ? chunk_valid(p.N, col) : 0;
+      if (valid > 0) {
+        float o[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) o[i] = (hv[k][i] * rstd) * wo[k][i] + shv[k][i];
+        store8_hint<TX, VEC, NT>(static_cast<TX *>(p.out) + row * (int64_t)p.N + col, valid,
+                                 o);
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+      xc[k] = xn[k];
+      yc[k] = yn[k];
     }
   }
 }
@@ -206,7 +252,14 @@ __device__ __forceinline__ void combine_store(float (&acc)[K][8], float *comb,
     }
   }
 }
-template <typename TX, typename TY, int K, int WPR, bool VEC>
+
+template <typename TX, typename TY, int K>
+struct BwdRow {
+  Raw8<TX> x[K], dout[K], dh[K];
+  Raw8<TY> y[K];
+};
+
+template <typename TX, typename TY, int K, int WPR, bool VEC, bool NT, bool PF>
 __global__ __launch_bounds__(BwdShape<WPR>::BLK) void adaln_bwd_kernel(
     BwdArgs p) {
   using S = BwdShape<WPR>;
@@ -253,31 +306,39 @@ __global__ __launch_bounds__(BwdShape<WPR>::BLK) void adaln_bwd_kernel(
   const TX *const dop = static_cast<const TX *>(p.dout);
   const TX *const dhp = static_cast<const TX *>(p.dh_up);
 
+  auto load_row = [&](int64_t t, BwdRow<TX, TY, K> &rw) {
+    const int64_t row = b * p.T + t;
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+      const int col = (k * S::R + rt) * 8;
+      const int valid = t < t1 ? chunk_valid(p.N, col) : 0;
+      if (valid > 0) {
+        rw.x[k].template load<VEC>(xp + row * p.ld_x + col, valid);
+        rw.y[k].template load<VEC>(yp + row * p.ld_y + col, valid);
+        if (dop) rw.dout[k].template load<VEC>(dop + row * (int64_t)p.N + col, valid);
+        else rw.dout[k].zero();
+        if (dhp) rw.dh[k].template load<VEC>(dhp + row * (int64_t)p.N + col, valid);
+        else rw.dh[k].zero();
+      } else {
+        rw.x[k].zero(); rw.y[k].zero(); rw.dout[k].zero(); rw.dh[k].zero();
+      }
+    }
+  };
+
   const int64_t nrows = t1 > t0 ? t1 - t0 : 0;
   const int64_t iters = (nrows + S::G - 1) / S::G;
+  BwdRow<TX, TY, K> cur, nxt;
+  if (PF && iters > 0) load_row(t0 + g, cur);
   for (int64_t it = 0; it < iters; ++it) {
     const int64_t t = t0 + it * S::G + g;
     const bool active = t < t1;
     const int64_t row = b * p.T + t;
-    const float rstd = active ? p.rstd[row] : 0.f;
-
-    Raw8<TX> xr[K], dor[K], dhr[K];
-    Raw8<TY> yr[K];
-#pragma unroll
-    for (int k = 0; k < K; ++k) {
-      const int col = (k * S::R + rt) * 8;
-      const int valid = active ? chunk_valid(p.N, col) : 0;
-      if (valid > 0) {
-        xr[k].template load<VEC>(xp + row * p.ld_x + col, valid);
-        yr[k].template load<VEC>(yp + row * p.ld_y + col, valid);
-        if (dop) dor[k].template load<VEC>(dop + row * (int64_t)p.N + col, valid);
-        else dor[k].zero();
-        if (dhp) dhr[k].template load<VEC>(dhp + row * (int64_t)p.N + col, valid);
-        else dhr[k].zero();
-      } else {
-        xr[k].zero(); yr[k].zero(); dor[k].zero(); dhr[k].zero();
-      }
+    if constexpr (PF) {
+      if (it + 1 < iters) load_row(t + S::G, nxt);
+    } else {
+      load_row(t, cur);
     }
+    const float rstd = active ? p.rstd[row] : 0.f;
 
     // xhat = (x + gate * y) * rstd (h recomputed in fp32, never re-read)
     float xh[K][8];
@@ -286,8 +347,8 @@ __global__ __launch_bounds__(BwdShape<WPR>::BLK) void adaln_bwd_kernel(
     for (int k = 0; k < K; ++k)
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
-        xh[k][i] = (xr[k][i] + gv[k][i] * yr[k][i]) * rstd;
-        dot += (dor[k][i] * wo[k][i]) * xh[k][i];
+        xh[k][i] = (cur.x[k][i] + gv[k][i] * cur.y[k][i]) * rstd;
+        dot += (cur.dout[k][i] * wo[k][i]) * xh[k][i];
       }
     dot = row_sum<WPR>(dot, red, g, rt);
     const float c = dot / (float)p.N;
@@ -300,17 +361,18 @@ __global__ __launch_bounds__(BwdShape<WPR>::BLK) void adaln_bwd_kernel(
         float dh[8], dyv[8];
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-          const float d = dor[k][i];
-          dh[i] = dhr[k][i] + rstd * (d * wo[k][i] - xh[k][i] * c);
+          const float d = cur.dout[k][i];
+          dh[i] = cur.dh[k][i] + rstd * (d * wo[k][i] - xh[k][i] * c);
           dyv[i] = dh[i] * gv[k][i];
           accA[k][i] += d * xh[k][i];
           accS[k][i] += d;
-          accG[k][i] += dh[i] * yr[k][i];
+          accG[k][i] += dh[i] * cur.y[k][i];
         }
-        store8<TX, VEC>(static_cast<TX *>(p.dx) + row * (int64_t)p.N + col, valid, dh);
-        store8<TY, VEC>(static_cast<TY *>(p.dy) + row * (int64_t)p.N + col, valid, dyv);
+        store8_hint<TX, VEC, NT>(static_cast<TX *>(p.dx) + row * (int64_t)p.N + col, valid, dh);
+        store8_hint<TY, VEC, NT>(static_cast<TY *>(p.dy) + row * (int64_t)p.N + col, valid, dyv);
       }
     }
+    if constexpr (PF) cur = nxt;
   }
 
   // combine the G row groups in a fixed order (group 0 + 1 + ... + G-1) and
@@ -325,8 +387,9 @@ __global__ __launch_bounds__(BwdShape<WPR>::BLK) void adaln_bwd_kernel(
 // planning
 // ---------------------------------------------------------------------------
 struct Plan {
-  int fwd_wpr;  // forward: wavefronts per row (1, 2, 4, 8)
-  int fwd_k;    // forward: 8-element chunks per thread (1, 2, 4)
+  int fwd_wpr;  // forward: wavefronts per row (1, 2, 4, 8, 16)
+  int fwd_k;    // forward: 8-element chunks per thread (1, 2)
+  int fwd_rpg;  // forward: contiguous rows per row group
   int bwd_wpr;  // backward: wavefronts per row (1, 2, 4, 8, 16)
   int bwd_k;    // backward: 8-element chunks per thread (1, 2)
   int J;        // backward blocks per sample
@@ -334,10 +397,20 @@ struct Plan {
   int64_t B;
 };
 
-// Target number of backward blocks: one 512-thread block per CU on the
-// 256-CU MI355X (8 wavefronts per CU), so each block covers many rows and the
-// partial-row traffic stays a few percent of the tensor traffic.
-constexpr int kBwdBlocksTarget = 256;
+// Launch shapes for the 256-CU MI355X, from sweeps at the BASELINE shapes
+// (bf16 [8,1024,1024] and [32,2048,2048]).  More wavefronts in flight beat
+// deeper per-thread buffering for these streaming kernels, so rows of
+// N >= 1024 are split over >= 2 wavefronts in the forward and the backward
+// keeps one 8-element chunk per thread (up to 16 wavefronts per row).
+// Forward: each row group walks clamp(M / 2048, 1, 8) consecutive rows.
+// Backward: ~512 blocks of 512 threads (2 per CU), each a run of one
+// sample's rows, so the partial rows stay a few percent of the traffic.
+constexpr int kBwdBlocksTarget = 512;
+// adaln_reduce_kernel stages at most 1024 partial rows of whole samples per
+// round, so one sample may contribute at most 1024 of them.
+constexpr int kMaxBlocksPerSample = 1024;
+constexpr int kFwdGroupsTarget = 2048;
+constexpr int kFwdMaxRowsPerGroup = 8;
 
 inline int pick_wpr(int64_t N, int max_k) {
   int wpr = 1;
@@ -350,20 +423,27 @@ inline int pick_k(int64_t N, int wpr) {
   return k <= 1 ? 1 : (k <= 2 ? 2 : 4);
 }
 
-inline Plan make_plan(int64_t M, int64_t N, int64_t T) {
+inline Plan make_plan(int64_t M, int64_t N, int64_t T, int fwd_groups = kFwdGroupsTarget,
+                      int bwd_blocks = kBwdBlocksTarget) {
   Plan pl{};
-  // forward holds up to 4 chunks per thread (no LDS sync up to N = 2048);
-  // backward holds up to 2 (its per-column accumulators live in registers)
-  pl.fwd_wpr = pick_wpr(N, 4);
+  pl.fwd_wpr = pick_wpr(N, 2);
+  if (N >= 1024 && pl.fwd_wpr < 2) pl.fwd_wpr = 2;
   pl.fwd_k = pick_k(N, pl.fwd_wpr);
-  pl.bwd_wpr = pick_wpr(N, 2);
+  {
+    int64_t rpg = M / fwd_groups;
+    if (rpg > kFwdMaxRowsPerGroup) rpg = kFwdMaxRowsPerGroup;
+    pl.fwd_rpg = (int)(rpg < 1 ? 1 : rpg);
+  }
+  pl.bwd_wpr = pick_wpr(N, 1);
+  if (pl.bwd_wpr > 16) pl.bwd_wpr = 16;
   pl.bwd_k = pick_k(N, pl.bwd_wpr);
   pl.B = M / T;
   const int R = 64 * pl.bwd_wpr;
   const int G = (R < 512 ? 512 : R) / R;
-  int64_t J = (kBwdBlocksTarget + pl.B - 1) / pl.B;
+  int64_t J = pl.B > 0 ? (bwd_blocks + pl.B - 1) / pl.B : 1;
   const int64_t jmax = (T + 2 * G - 1) / (2 * G);  // >= 2 rows per row group
   if (J > jmax) J = jmax;
+  if (J > kMaxBlocksPerSample) J = kMaxBlocksPerSample;
   if (J < 1) J = 1;
   pl.rows_per_block = (int)((T + J - 1) / J);
   pl.J = (int)((T + pl.rows_per_block - 1) / pl.rows_per_block);
@@ -371,37 +451,46 @@ inline Plan make_plan(int64_t M, int64_t N, int64_t T) {
 }
 
 inline size_t workspace_bytes(const Plan &pl, int64_t N) {
-  return (size_t)(pl.B * pl.J * 3 * N + pl.B * N) * sizeof(float);
+  return (size_t)(pl.B * pl.J * 3 * N) * sizeof(float);
+}
+
+inline unsigned fwd_grid(const Plan &pl, int64_t M) {
+  // must match FwdShape<pl.fwd_wpr>
+  const int R = 64 * pl.fwd_wpr;
+  const int G = (R < 256 ? 256 : R) / R;
+  const int64_t per_block = (int64_t)G * pl.fwd_rpg;
+  return (unsigned)((M + per_block - 1) / per_block);
 }
 
 // ---------------------------------------------------------------------------
-// dispatch over (TX, TY) x K x WPR x VEC
+// dispatch over (TX, TY) x K x WPR x VEC (stores: non-temporal; backward:
+// next-row prefetch)
 // ---------------------------------------------------------------------------
+constexpr bool kFwdNT = true;
+constexpr bool kBwdNT = true;
+
 template <typename TX, typename TY, bool VEC, int WPR, int K>
-int launch_fwd_t(const FwdArgs &a, hipStream_t s) {
+int launch_fwd_t(const FwdArgs &a, const Plan &pl, hipStream_t s) {
   using S = FwdShape<WPR>;
-  const unsigned grid = (unsigned)((a.M + S::G - 1) / S::G);
-  adaln_fwd_kernel<TX, TY, K, WPR, VEC><<<grid, S::BLK, 0, s>>>(a);
+  adaln_fwd_kernel<TX, TY, K, WPR, VEC, kFwdNT><<<fwd_grid(pl, a.M), S::BLK, 0, s>>>(a);
   return check_launch("nf_adaln_fwd");
 }
 template <typename TX, typename TY, bool VEC, int WPR, int K>
 int launch_bwd_t(const BwdArgs &a, int64_t B, hipStream_t s) {
   using S = BwdShape<WPR>;
   const unsigned grid = (unsigned)(B * a.J);
-  adaln_bwd_kernel<TX, TY, K, WPR, VEC><<<grid, S::BLK, 0, s>>>(a);
+  // next-row prefetch pays only when a thread holds two chunks per row
+  adaln_bwd_kernel<TX, TY, K, WPR, VEC, kBwdNT, (K > 1)><<<grid, S::BLK, 0, s>>>(a);
   return check_launch("nf_adaln_bwd");
 }
 
 template <typename TX, typename TY, bool VEC, int WPR>
 int fwd_k(const FwdArgs &a, const Plan &pl, hipStream_t s) {
   if constexpr (!VEC) {
-    return launch_fwd_t<TX, TY, false, WPR, 4>(a, s);
+    return launch_fwd_t<TX, TY, false, WPR, 2>(a, pl, s);
   } else {
-    switch (pl.fwd_k) {
-      case 1: return launch_fwd_t<TX, TY, true, WPR, 1>(a, s);
-      case 2: return launch_fwd_t<TX, TY, true, WPR, 2>(a, s);
-      default: return launch_fwd_t<TX, TY, true, WPR, 4>(a, s);
-    }
+    if (pl.fwd_k == 1) return launch_fwd_t<TX, TY, true, WPR, 1>(a, pl, s);
+    return launch_fwd_t<TX, TY, true, WPR, 2>(a, pl, s);
   }
 }
 template <typename TX, typename TY, bool VEC, int WPR>
@@ -420,7 +509,8 @@ int fwd_w(const FwdArgs &a, const Plan &pl, hipStream_t s) {
     case 1: return fwd_k<TX, TY, VEC, 1>(a, pl, s);
     case 2: return fwd_k<TX, TY, VEC, 2>(a, pl, s);
     case 4: return fwd_k<TX, TY, VEC, 4>(a, pl, s);
-    default: return fwd_k<TX, TY, VEC, 8>(a, pl, s);
+    case 8: return fwd_k<TX, TY, VEC, 8>(a, pl, s);
+    default: return fwd_k<TX, TY, VEC, 16>(a, pl, s);
   }
 }
 template <typename TX, typename TY, bool VEC>

@@ -115,6 +115,33 @@ __device__ __forceinline__ void store8(T *p, int valid, const float (&v)[8]) {
     store8_masked<T>(p, valid, v);
 }
 
+// As store8, with the non-temporal hint on the 16-byte vector stores when NT
+// (streaming outputs that are not re-read by this kernel).
+template <typename T, bool VEC, bool NT>
+__device__ __forceinline__ void store8_hint(T *p, int valid, const float (&v)[8]) {
+  if constexpr (NT) {
+    if (VEC && valid >= 8) {
+      if constexpr (sizeof(T) == 4) {
+        u32x4 a, b;
+        a.x = __float_as_uint(v[0]); a.y = __float_as_uint(v[1]);
+        a.z = __float_as_uint(v[2]); a.w = __float_as_uint(v[3]);
+        b.x = __float_as_uint(v[4]); b.y = __float_as_uint(v[5]);
+        b.z = __float_as_uint(v[6]); b.w = __float_as_uint(v[7]);
+        __builtin_nontemporal_store(a, reinterpret_cast<u32x4 *>(p));
+        __builtin_nontemporal_store(b, reinterpret_cast<u32x4 *>(p + 4));
+      } else {
+        typedef T t8 __attribute__((ext_vector_type(8)));
+        t8 a;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) a[i] = static_cast<T>(v[i]);
+        __builtin_nontemporal_store(__builtin_bit_cast(u32x4, a), reinterpret_cast<u32x4 *>(p));
+      }
+      return;
+    }
+  }
+  store8<T, VEC>(p, valid, v);
+}
+
 // An 8-element chunk kept in its storage type (4 VGPRs for bf16/f16, 8 for
 // f32) and widened to fp32 element by element on use.  Holding a row's
 // incoming chunks this way halves the register cost of 16-bit inputs.

@@ -32,6 +32,7 @@ from .utils import device_of, require_device
 MAX_N = 16384
 
 
+
 def _rows(t: torch.Tensor) -> torch.Tensor:
     """2-D view with unit-stride columns (copy only if the last dim is strided)."""
     return t if t.stride(-1) == 1 else t.contiguous()
@@ -107,29 +108,31 @@ class _FusedAdaLNResidualRMSNorm(torch.autograd.Function):
         dweight = torch.empty((n,), dtype=weight.dtype, device=dev) if need[3] else None
         dscale = torch.empty((b, n), dtype=scale.dtype, device=dev) if need[4] else None
         dshift = torch.empty((b, n), dtype=ctx.shift_dtype, device=dev) if need[5] else None
-        if m == 0:
-            if dweight is not None:
-                dweight.zero_()
-            return dx, dy, dgate, dweight, dscale, dshift, None, None
-
         L = _lib.lib()
         dc = _lib.dtype_code
         ws_bytes = L.nf_adaln_bwd_workspace(m, n, t)
-        ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+        ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
         with device_of(x):
+            stream = _lib.stream_of(x)
             _lib.check(
                 L.nf_adaln_bwd(
                     _lib.ptr(dh_up), _lib.ptr(dout),
                     x.data_ptr(), x.stride(0), y.data_ptr(), y.stride(0),
                     gate.data_ptr(), gate.stride(0), weight.data_ptr(),
                     scale.data_ptr(), scale.stride(0), rstd.data_ptr(),
-                    dx.data_ptr(), dy.data_ptr(),
-                    _lib.ptr(dgate), _lib.ptr(dweight), _lib.ptr(dscale), _lib.ptr(dshift),
-                    ws.data_ptr(), ws_bytes, m, n, t,
-                    dc(x), dc(y), dc(gate), dc(weight), dc(scale), dc(ctx.shift_dtype),
-                    _lib.stream_of(x),
+                    dx.data_ptr(), dy.data_ptr(), ws.data_ptr(), ws_bytes, m, n, t,
+                    dc(x), dc(y), dc(gate), dc(weight), dc(scale), stream,
                 ),
                 "nf_adaln_bwd",
+            )
+            _lib.check(
+                L.nf_adaln_bwd_reduce(
+                    ws.data_ptr(), ws_bytes, weight.data_ptr(), scale.data_ptr(),
+                    scale.stride(0), _lib.ptr(dgate), _lib.ptr(dweight), _lib.ptr(dscale),
+                    _lib.ptr(dshift), m, n, t, dc(gate), dc(weight), dc(scale),
+                    dc(ctx.shift_dtype), stream,
+                ),
+                "nf_adaln_bwd_reduce",
             )
         return (dx if need[0] else None, dy if need[1] else None,
                 dgate, dweight, dscale, dshift, None, None)

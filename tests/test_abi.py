@@ -81,9 +81,16 @@ def test_adaln_argument_validation():
     assert L.nf_adaln_bwd_workspace(10, 1024, 3) == 0
     small = L.nf_adaln_bwd_workspace(64, 1024, 8)
     bwd = [FAKE, FAKE, FAKE, 1024, FAKE, 1024, FAKE, 1024, FAKE, FAKE, 1024, FAKE, FAKE, FAKE,
-           None, None, None, None, FAKE, small - 1, 64, 1024, 8, 1, 1, 1, 1, 1, 1, None]
+           FAKE, small - 1, 64, 1024, 8, 1, 1, 1, 1, 1, None]
     assert L.nf_adaln_bwd(*bwd) == NF_ERR_WORKSPACE
     assert "workspace" in _err()
+    red = [FAKE, small - 1, FAKE, FAKE, 1024, FAKE, None, None, None, 64, 1024, 8, 1, 1, 1, 1, None]
+    assert L.nf_adaln_bwd_reduce(*red) == NF_ERR_WORKSPACE
+    red[1] = small
+    red[3] = None
+    assert L.nf_adaln_bwd_reduce(*red) == NF_ERR_ARG  # scale missing
+    assert L.nf_adaln_bwd_reduce(FAKE, small, FAKE, FAKE, 1024, None, None, None, None,
+                                 64, 1024, 8, 1, 1, 1, 1, None) == NF_OK  # nothing requested
 
 
 def test_ce_argument_validation():

@@ -6,7 +6,8 @@ shapes (tests/test_kernels.py:85-115, incl. the N=1000 masked tail), odd N
 (element-wise kernel variant), wide N (multi-wavefront rows), mixed autocast
 dtypes, strided / broadcast conditioning views as the DiT block passes them
 (model/dit.py:146-166), missing upstream gradients, and the large seam stress
-shape [32,2048,2048] checked sample by sample.
+shape [32,2048,2048]; many samples with one row each (several reduction
+rounds) and single-row inputs.
 """
 
 from __future__ import annotations
@@ -75,7 +76,8 @@ def test_cfg1_fp32_all_six_gradients(cuda):
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("b,t,n", [(2, 16, 256), (4, 32, 1024), (3, 7, 768), (1, 64, 1536),
                                    (2, 8, 1000), (2, 3, 333), (1, 5, 8), (2, 4, 4096),
-                                   (1, 2, 16384)])
+                                   (1, 2, 16384), (300, 1, 64), (1, 1, 1024), (5, 3, 2048),
+                                   (3, 700, 512)])
 def test_adaln_matches_oracle(cuda, dtype, b, t, n):
     note(f"adaln dtype={dtype} b={b} t={t} n={n}")
     inp = _inputs(b, t, n, dtype, cuda)
