@@ -54,6 +54,9 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-extra", action="store_true", help="headline workload only")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baselines")
+    ap.add_argument("--only", choices=("swiglu", "ce", "stress"), default=None,
+                    help="run one secondary workload alone (for profiling) and print its "
+                         "record instead of the headline line")
     ap.add_argument("--json-out", default=None, help="also write the JSON record here")
     return ap.parse_args()
 
@@ -448,6 +451,10 @@ def main() -> int:
         return 1
     dev = torch.device("cuda", 0)
     log(f"device: {torch.cuda.get_device_name(0)}  torch {torch.__version__}")
+    if args.only:
+        fn = {"swiglu": bench_swiglu, "ce": bench_ce, "stress": bench_stress}[args.only]
+        print(json.dumps({"workload": args.only, **fn(args, dev)}), flush=True)
+        return 0
 
     log("adaLN cfg2 ...")
     ad = bench_adaln(args, dev)

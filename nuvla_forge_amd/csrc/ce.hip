@@ -29,10 +29,27 @@ namespace ce {
 using gemm::Cfg;
 using gemm::floatx16;
 
-constexpr int kTileN = 128;  // vocabulary columns per stats partial
 
+// bf16: 256x256 block tiles, 8 wavefronts of 128x64 (two per SIMD, so one
+// wavefront's LDS waits and epilogue overlap the other's MFMAs), operands
+// copied global -> LDS directly, four K-stages in flight; f32 (correctness
+// path): 128x128 tiles staged through registers.
 template <typename TI>
-using MainCfg = Cfg<TI, 128, 128, 2, 2>;
+struct MainCfgT;
+template <>
+struct MainCfgT<bf16> { using type = gemm::DCfg<256, 256, 2, 4, 4>; };
+template <>
+struct MainCfgT<float> { using type = Cfg<float, 128, 128, 2, 2>; };
+template <typename TI>
+using MainCfg = typename MainCfgT<TI>::type;
+
+// Can an operand of `rows` x K (row stride ld) use the buffer-load path?
+template <typename TI>
+inline bool buf_ok(const void *p, int64_t ld, int64_t rows, int64_t K) {
+  constexpr int VE = 16 / sizeof(TI);
+  return K % VE == 0 && ld % VE == 0 && aligned16(p) &&
+         rows * ld * (int64_t)sizeof(TI) < ((int64_t)1 << 31) - 64;
+}
 
 __device__ __forceinline__ float log_f32(float x) {
   constexpr float kLn2 = 0.6931471805599453f;  // ln(2)
@@ -40,43 +57,64 @@ __device__ __forceinline__ float log_f32(float x) {
 }
 
 // ---------------------------------------------------------------------------
-// plain store epilogue: C[m, n] (+)= acc
+// plain store epilogue, C[m, n] (+)= acc, for one or two independent GEMMs in
+// one launch (the dW and dH products of a vocabulary chunk: each alone is too
+// few 256x256 tiles to fill the chip, together they do)
 // ---------------------------------------------------------------------------
-template <class C, bool VK>
-__global__ __launch_bounds__(C::NT) void gemm_store_kernel(
-    const typename C::TI *A, int64_t lda, const typename C::TI *B, int64_t ldb,
-    float *Cout, int64_t ldc, int64_t M, int64_t N, int64_t K, int accumulate) {
+template <typename TI>
+struct GemmJob {
+  const TI *A;
+  const TI *B;
+  float *C;
+  int64_t lda, ldb, ldc, M, N, K;
+  int accumulate;
+  int tiles_m;  // tiles along M; tile t is (t % tiles_m, t / tiles_m)
+  int tiles;    // tiles of this job
+};
+
+template <class C, bool BUF>
+__global__ NF_GEMM_BOUNDS(C) void gemm_store_kernel(GemmJob<typename C::TI> j0,
+                                                           GemmJob<typename C::TI> j1) {
   __shared__ __attribute__((aligned(16))) char smem[C::LDS_BYTES];
-  const int64_t m0 = (int64_t)blockIdx.x * C::BM;
-  const int64_t n0 = (int64_t)blockIdx.y * C::BN;
+  int t = blockIdx.x;
+  const bool second = t >= j0.tiles;
+  const GemmJob<typename C::TI> &j = second ? j1 : j0;
+  if (second) t -= j0.tiles;
+  const int64_t m0 = (int64_t)(t % j.tiles_m) * C::BM;
+  const int64_t n0 = (int64_t)(t / j.tiles_m) * C::BN;
+  const int64_t M = j.M, N = j.N, ldc = j.ldc;
+  float *const Cout = j.C;
+  const int accumulate = j.accumulate;
   floatx16 acc[C::TM][C::TN];
-  gemm::mainloop<C, VK>(A, lda, B, ldb, M, N, K, m0, n0, smem, acc);
+  gemm::mainloop<C, BUF>(j.A, j.lda, j.B, j.ldb, M, N, j.K, m0, n0, smem, acc);
   const int w = threadIdx.x >> 6, wm = w / C::WN, wn = w % C::WN;
 #pragma unroll
   for (int i = 0; i < C::TM; ++i)
 #pragma unroll
-    for (int j = 0; j < C::TN; ++j) {
-      const int64_t col = n0 + gemm::acc_col<C>(wn, j);
+    for (int jj = 0; jj < C::TN; ++jj) {
+      const int64_t col = n0 + gemm::acc_col<C>(wn, jj);
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int64_t row = m0 + gemm::acc_row<C>(wm, i, r);
         if (row < M && col < N) {
           float *p = Cout + row * ldc + col;
-          *p = accumulate ? *p + acc[i][j][r] : acc[i][j][r];
+          *p = accumulate ? *p + acc[i][jj][r] : acc[i][jj][r];
         }
       }
+      // one 32x32 tile at a time: the read-modify-write loads of the whole
+      // accumulator are not hoisted into (and spilled from) registers
+      __builtin_amdgcn_sched_barrier(0);
     }
 }
 
 // ---------------------------------------------------------------------------
 // stats epilogue: per-row (max, sum exp) over this block's 128 columns
 // ---------------------------------------------------------------------------
-template <class C, bool VK>
-__global__ __launch_bounds__(C::NT) void ce_stats_kernel(
+template <class C, bool BUF>
+__global__ NF_GEMM_BOUNDS(C) void ce_stats_kernel(
     const typename C::TI *H, const typename C::TI *W, int64_t M, int64_t V,
     int64_t D, const int64_t *targets, float2 *stats, float *tgt_logit,
     int ntiles) {
-  static_assert(C::BN == kTileN, "stats tile width");
   __shared__ __attribute__((aligned(16))) char smem[C::LDS_BYTES];
   __shared__ int tgt_s[C::BM];
   __shared__ float redm[C::BM][C::WN];
@@ -92,7 +130,7 @@ __global__ __launch_bounds__(C::NT) void ce_stats_kernel(
     tgt_s[t] = tc;
   }
   floatx16 acc[C::TM][C::TN];
-  gemm::mainloop<C, VK>(H, D, W, D, M, V, D, m0, n0, smem, acc);
+  gemm::mainloop<C, BUF>(H, D, W, D, M, V, D, m0, n0, smem, acc);
 
   const int l = threadIdx.x & 63;
   const int w = threadIdx.x >> 6, wm = w / C::WN, wn = w % C::WN;
@@ -210,16 +248,16 @@ __global__ __launch_bounds__(kLossThreads) void ce_loss_kernel(
 // ---------------------------------------------------------------------------
 // probability epilogue: P = inv * (softmax - onehot) for one vocab chunk
 // ---------------------------------------------------------------------------
-template <class C, bool VK>
-__global__ __launch_bounds__(C::NT) void ce_prob_kernel(
+template <class C, bool BUF>
+__global__ NF_GEMM_BOUNDS(C) void ce_prob_kernel(
     const typename C::TI *H, const typename C::TI *Wc, int64_t M, int64_t Vc,
     int64_t D, int64_t vbase, const int *tcol, const float *lse,
     const float *inv_ptr, typename C::TI *P, int64_t ldp, int64_t kpad,
     typename C::TI *PT, int64_t ldpt) {
   using TI = typename C::TI;
   constexpr int TP = C::BM + 16;  // transposed-tile pitch (elements)
-  static_assert(C::BN * TP * sizeof(TI) <= C::LDS_BYTES, "transpose tile");
-  __shared__ __attribute__((aligned(16))) char smem[C::LDS_BYTES];
+  constexpr int kTile = C::BN * TP * (int)sizeof(TI);
+  __shared__ __attribute__((aligned(16))) char smem[kTile > C::LDS_BYTES ? kTile : C::LDS_BYTES];
   __shared__ int tc_s[C::BM];
   __shared__ float lse_s[C::BM];
   const int64_t m0 = (int64_t)blockIdx.x * C::BM;
@@ -230,7 +268,7 @@ __global__ __launch_bounds__(C::NT) void ce_prob_kernel(
     lse_s[t] = in ? lse[m0 + t] : 0.f;
   }
   floatx16 acc[C::TM][C::TN];
-  gemm::mainloop<C, VK>(H, D, Wc, D, M, Vc, D, m0, n0, smem, acc);
+  gemm::mainloop<C, BUF>(H, D, Wc, D, M, Vc, D, m0, n0, smem, acc);
   const float inv = *inv_ptr;
 
   TI *tile = reinterpret_cast<TI *>(smem);  // [BN][TP]: tile[col][row]
@@ -338,7 +376,8 @@ inline Layout make_layout(int64_t M, int64_t D, int64_t V, int64_t vocab_chunk, 
   L.ldht = round_up(M, 8);
   L.vc = round_up(vocab_chunk < V ? vocab_chunk : V, 8);
   L.ldp = L.vc;
-  L.ntiles = (V + kTileN - 1) / kTileN;
+  L.ntiles = (V + MainCfg<bf16>::BN - 1) / MainCfg<bf16>::BN;
+  if (es == 4) L.ntiles = (V + MainCfg<float>::BN - 1) / MainCfg<float>::BN;
   size_t o = 0;
   auto take = [&](size_t bytes) { const size_t at = o; o = align256(o + bytes); return at; };
   L.off_wt = take((size_t)D * L.ldwt * es);
@@ -357,18 +396,35 @@ inline Layout make_layout(int64_t M, int64_t D, int64_t V, int64_t vocab_chunk, 
 }
 
 template <class C>
-int launch_gemm_store(const typename C::TI *A, int64_t lda, const typename C::TI *B,
-                      int64_t ldb, float *Cout, int64_t ldc, int64_t M, int64_t N,
-                      int64_t K, int accumulate, hipStream_t s) {
-  using TI = typename C::TI;
-  constexpr int VE = 16 / sizeof(TI);
-  const bool vk = K % VE == 0 && lda % VE == 0 && ldb % VE == 0 && aligned16(A) &&
-                  aligned16(B);
-  dim3 grid((unsigned)((M + C::BM - 1) / C::BM), (unsigned)((N + C::BN - 1) / C::BN));
-  if (vk)
-    gemm_store_kernel<C, true><<<grid, C::NT, 0, s>>>(A, lda, B, ldb, Cout, ldc, M, N, K, accumulate);
+GemmJob<typename C::TI> make_job(const typename C::TI *A, int64_t lda, const typename C::TI *B,
+                                 int64_t ldb, float *Cout, int64_t ldc, int64_t M, int64_t N,
+                                 int64_t K, int accumulate) {
+  GemmJob<typename C::TI> j;
+  j.A = A; j.B = B; j.C = Cout;
+  j.lda = lda; j.ldb = ldb; j.ldc = ldc; j.M = M; j.N = N; j.K = K;
+  j.accumulate = accumulate;
+  j.tiles_m = (int)((M + C::BM - 1) / C::BM);
+  j.tiles = j.tiles_m * (int)((N + C::BN - 1) / C::BN);
+  return j;
+}
+
+template <typename TI>
+bool job_buf_ok(const GemmJob<TI> &j) {
+  return j.tiles == 0 || (buf_ok<TI>(j.A, j.lda, j.M, j.K) && buf_ok<TI>(j.B, j.ldb, j.N, j.K));
+}
+
+// Both jobs in one grid (j1 may be empty: tiles == 0).
+template <class C>
+int launch_gemm_store(const GemmJob<typename C::TI> &j0, const GemmJob<typename C::TI> &j1,
+                      hipStream_t s) {
+  const int64_t total = (int64_t)j0.tiles + j1.tiles;
+  if (total == 0) return NF_OK;
+  if (total > 0x7fffffffLL) return set_error(NF_ERR_ARG, "gemm: too many tiles");
+  const dim3 grid((unsigned)total);
+  if (job_buf_ok(j0) && job_buf_ok(j1))
+    gemm_store_kernel<C, true><<<grid, C::NT, 0, s>>>(j0, j1);
   else
-    gemm_store_kernel<C, false><<<grid, C::NT, 0, s>>>(A, lda, B, ldb, Cout, ldc, M, N, K, accumulate);
+    gemm_store_kernel<C, false><<<grid, C::NT, 0, s>>>(j0, j1);
   return check_launch("gemm_store");
 }
 
@@ -385,7 +441,6 @@ int ce_run(const TI *H, const TI *W, const int64_t *targets, int64_t M, int64_t 
            int64_t V, int64_t ignore_index, int64_t vocab_chunk, float *loss,
            float *dH, float *dW, int32_t *bad, char *ws, hipStream_t s) {
   using C = MainCfg<TI>;
-  constexpr int VE = 16 / sizeof(TI);
   const Layout L = make_layout(M, D, V, vocab_chunk, sizeof(TI));
   TI *Wt = reinterpret_cast<TI *>(ws + L.off_wt);
   TI *Ht = reinterpret_cast<TI *>(ws + L.off_ht);
@@ -404,7 +459,7 @@ int ce_run(const TI *H, const TI *W, const int64_t *targets, int64_t M, int64_t 
   if ((e = launch_transpose<U>(W, V, D, D, Wt, L.ldwt, s))) return e;
   if ((e = launch_transpose<U>(H, M, D, D, Ht, L.ldht, s))) return e;
 
-  const bool vk = D % VE == 0 && aligned16(H) && aligned16(W);
+  const bool vk = buf_ok<TI>(H, D, M, D) && buf_ok<TI>(W, D, V, D);
   dim3 gs((unsigned)((M + C::BM - 1) / C::BM), (unsigned)L.ntiles);
   if (vk)
     ce_stats_kernel<C, true><<<gs, C::NT, 0, s>>>(H, W, M, V, D, targets, stats, tgt, (int)L.ntiles);
@@ -423,19 +478,18 @@ int ce_run(const TI *H, const TI *W, const int64_t *targets, int64_t M, int64_t 
     const int64_t kpad = round_up(vc, 8);
     const TI *Wc = W + vb * D;
     dim3 gp((unsigned)((M + C::BM - 1) / C::BM), (unsigned)((vc + C::BN - 1) / C::BN));
-    if (vk)
+    if (vk && buf_ok<TI>(Wc, D, vc, D))
       ce_prob_kernel<C, true><<<gp, C::NT, 0, s>>>(H, Wc, M, vc, D, vb, tcol, lse, inv, P, L.ldp,
                                                    kpad, PT, L.ldht);
     else
       ce_prob_kernel<C, false><<<gp, C::NT, 0, s>>>(H, Wc, M, vc, D, vb, tcol, lse, inv, P, L.ldp,
                                                     kpad, PT, L.ldht);
     if ((e = check_launch("ce_prob"))) return e;
-    // dW[vb:vb+vc, :] = P_c^T H   (K = tokens, zero-padded to ldht)
-    if ((e = launch_gemm_store<C>(PT, L.ldht, Ht, L.ldht, dW + vb * D, D, vc, D, L.ldht, 0, s)))
-      return e;
-    // dH += P_c W_c   (K = chunk columns, zero-padded to kpad)
-    if ((e = launch_gemm_store<C>(P, L.ldp, Wt + vb, L.ldwt, dH, D, M, D, kpad, vb > 0 ? 1 : 0, s)))
-      return e;
+    // dW[vb:vb+vc, :] = P_c^T H   (K = tokens, zero-padded to ldht) and
+    // dH += P_c W_c               (K = chunk columns, zero-padded to kpad)
+    const auto jw = make_job<C>(PT, L.ldht, Ht, L.ldht, dW + vb * D, D, vc, D, L.ldht, 0);
+    const auto jh = make_job<C>(P, L.ldp, Wt + vb, L.ldwt, dH, D, M, D, kpad, vb > 0 ? 1 : 0);
+    if ((e = launch_gemm_store<C>(jw, jh, s))) return e;
   }
   return NF_OK;
 }
@@ -517,14 +571,21 @@ extern "C" int nf_gemm_nt(const void *A, int64_t lda, const void *B, int64_t ldb
   if (M == 0 || N == 0) return NF_OK;
   if (!A || !B || !C) return set_error(NF_ERR_ARG, "nf_gemm_nt: null pointer");
   if (lda < K || ldb < K || ldc < N) return set_error(NF_ERR_ARG, "nf_gemm_nt: bad leading dim");
-  if ((M + 127) / 128 > 0x7fffffffLL || (N + 127) / 128 > 65535)
+  // tiles are at least 128 x 128; the grid is one-dimensional
+  if (((M + 127) / 128) * ((N + 127) / 128) > 0x7fffffffLL)
     return set_error(NF_ERR_ARG, "nf_gemm_nt: grid too large");
   hipStream_t s = static_cast<hipStream_t>(stream);
-  if (dtype == NF_DTYPE_BF16)
-    return launch_gemm_store<MainCfg<bf16>>((const bf16 *)A, lda, (const bf16 *)B, ldb, C, ldc, M,
-                                            N, K, 0, s);
-  if (dtype == NF_DTYPE_F32)
-    return launch_gemm_store<MainCfg<float>>((const float *)A, lda, (const float *)B, ldb, C, ldc,
-                                             M, N, K, 0, s);
+  if (dtype == NF_DTYPE_BF16) {
+    using C16 = MainCfg<bf16>;
+    const GemmJob<bf16> none{};
+    return launch_gemm_store<C16>(
+        make_job<C16>((const bf16 *)A, lda, (const bf16 *)B, ldb, C, ldc, M, N, K, 0), none, s);
+  }
+  if (dtype == NF_DTYPE_F32) {
+    using C32 = MainCfg<float>;
+    const GemmJob<float> none{};
+    return launch_gemm_store<C32>(
+        make_job<C32>((const float *)A, lda, (const float *)B, ldb, C, ldc, M, N, K, 0), none, s);
+  }
   return set_error(NF_ERR_DTYPE, "nf_gemm_nt: dtype %d unsupported", dtype);
 }

@@ -10,14 +10,27 @@
 //  * Accumulator (32x32, 16 fp32 per lane): register r of lane l holds
 //    row 8 * (r / 4) + 4 * (l / 32) + (r % 4), column l % 32.
 //
-// A K-stage is 128 bytes of every tile row (64 bf16 / 32 f32).  Rows are
-// staged in LDS with a 144-byte pitch, which makes both the 16-byte row
-// writes and the 16-byte MFMA operand reads (eight lanes, eight distinct
-// rows) bank-conflict free.  Two LDS stages plus a register prefetch of the
-// next stage give one barrier per K-stage.
+// Two stagings of the operand tiles in LDS:
+//  * Cfg (bf16 and f32): a K-stage is 128 bytes of every tile row (64 bf16 /
+//    32 f32), loaded into registers and written to LDS with a 144-byte row
+//    pitch, which makes both the 16-byte row writes and the 16-byte MFMA
+//    operand reads (eight lanes, eight distinct rows) bank-conflict free.
+//  * DCfg (bf16): a K-stage is 64 bytes of every tile row (32 bf16), copied
+//    global -> LDS by the buffer unit (buffer_load_dwordx4 ... lds) with no
+//    register staging, four stages in flight.  One such load writes 1 KB
+//    contiguously (lane i at +16 i), i.e. 16 unpadded 64-byte rows; the
+//    16-byte vectors of row r are stored XOR-swizzled (slot = kvec ^
+//    ((r >> 2) & 3)), which keeps the MFMA operand reads conflict free.
 #pragma once
 
 #include "nf_device.h"
+
+// Kernel attributes for a GEMM block of configuration C: its thread count,
+// and exactly the wavefronts per SIMD that one block brings (one block per
+// CU at these LDS sizes), so the compiler does not trade registers for an
+// occupancy the LDS cannot give anyway.
+#define NF_GEMM_BOUNDS(C) \
+  __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(C::NT / 256, C::NT / 256)))
 
 namespace nf {
 namespace gemm {
@@ -43,8 +56,38 @@ struct Cfg {
   static constexpr int LDS_BYTES = 2 * STAGE;
   static constexpr int AV = BM * KV / NT;        // A vectors per thread per stage
   static constexpr int BV = BN * KV / NT;        // B vectors per thread per stage
+  // K-stages of global loads in flight ahead of the MFMAs (register sets):
+  // 2 for small wave tiles, whose short compute stage hides little latency,
+  // 1 where a second set would not fit beside the accumulators.
+  static constexpr int PF = (NT <= 256 && TM * TN <= 4) ? 2 : 1;
+  static constexpr bool DTL = false;
   static_assert(BM % (WM * 32) == 0 && BN % (WN * 32) == 0, "tile/wave mismatch");
   static_assert((BM * KV) % NT == 0 && (BN * KV) % NT == 0, "loader mismatch");
+};
+
+// Direct-to-LDS bf16 configuration (see the file comment).
+template <int BM_, int BN_, int WM_, int WN_, int STAGES_ = 4>
+struct DCfg {
+  using TI = bf16;
+  static constexpr bool DTL = true;
+  static constexpr int BM = BM_, BN = BN_, WM = WM_, WN = WN_, STAGES = STAGES_;
+  static constexpr int NW = WM * WN;              // wavefronts per block
+  static constexpr int NT = NW * 64;
+  static constexpr int WTM = BM / WM, WTN = BN / WN;
+  static constexpr int TM = WTM / 32, TN = WTN / 32;
+  static constexpr int VE = 8;                    // bf16 per 16-byte vector
+  static constexpr int BK = 32;                   // k per stage: 64-byte LDS rows
+  static constexpr int ROW = 64;
+  static constexpr int STAGE = (BM + BN) * ROW;
+  static constexpr int LDS_BYTES = STAGES * STAGE;
+  static constexpr int ACW = BM / 16 / NW;        // 1 KB A chunks per wave per stage
+  static constexpr int BCW = BN / 16 / NW;        // 1 KB B chunks per wave per stage
+  static constexpr int PF = 0;
+  static_assert(BM % (WM * 32) == 0 && BN % (WN * 32) == 0, "tile/wave mismatch");
+  static_assert((BM / 16) % NW == 0 && (BN / 16) % NW == 0, "chunk/wave mismatch");
+  static_assert(WTM % 16 == 0 && WTN % 16 == 0, "swizzle assumes 16-row alignment");
+  static_assert(STAGES >= 2 && STAGES <= 5 && (STAGES - 1) * (ACW + BCW) <= 63,
+                "vmcnt range");
 };
 
 // One 16-byte vector of a tile row: rows >= nrows or k >= K read as zero.
@@ -70,27 +113,56 @@ __device__ __forceinline__ u32x4 load_vec(const TI *base, int64_t ld,
   return r;
 }
 
-template <class C, bool VK>
-__device__ __forceinline__ void load_stage(const typename C::TI *A, int64_t lda,
-                                           int64_t M, const typename C::TI *B,
-                                           int64_t ldb, int64_t N, int64_t K,
-                                           int64_t m0, int64_t n0, int64_t k0,
-                                           u32x4 (&ra)[C::AV],
-                                           u32x4 (&rb)[C::BV]) {
-  const int t = threadIdx.x;
-#pragma unroll
-  for (int i = 0; i < C::AV; ++i) {
-    const int v = t + i * C::NT;
-    ra[i] = load_vec<typename C::TI, VK>(A, lda, m0 + v / C::KV, M,
-                                         k0 + (v % C::KV) * C::VE, K);
+// Operand source for the K loop.  BUF (the fast path): a buffer resource
+// over the whole operand, each thread's 16-byte vectors addressed by one
+// 32-bit base offset plus uniform strides; a vector whose row is past the
+// matrix or whose k is past K gets an out-of-range offset, which the buffer
+// unit turns into zeros (no branches, no 64-bit address math).  Requires
+// K % VE == 0, 16-byte aligned rows and an operand under 2 GiB.
+// !BUF: plain pointer loads with per-element masking (any K, any alignment).
+template <class C, bool BUF>
+struct Operand {
+  using TI = typename C::TI;
+  const TI *base;
+  int64_t ld, rows, K, r0;
+  __amdgpu_buffer_rsrc_t rsrc;
+  uint32_t off0;       // byte offset of this thread's first vector at k = 0
+  uint32_t row_step;   // bytes between this thread's successive vectors
+  __device__ __forceinline__ void init(const TI *p, int64_t ld_, int64_t rows_, int64_t K_,
+                                       int64_t r0_) {
+    base = p; ld = ld_; rows = rows_; K = K_; r0 = r0_;
+    if constexpr (BUF) {
+      rsrc = __builtin_amdgcn_make_buffer_rsrc(const_cast<TI *>(p), (short)0,
+                                               (int)(rows_ * ld_ * (int64_t)sizeof(TI)),
+                                               0x00020000);
+      const int t = threadIdx.x;
+      off0 = (uint32_t)(((r0_ + t / C::KV) * ld_ + (t % C::KV) * C::VE) * (int64_t)sizeof(TI));
+      row_step = (uint32_t)((C::NT / C::KV) * ld_ * (int64_t)sizeof(TI));
+    }
   }
+  // vector i (0 <= i < count) of the stage starting at k0
+  template <int COUNT>
+  __device__ __forceinline__ void load(int64_t k0, u32x4 (&r)[COUNT]) const {
+    const int t = threadIdx.x;
+    if constexpr (BUF) {
+      const int64_t kk = k0 + (t % C::KV) * C::VE;
+      const bool kin = kk < K;
+      const uint32_t kb = (uint32_t)(k0 * (int64_t)sizeof(TI));
 #pragma unroll
-  for (int i = 0; i < C::BV; ++i) {
-    const int v = t + i * C::NT;
-    rb[i] = load_vec<typename C::TI, VK>(B, ldb, n0 + v / C::KV, N,
-                                         k0 + (v % C::KV) * C::VE, K);
+      for (int i = 0; i < COUNT; ++i) {
+        const bool in = kin && (r0 + t / C::KV + (int64_t)i * (C::NT / C::KV)) < rows;
+        const uint32_t off = in ? off0 + (uint32_t)i * row_step + kb : 0x80000000u;
+        r[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, off, 0, 0));
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < COUNT; ++i) {
+        const int v = t + i * C::NT;
+        r[i] = load_vec<TI, false>(base, ld, r0 + v / C::KV, rows, k0 + (v % C::KV) * C::VE, K);
+      }
+    }
   }
-}
+};
 
 template <class C>
 __device__ __forceinline__ void store_stage(char *stage, const u32x4 (&ra)[C::AV],
@@ -130,35 +202,265 @@ __device__ __forceinline__ void mfma_slab<float>(const u32x4 &a, const u32x4 &b,
 }
 
 template <class C>
+__device__ __forceinline__ void read_operands(const char *as, const char *bs, int kg,
+                                              u32x4 (&a)[C::TM], u32x4 (&b)[C::TN]) {
+#pragma unroll
+  for (int i = 0; i < C::TM; ++i)
+    a[i] = *reinterpret_cast<const u32x4 *>(as + i * 32 * C::PITCH + kg * 32);
+#pragma unroll
+  for (int j = 0; j < C::TN; ++j)
+    b[j] = *reinterpret_cast<const u32x4 *>(bs + j * 32 * C::PITCH + kg * 32);
+}
+
+template <class C>
+__device__ __forceinline__ void mfma_block(const u32x4 (&a)[C::TM], const u32x4 (&b)[C::TN],
+                                           floatx16 (&acc)[C::TM][C::TN]) {
+#pragma unroll
+  for (int i = 0; i < C::TM; ++i)
+#pragma unroll
+    for (int j = 0; j < C::TN; ++j) mfma_slab<typename C::TI>(a[i], b[j], acc[i][j]);
+}
+
+// Scheduling hint for one k-group: the (TM + TN) LDS operand reads of the
+// next k-group are spread between this k-group's TM * TN MFMAs, so their
+// latency hides behind matrix work instead of stalling the wavefront (one
+// wavefront per SIMD leaves no other wave to switch to).
+template <class C>
+__device__ __forceinline__ void interleave_hint() {
+  constexpr int kReads = C::TM + C::TN;
+  constexpr int kMfma = C::TM * C::TN * (sizeof(typename C::TI) == 2 ? 1 : 4);
+  constexpr int kPer = kMfma / kReads > 0 ? kMfma / kReads : 1;
+#pragma unroll
+  for (int r = 0; r < kReads; ++r) {
+    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);     // 1 DS read
+    __builtin_amdgcn_sched_group_barrier(0x008, kPer, 0);  // kPer MFMAs
+  }
+}
+
+template <class C>
 __device__ __forceinline__ void compute_stage(const char *stage, int wm, int wn,
                                               floatx16 (&acc)[C::TM][C::TN]) {
   const int l = threadIdx.x & 63;
   const char *as = stage + (wm * C::WTM + (l & 31)) * C::PITCH + (l >> 5) * 16;
   const char *bs = stage + (C::BM + wn * C::WTN + (l & 31)) * C::PITCH + (l >> 5) * 16;
+  // operands double-buffered across the four 32-byte k-groups of a stage
+  u32x4 a0[C::TM], b0[C::TN], a1[C::TM], b1[C::TN];
+  read_operands<C>(as, bs, 0, a0, b0);
 #pragma unroll
-  for (int kg = 0; kg < 4; ++kg) {
-    u32x4 a[C::TM], b[C::TN];
-#pragma unroll
-    for (int i = 0; i < C::TM; ++i)
-      a[i] = *reinterpret_cast<const u32x4 *>(as + i * 32 * C::PITCH + kg * 32);
-#pragma unroll
-    for (int j = 0; j < C::TN; ++j)
-      b[j] = *reinterpret_cast<const u32x4 *>(bs + j * 32 * C::PITCH + kg * 32);
-#pragma unroll
-    for (int i = 0; i < C::TM; ++i)
-#pragma unroll
-      for (int j = 0; j < C::TN; ++j) mfma_slab<typename C::TI>(a[i], b[j], acc[i][j]);
+  for (int kg = 0; kg < 4; kg += 2) {
+    read_operands<C>(as, bs, kg + 1, a1, b1);
+    mfma_block<C>(a0, b0, acc);
+    interleave_hint<C>();
+    if (kg + 2 < 4) {
+      read_operands<C>(as, bs, kg + 2, a0, b0);
+      mfma_block<C>(a1, b1, acc);
+      interleave_hint<C>();
+    } else {
+      mfma_block<C>(a1, b1, acc);
+    }
   }
 }
 
+// ---- direct-to-LDS path (DCfg) ----------------------------------------------
+
+// Lane l of a 1 KB chunk load covers tile row (chunk * 16 + l / 4) and LDS
+// slot l % 4, which holds k-vector (l % 4) ^ ((l >> 4) & 3) of that row.
+__device__ __forceinline__ int dtl_row(int l) { return l >> 2; }
+__device__ __forceinline__ int dtl_kvec(int l) { return (l & 3) ^ ((l >> 4) & 3); }
+
+typedef __attribute__((address_space(3))) void *lds_ptr_t;
+
+// One operand (A or B) of the block tile: CW chunks per wavefront.
+template <class C, int CW>
+struct DtlOperand {
+  using TI = typename C::TI;
+  const TI *base;
+  int64_t ld, rows, K;
+  __amdgpu_buffer_rsrc_t rsrc;
+  uint32_t off[CW];  // byte offset of this lane's vector at k = 0, or kOob
+  bool row_in[CW];
+  int lds_off[CW];   // chunk offset inside the operand's LDS region
+  int kvec;
+  static constexpr uint32_t kOob = 0x80000000u;
+
+  __device__ __forceinline__ void init(const TI *p, int64_t ld_, int64_t rows_, int64_t K_,
+                                       int64_t r0, int wave) {
+    base = p; ld = ld_; rows = rows_; K = K_;
+    rsrc = __builtin_amdgcn_make_buffer_rsrc(const_cast<TI *>(p), (short)0,
+                                             (int)(rows_ * ld_ * (int64_t)sizeof(TI)),
+                                             0x00020000);
+    const int l = threadIdx.x & 63;
+    kvec = dtl_kvec(l);
+#pragma unroll
+    for (int c = 0; c < CW; ++c) {
+      const int g = wave * CW + c;  // chunk index inside the tile
+      const int64_t row = r0 + g * 16 + dtl_row(l);
+      row_in[c] = row < rows_;
+      off[c] = row_in[c] ? (uint32_t)((row * ld_ + kvec * C::VE) * (int64_t)sizeof(TI)) : kOob;
+      lds_off[c] = g * 1024;
+    }
+  }
+  // copy the stage starting at k0 into `region` (this operand's part of a stage)
+  __device__ __forceinline__ void issue(int64_t k0, char *region) const {
+    const bool kin = k0 + kvec * C::VE < K;
+    const uint32_t kb = (uint32_t)(k0 * (int64_t)sizeof(TI));
+#pragma unroll
+    for (int c = 0; c < CW; ++c) {
+      const uint32_t o = (kin && row_in[c]) ? off[c] + kb : kOob;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (lds_ptr_t)(region + lds_off[c]), 16, o, 0,
+                                               0, 0);
+    }
+  }
+  // the same copy through registers and ds_write (any alignment, any K)
+  __device__ __forceinline__ void copy_sync(int64_t k0, int64_t r0, int wave, char *region) const {
+    const int l = threadIdx.x & 63;
+#pragma unroll
+    for (int c = 0; c < CW; ++c) {
+      const int g = wave * CW + c;
+      const u32x4 v = load_vec<TI, false>(base, ld, r0 + g * 16 + dtl_row(l), rows,
+                                          k0 + kvec * C::VE, K);
+      *reinterpret_cast<u32x4 *>(region + g * 1024 + l * 16) = v;
+    }
+  }
+};
+
+// s_waitcnt vmcnt(N) lgkmcnt(0), then s_barrier: after it the direct LDS
+// copies of the stage about to be read are complete in every wavefront, and
+// so are every wavefront's reads of the buffer about to be refilled.  The
+// wait is the builtin (so the compiler's own counter bookkeeping sees it);
+// the empty asm statements with memory clobbers keep LDS accesses from
+// moving across.  gfx9 encoding: vmcnt[3:0] bits 3:0, expcnt bits 6:4,
+// lgkmcnt bits 11:8, vmcnt[5:4] bits 15:14.
+template <int N>
+__device__ __forceinline__ void wait_vm_barrier() {
+  static_assert(N >= 0 && N <= 63, "vmcnt range");
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (0 << 8) | ((N >> 4) << 14));
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+template <class C>
+__device__ __forceinline__ void wait_stage(int n_after) {
+  constexpr int L = C::ACW + C::BCW;  // copies per wavefront per stage
+  static_assert((C::STAGES - 1) * L <= 63, "vmcnt range");
+  switch (n_after) {  // stages whose copies may still be in flight
+    case 0: wait_vm_barrier<0>(); break;
+    case 1: wait_vm_barrier<(1 * L < 63 ? 1 * L : 63)>(); break;
+    case 2: wait_vm_barrier<(2 * L < 63 ? 2 * L : 63)>(); break;
+    case 3: wait_vm_barrier<(3 * L < 63 ? 3 * L : 63)>(); break;
+    default: wait_vm_barrier<(4 * L < 63 ? 4 * L : 63)>(); break;
+  }
+}
+
+// Operands of one 16-wide k-group (0 or 1) of a stage, for this lane.
+template <class C>
+__device__ __forceinline__ void read_kgroup_dtl(const char *stage, int wm, int wn, int kg,
+                                                u32x4 (&a)[C::TM], u32x4 (&b)[C::TN]) {
+  const int l = threadIdx.x & 63;
+  // slot of this lane's k-vector: kvec = 2 kg + l / 32, swizzled by row
+  const int sw = (((2 * kg + (l >> 5)) ^ ((l >> 2) & 3)) * 16);
+  const char *as = stage + (wm * C::WTM + (l & 31)) * C::ROW + sw;
+  const char *bs = stage + (C::BM + wn * C::WTN + (l & 31)) * C::ROW + sw;
+#pragma unroll
+  for (int i = 0; i < C::TM; ++i) a[i] = *reinterpret_cast<const u32x4 *>(as + i * 32 * C::ROW);
+#pragma unroll
+  for (int j = 0; j < C::TN; ++j) b[j] = *reinterpret_cast<const u32x4 *>(bs + j * 32 * C::ROW);
+}
+
+template <class C, bool BUF>
+__device__ __forceinline__ void mainloop_dtl(const bf16 *A, int64_t lda, const bf16 *B,
+                                             int64_t ldb, int64_t M, int64_t N, int64_t K,
+                                             int64_t m0, int64_t n0, char *smem,
+                                             floatx16 (&acc)[C::TM][C::TN]) {
+  const int w = threadIdx.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(w);
+  const int wm = w / C::WN, wn = w % C::WN;
+#pragma unroll
+  for (int i = 0; i < C::TM; ++i)
+#pragma unroll
+    for (int j = 0; j < C::TN; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+  DtlOperand<C, C::ACW> opa;
+  DtlOperand<C, C::BCW> opb;
+  opa.init(A, lda, M, K, m0, wave);
+  opb.init(B, ldb, N, K, n0, wave);
+  const int64_t nk = (K + C::BK - 1) / C::BK;
+  u32x4 a0[C::TM], b0[C::TN], a1[C::TM], b1[C::TN];
+  if constexpr (BUF) {
+    // Stage kt lives in buffer kt % STAGES.  Every buffer is filled up front;
+    // buffer kt % STAGES is refilled with stage kt + STAGES right after the
+    // barrier that follows the last read of stage kt.  The operands of
+    // k-group 1 of stage kt and of k-group 0 of stage kt + 1 are read from
+    // LDS while the MFMAs of the other register set run.
+#pragma unroll
+    for (int s = 0; s < C::STAGES; ++s)
+      if (s < nk) {
+        char *st = smem + s * C::STAGE;
+        opa.issue((int64_t)s * C::BK, st);
+        opb.issue((int64_t)s * C::BK, st + C::BM * C::ROW);
+      }
+    if (nk > 0) {
+      wait_stage<C>(nk - 1 < C::STAGES - 1 ? (int)(nk - 1) : C::STAGES - 1);
+      read_kgroup_dtl<C>(smem, wm, wn, 0, a0, b0);
+    }
+    int cur = 0;  // buffer of stage kt
+    for (int64_t kt = 0; kt + 1 < nk; ++kt) {
+      read_kgroup_dtl<C>(smem + cur * C::STAGE, wm, wn, 1, a1, b1);
+      mfma_block<C>(a0, b0, acc);
+      interleave_hint<C>();
+      const int64_t later = nk - 2 - kt;  // stages issued beyond kt + 1
+      wait_stage<C>(later < C::STAGES - 2 ? (int)later : C::STAGES - 2);
+      if (kt + C::STAGES < nk) {
+        char *re = smem + cur * C::STAGE;
+        opa.issue((kt + C::STAGES) * C::BK, re);
+        opb.issue((kt + C::STAGES) * C::BK, re + C::BM * C::ROW);
+      }
+      cur = cur + 1 == C::STAGES ? 0 : cur + 1;
+      read_kgroup_dtl<C>(smem + cur * C::STAGE, wm, wn, 0, a0, b0);
+      mfma_block<C>(a1, b1, acc);
+      interleave_hint<C>();
+    }
+    if (nk > 0) {  // last stage: no further copies to wait for
+      read_kgroup_dtl<C>(smem + cur * C::STAGE, wm, wn, 1, a1, b1);
+      mfma_block<C>(a0, b0, acc);
+      mfma_block<C>(a1, b1, acc);
+    }
+  } else {
+    for (int64_t kt = 0; kt < nk; ++kt) {
+      opa.copy_sync(kt * C::BK, m0, wave, smem);
+      opb.copy_sync(kt * C::BK, n0, wave, smem + C::BM * C::ROW);
+      __syncthreads();
+      read_kgroup_dtl<C>(smem, wm, wn, 0, a0, b0);
+      read_kgroup_dtl<C>(smem, wm, wn, 1, a1, b1);
+      mfma_block<C>(a0, b0, acc);
+      mfma_block<C>(a1, b1, acc);
+      __syncthreads();
+    }
+  }
+  __syncthreads();
+}
+
 // Full K loop for the block tile at (m0, n0).  `smem` holds C::LDS_BYTES.
+// With C::PF == 2, global loads run two K-stages ahead of the MFMAs in two
+// alternating register sets (while stage k is multiplied out of LDS, stage
+// k+1 sits in registers waiting for the other LDS buffer and stage k+2 is in
+// flight): a small wave tile's compute stage is too short to hide HBM/MALL
+// latency alone.  With C::PF == 1 one register set holds stage k+1 while
+// stage k is computed: large wave tiles (and a second wavefront per SIMD)
+// cover the latency, and a second set would not fit beside the accumulators.
 // Ends with a barrier, so the caller may reuse smem for its epilogue.
-template <class C, bool VK>
+template <class C, bool BUF>
 __device__ __forceinline__ void mainloop(const typename C::TI *A, int64_t lda,
                                          const typename C::TI *B, int64_t ldb,
                                          int64_t M, int64_t N, int64_t K,
                                          int64_t m0, int64_t n0, char *smem,
                                          floatx16 (&acc)[C::TM][C::TN]) {
+  if constexpr (C::DTL) {
+    mainloop_dtl<C, BUF>(A, lda, B, ldb, M, N, K, m0, n0, smem, acc);
+    return;
+  } else {
   const int w = threadIdx.x >> 6;
   const int wm = w / C::WN, wn = w % C::WN;
 #pragma unroll
@@ -168,19 +470,56 @@ __device__ __forceinline__ void mainloop(const typename C::TI *A, int64_t lda,
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
+  Operand<C, BUF> opa, opb;
+  opa.init(A, lda, M, K, m0);
+  opb.init(B, ldb, N, K, n0);
   const int64_t nk = (K + C::BK - 1) / C::BK;
-  u32x4 ra[C::AV], rb[C::BV];
-  load_stage<C, VK>(A, lda, M, B, ldb, N, K, m0, n0, 0, ra, rb);
-  store_stage<C>(smem, ra, rb);
-  __syncthreads();
-  for (int64_t kt = 0; kt < nk; ++kt) {
-    char *cur = smem + (kt & 1) * C::STAGE;
-    char *nxt = smem + ((kt + 1) & 1) * C::STAGE;
-    const bool more = kt + 1 < nk;
-    if (more) load_stage<C, VK>(A, lda, M, B, ldb, N, K, m0, n0, (kt + 1) * C::BK, ra, rb);
-    compute_stage<C>(cur, wm, wn, acc);
-    if (more) store_stage<C>(nxt, ra, rb);
+  char *const lds0 = smem;
+  char *const lds1 = smem + C::STAGE;
+  if constexpr (C::PF == 2) {
+    u32x4 ra0[C::AV], rb0[C::BV], ra1[C::AV], rb1[C::BV];
+    opa.load(0, ra0);
+    opb.load(0, rb0);
+    store_stage<C>(lds0, ra0, rb0);
+    if (nk > 1) { opa.load(C::BK, ra1); opb.load(C::BK, rb1); }
+    if (nk > 2) { opa.load(2 * C::BK, ra0); opb.load(2 * C::BK, rb0); }
     __syncthreads();
+    for (int64_t kt = 0; kt < nk; kt += 2) {
+      // even stage kt in lds0; stage kt+1 in (ra1, rb1); stage kt+2 in (ra0, rb0)
+      compute_stage<C>(lds0, wm, wn, acc);
+      if (kt + 1 < nk) {
+        store_stage<C>(lds1, ra1, rb1);
+        if (kt + 3 < nk) { opa.load((kt + 3) * C::BK, ra1); opb.load((kt + 3) * C::BK, rb1); }
+      }
+      __syncthreads();
+      if (kt + 1 >= nk) break;
+      // odd stage kt+1 in lds1; stage kt+2 in (ra0, rb0); stage kt+3 in (ra1, rb1)
+      compute_stage<C>(lds1, wm, wn, acc);
+      if (kt + 2 < nk) {
+        store_stage<C>(lds0, ra0, rb0);
+        if (kt + 4 < nk) { opa.load((kt + 4) * C::BK, ra0); opb.load((kt + 4) * C::BK, rb0); }
+      }
+      __syncthreads();
+    }
+  } else {
+    u32x4 ra[C::AV], rb[C::BV];
+    opa.load(0, ra);
+    opb.load(0, rb);
+    store_stage<C>(lds0, ra, rb);
+    if (nk > 1) { opa.load(C::BK, ra); opb.load(C::BK, rb); }
+    __syncthreads();
+    for (int64_t kt = 0; kt < nk; ++kt) {
+      // stage kt in LDS buffer kt&1; stage kt+1 in (ra, rb)
+      char *const cur = (kt & 1) ? lds1 : lds0;
+      char *const nxt = (kt & 1) ? lds0 : lds1;
+      compute_stage<C>(cur, wm, wn, acc);
+      if (kt + 1 < nk) {
+        store_stage<C>(nxt, ra, rb);
+        if (kt + 2 < nk) { opa.load((kt + 2) * C::BK, ra); opb.load((kt + 2) * C::BK, rb); }
+      }
+      __syncthreads();
+    }
+  }
   }
 }
 
