@@ -54,7 +54,7 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-extra", action="store_true", help="headline workload only")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baselines")
-    ap.add_argument("--only", choices=("swiglu", "ce", "stress"), default=None,
+    ap.add_argument("--only", choices=("swiglu", "ce", "stress", "traffic"), default=None,
                     help="run one secondary workload alone (for profiling) and print its "
                          "record instead of the headline line")
     ap.add_argument("--json-out", default=None, help="also write the JSON record here")
@@ -216,9 +216,9 @@ def per_launch_ms(launch, steps: int, reps: int = 20) -> float:
     return e0.elapsed_time(e1) / (steps * reps)
 
 
-def adaln_kernel_ms(inp, t, dh, dout, steps):
-    """Per-launch time of nf_adaln_fwd / nf_adaln_bwd / nf_adaln_bwd_reduce on
-    the step's own inputs."""
+def adaln_launchers(inp, t, dh, dout):
+    """Closures that launch nf_adaln_fwd / nf_adaln_bwd / nf_adaln_bwd_reduce
+    directly through the C ABI on the step's own inputs."""
     import torch
 
     from nuvla_forge_amd import _lib
@@ -253,12 +253,62 @@ def adaln_kernel_ms(inp, t, dh, dout, steps):
             dweight.data_ptr(), dscale.data_ptr(), dshift.data_ptr(), m, n, t, dc(gate), dc(w),
             dc(scale), dc(shift), _lib.stream_of(x)), "reduce")
 
+    assert b * t == m
+    return fwd, bwd, red
+
+
+def adaln_kernel_ms(inp, t, dh, dout, steps):
+    """Per-launch time of nf_adaln_fwd / nf_adaln_bwd / nf_adaln_bwd_reduce on
+    the step's own inputs."""
+    fwd, bwd, red = adaln_launchers(inp, t, dh, dout)
     fwd()
     bwd()
     _sync()
-    assert b * t == m
     return {"nf_adaln_fwd": per_launch_ms(fwd, steps), "nf_adaln_bwd": per_launch_ms(bwd, steps),
             "nf_adaln_bwd_reduce": per_launch_ms(red, steps)}
+
+
+TRAFFIC_FILE = "profiles/adaln_cfg2_pmc_traffic.json"
+
+
+def pmc_traffic(kernel):
+    """HBM bytes per launch of an adaLN kernel at cfg2, from the committed
+    summary of the two rocprofv3 PMC passes (FETCH_SIZE, WRITE_SIZE) over
+    `bench.py --only traffic`, each scaled by the counter's reading for a
+    plain copy of known size; None when the summary is absent."""
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), TRAFFIC_FILE)
+    try:
+        with open(path) as f:
+            return round(json.load(f)["kernels"][kernel]["traffic_bytes"])
+    except (OSError, KeyError, ValueError):
+        return None
+
+
+COPY_BYTES = 64 << 20  # the reference copy of the traffic run: 64 MiB read + 64 MiB written
+
+
+def bench_traffic(args, dev):
+    """Workload for the PMC runs (rocprofv3 --pmc FETCH_SIZE, then WRITE_SIZE):
+    a plain device copy of COPY_BYTES (torch's copy kernel), whose counters give
+    the scale between counter and bytes, then the three adaLN kernels at cfg2,
+    five launches each, eager."""
+    import torch
+
+    src = torch.randn(COPY_BYTES // 4, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(5):
+        dst.copy_(src)
+    _sync()
+    b, t, n = 8, 1024, 1024
+    inp, dh, dout = adaln_inputs(b, t, n, dev)
+    fwd, bwd, red = adaln_launchers(inp, t, dh, dout)
+    for f in (fwd, bwd, red):
+        for _ in range(5):
+            f()
+    _sync()
+    return {"copy_bytes_each_way": COPY_BYTES, "launches": 5,
+            "adaln_fwd_alg_bytes": (4 * b * t * n + 3 * b * n + n) * 2,
+            "adaln_bwd_alg_bytes": (6 * b * t * n + 2 * b * n + n) * 2}
 
 
 def bench_adaln(args, dev):
@@ -452,7 +502,8 @@ def main() -> int:
     dev = torch.device("cuda", 0)
     log(f"device: {torch.cuda.get_device_name(0)}  torch {torch.__version__}")
     if args.only:
-        fn = {"swiglu": bench_swiglu, "ce": bench_ce, "stress": bench_stress}[args.only]
+        fn = {"swiglu": bench_swiglu, "ce": bench_ce, "stress": bench_stress,
+              "traffic": bench_traffic}[args.only]
         print(json.dumps({"workload": args.only, **fn(args, dev)}), flush=True)
         return 0
 
@@ -515,7 +566,8 @@ def main() -> int:
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(ad["bwd_gbs"] / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": pmc_traffic("bwd"),
+            "traffic_source": TRAFFIC_FILE,
             "alg_bytes_per_launch": ad["bwd_alg_bytes"],
             "mean_launch_ms": round(bwd_ms, 5),
         },

@@ -51,7 +51,14 @@ __global__ __launch_bounds__(kRcThreads) void adaln_reduce_kernel(ReduceArgs p) 
   __shared__ float qbuf[kRcQ][kRcCols];
   const int c = threadIdx.x % kRcCols;
   const int q = threadIdx.x / kRcCols;
-  const int col = blockIdx.x * kRcCols + c;
+  // Workgroups are dealt to the 8 XCDs round-robin (block i -> XCD i % 8) and
+  // each XCD has its own L2.  Give every XCD a contiguous range of column
+  // slices, so the four 32-byte slices of a 128-byte line are read by one L2
+  // instead of four (bijection of [0, gridDim.x)).
+  const int nblk = gridDim.x, xcd = blockIdx.x % 8, loc = blockIdx.x / 8;
+  const int qx = nblk / 8, rx = nblk % 8;
+  const int slice = xcd * qx + (xcd < rx ? xcd : rx) + loc;
+  const int col = slice * kRcCols + c;
   const bool cv = col < p.N;
   const int64_t N = p.N;
   int per_round = kRcSlots / p.J;  // J <= 1024 by construction of the plan
@@ -67,6 +74,20 @@ __global__ __launch_bounds__(kRcThreads) void adaln_reduce_kernel(ReduceArgs p) 
       buf[0][s][c] = cv ? src[0] : 0.f;
       buf[1][s][c] = cv ? src[N] : 0.f;
       buf[2][s][c] = cv ? src[2 * N] : 0.f;
+    }
+    // the (sample, column) threads' weight and scale, loaded now so their
+    // latency overlaps the partial-row loads instead of following the sums
+    float wcol = 0.f, scol = 0.f;
+    if (q < nb && cv) {
+      float t8[8];
+      if (p.dscale) {
+        load8_dyn<false>(p.weight, p.dt_weight, col, 1, t8);
+        wcol = t8[0];
+      }
+      if (p.dweight) {
+        load8_dyn<false>(p.scale, p.dt_scale, (int64_t)(b0 + q) * p.ld_scale + col, 1, t8);
+        scol = t8[0];
+      }
     }
     __syncthreads();
     const int S = kRcQ / nb;  // splits per sample, >= 1
@@ -98,16 +119,8 @@ __global__ __launch_bounds__(kRcThreads) void adaln_reduce_kernel(ReduceArgs p) 
         const int64_t o = b * N + col;
         if (p.dgate) store_dyn(p.dgate, p.dt_gate, o, G);
         if (p.dshift) store_dyn(p.dshift, p.dt_shift, o, Sh);
-        if (p.dscale) {
-          float w[8];
-          load8_dyn<false>(p.weight, p.dt_weight, col, 1, w);
-          store_dyn(p.dscale, p.dt_scale, o, w[0] * A);
-        }
-        if (p.dweight) {
-          float sc[8];
-          load8_dyn<false>(p.scale, p.dt_scale, b * p.ld_scale + col, 1, sc);
-          qv = (1.f + sc[0]) * A;
-        }
+        if (p.dscale) store_dyn(p.dscale, p.dt_scale, o, wcol * A);
+        if (p.dweight) qv = (1.f + scol) * A;
       }
       qbuf[q][c] = qv;
     }
