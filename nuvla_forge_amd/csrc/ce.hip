@@ -4,17 +4,17 @@
 // Pipeline (all on the caller's stream, fixed reduction orders throughout):
 //   1. transpose  W [V, D] -> Wt [D, ldwt],  H [M, D] -> Ht [D, ldht]
 //      (zero-padded columns), so every GEMM below is K-contiguous (NT).
-//   2. ce_stats:  S = H W^T tile by tile; per (row, 128-column tile) the
-//      row max and sum of exp(S - max), plus S[m, t_m] for the target column.
+//   2. ce_stats:  S^T = W H^T tile by tile; per (vocabulary tile, token) the
+//      max and sum of exp(S - max), plus S[m, t_m] for the target column.
 //      S itself is never stored.
 //   3. ce_lse:    lse[m] = combine of the tile partials (fixed order);
 //                 loss_row[m] = lse - S[m, t_m] for valid rows.
 //   4. ce_loss:   one block: n_valid, loss = sum(loss_row) / max(n, 1),
 //                 inv = 1 / max(n, 1).
 //   5. per vocabulary chunk c of `vocab_chunk` columns:
-//      ce_prob:  recompute S_c = H W_c^T; P_c = inv * (softmax - onehot)
+//      ce_prob:  recompute S_c^T = W_c H^T; P_c = inv * (softmax - onehot)
 //                (0 for ignored rows) in the input type, written row-major
-//                [M, Vc] and transposed [Vc, M] (through an LDS tile);
+//                [M, Vc] and transposed [Vc, M];
 //      dW_c  = P_c^T H        (gemm_store, K = M)   -> dweight rows of c
 //      dH   += P_c   W_c      (gemm_store, K = Vc)  -> dhidden (chunk 0
 //                                                     writes, later add)
@@ -32,12 +32,13 @@ using gemm::floatx16;
 
 // bf16: 256x256 block tiles, 8 wavefronts of 128x64 (two per SIMD, so one
 // wavefront's LDS waits and epilogue overlap the other's MFMAs), operands
-// copied global -> LDS directly, four K-stages in flight; f32 (correctness
-// path): 128x128 tiles staged through registers.
+// copied global -> LDS directly in 64-wide K-stages, two stage buffers (one
+// barrier per 64 k: measured ~12% faster than 32-wide stages with four
+// buffers); f32 (correctness path): 128x128 tiles staged through registers.
 template <typename TI>
 struct MainCfgT;
 template <>
-struct MainCfgT<bf16> { using type = gemm::DCfg<256, 256, 2, 4, 4>; };
+struct MainCfgT<bf16> { using type = gemm::DCfg<256, 256, 2, 4, 2, 64>; };
 template <>
 struct MainCfgT<float> { using type = Cfg<float, 128, 128, 2, 2>; };
 template <typename TI>
@@ -57,9 +58,58 @@ __device__ __forceinline__ float log_f32(float x) {
 }
 
 // ---------------------------------------------------------------------------
+// Branch-free epilogue stores.  With SB, a store goes through a buffer
+// resource over the destination (which must be under 2 GiB); a masked
+// element gets an out-of-range offset and the buffer unit drops it, so no
+// lane diverges.  Without SB, plain stores under a per-element condition.
+// ---------------------------------------------------------------------------
+constexpr uint32_t kOobOffset = 0x80000000u;
+
+template <bool SB>
+struct OutBuf {
+  char *base;
+  __amdgpu_buffer_rsrc_t rsrc;
+  __device__ __forceinline__ void init(void *p, int64_t bytes) {
+    base = static_cast<char *>(p);
+    if constexpr (SB)
+      rsrc = __builtin_amdgcn_make_buffer_rsrc(p, (short)0, (int)bytes, 0x00020000);
+  }
+  __device__ __forceinline__ void st32(int64_t off, bool ok, float v) const {
+    if constexpr (SB)
+      __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), rsrc,
+                                            ok ? (uint32_t)off : kOobOffset, 0, 0);
+    else if (ok)
+      *reinterpret_cast<float *>(base + off) = v;
+  }
+  __device__ __forceinline__ float ld32(int64_t off, bool ok) const {
+    if constexpr (SB)
+      return __uint_as_float(
+          __builtin_amdgcn_raw_buffer_load_b32(rsrc, ok ? (uint32_t)off : kOobOffset, 0, 0));
+    else
+      return ok ? *reinterpret_cast<const float *>(base + off) : 0.f;
+  }
+  __device__ __forceinline__ void st16(int64_t off, bool ok, uint16_t v) const {
+    if constexpr (SB)
+      __builtin_amdgcn_raw_buffer_store_b16(v, rsrc, ok ? (uint32_t)off : kOobOffset, 0, 0);
+    else if (ok)
+      *reinterpret_cast<uint16_t *>(base + off) = v;
+  }
+  __device__ __forceinline__ void st64(int64_t off, bool ok, u32x2 v) const {
+    if constexpr (SB)
+      __builtin_amdgcn_raw_buffer_store_b64(v, rsrc, ok ? (uint32_t)off : kOobOffset, 0, 0);
+    else if (ok)
+      *reinterpret_cast<u32x2 *>(base + off) = v;
+  }
+};
+
+inline bool sb_ok(int64_t bytes) { return bytes < ((int64_t)1 << 31) - 64; }
+
+// ---------------------------------------------------------------------------
 // plain store epilogue, C[m, n] (+)= acc, for one or two independent GEMMs in
 // one launch (the dW and dH products of a vocabulary chunk: each alone is too
-// few 256x256 tiles to fill the chip, together they do)
+// few 256x256 tiles to fill the chip, together they do).  An accumulating job
+// loads its C tile into the accumulators before the K loop, so the load
+// latency overlaps the first operand copies and the epilogue only stores.
 // ---------------------------------------------------------------------------
 template <typename TI>
 struct GemmJob {
@@ -68,143 +118,177 @@ struct GemmJob {
   float *C;
   int64_t lda, ldb, ldc, M, N, K;
   int accumulate;
-  int tiles_m;  // tiles along M; tile t is (t % tiles_m, t / tiles_m)
+  int tiles_m;  // tiles along M
   int tiles;    // tiles of this job
 };
 
-template <class C, bool BUF>
+template <class C, bool BUF, bool SB>
 __global__ NF_GEMM_BOUNDS(C) void gemm_store_kernel(GemmJob<typename C::TI> j0,
-                                                           GemmJob<typename C::TI> j1) {
+                                                    GemmJob<typename C::TI> j1) {
   __shared__ __attribute__((aligned(16))) char smem[C::LDS_BYTES];
-  int t = blockIdx.x;
+  int t = gemm::xcd_order(blockIdx.x, j0.tiles + j1.tiles);
   const bool second = t >= j0.tiles;
   const GemmJob<typename C::TI> &j = second ? j1 : j0;
   if (second) t -= j0.tiles;
-  const int64_t m0 = (int64_t)(t % j.tiles_m) * C::BM;
-  const int64_t n0 = (int64_t)(t / j.tiles_m) * C::BN;
+  int tm, tn;
+  gemm::group_tile(t, j.tiles_m, j.tiles / j.tiles_m, gemm::kTileGroup, tm, tn);
+  const int64_t m0 = (int64_t)tm * C::BM;
+  const int64_t n0 = (int64_t)tn * C::BN;
   const int64_t M = j.M, N = j.N, ldc = j.ldc;
-  float *const Cout = j.C;
-  const int accumulate = j.accumulate;
-  floatx16 acc[C::TM][C::TN];
-  gemm::mainloop<C, BUF>(j.A, j.lda, j.B, j.ldb, M, N, j.K, m0, n0, smem, acc);
+  OutBuf<SB> out;
+  out.init(j.C, M * ldc * (int64_t)sizeof(float));
   const int w = threadIdx.x >> 6, wm = w / C::WN, wn = w % C::WN;
+  // element (i, jj, r) of this lane sits at byte offset base + i * 32 rows
+  // + 8 * (r / 4) + (r % 4) rows + jj * 32 columns
+  const int64_t row0 = m0 + gemm::acc_row<C>(wm, 0, 0);
+  const int64_t col0 = n0 + gemm::acc_col<C>(wn, 0);
+  floatx16 acc[C::TM][C::TN];
 #pragma unroll
   for (int i = 0; i < C::TM; ++i)
 #pragma unroll
-    for (int jj = 0; jj < C::TN; ++jj) {
-      const int64_t col = n0 + gemm::acc_col<C>(wn, jj);
+    for (int jj = 0; jj < C::TN; ++jj)
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const int64_t row = m0 + gemm::acc_row<C>(wm, i, r);
-        if (row < M && col < N) {
-          float *p = Cout + row * ldc + col;
-          *p = accumulate ? *p + acc[i][jj][r] : acc[i][jj][r];
-        }
+        const int dr = i * 32 + 8 * (r >> 2) + (r & 3);
+        const bool ok = row0 + dr < M && col0 + jj * 32 < N;
+        acc[i][jj][r] = j.accumulate ? out.ld32(((row0 + dr) * ldc + col0 + jj * 32) * 4, ok)
+                                     : 0.f;
       }
-      // one 32x32 tile at a time: the read-modify-write loads of the whole
-      // accumulator are not hoisted into (and spilled from) registers
-      __builtin_amdgcn_sched_barrier(0);
-    }
+  gemm::mainloop<C, BUF, false>(j.A, j.lda, j.B, j.ldb, M, N, j.K, m0, n0, smem, acc);
+#pragma unroll
+  for (int i = 0; i < C::TM; ++i)
+#pragma unroll
+    for (int jj = 0; jj < C::TN; ++jj)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int dr = i * 32 + 8 * (r >> 2) + (r & 3);
+        const bool ok = row0 + dr < M && col0 + jj * 32 < N;
+        out.st32(((row0 + dr) * ldc + col0 + jj * 32) * 4, ok, acc[i][jj][r]);
+      }
 }
 
 // ---------------------------------------------------------------------------
-// stats epilogue: per-row (max, sum exp) over this block's 128 columns
+// Logit statistics of one (vocabulary tile, token tile) block.  The product
+// is formed transposed, acc = W_tile H_tile^T (rows: vocabulary entries,
+// columns: tokens), so each lane holds 16 * TM logits of each of its TN
+// tokens and the per-token max / sum of exp are reductions in registers,
+// then one exchange between the two lane halves and a fixed-order combine
+// of the WM wavefronts that share the token (through LDS).  Writes
+// stats[vtile * M + token] = (max, sum exp(logit - max)) over the tile, and
+// tgt_logit[token] from the block holding the token's target column.
 // ---------------------------------------------------------------------------
+__device__ __forceinline__ float2 combine_stats(float2 a, float2 b) {
+  const float m = fmaxf(a.x, b.x);
+  if (m == -INFINITY) return make_float2(m, 0.f);
+  return make_float2(m, a.y * exp_f32(a.x - m) + b.y * exp_f32(b.x - m));
+}
+
 template <class C, bool BUF>
 __global__ NF_GEMM_BOUNDS(C) void ce_stats_kernel(
-    const typename C::TI *H, const typename C::TI *W, int64_t M, int64_t V,
-    int64_t D, const int64_t *targets, float2 *stats, float *tgt_logit,
-    int ntiles) {
+    const typename C::TI *W, const typename C::TI *H, int64_t V, int64_t M, int64_t D,
+    const int64_t *targets, float2 *stats, float *tgt_logit, int vtiles, int mtiles) {
+  // one LDS buffer only: a second __shared__ object makes the compiler wait
+  // for every direct-to-LDS copy in flight before each operand read of the
+  // K loop (it cannot tell the copies do not write that object); the
+  // per-wavefront partials reuse the operand stages after the K loop
   __shared__ __attribute__((aligned(16))) char smem[C::LDS_BYTES];
-  __shared__ int tgt_s[C::BM];
-  __shared__ float redm[C::BM][C::WN];
-  __shared__ float reds[C::BM][C::WN];
-  const int64_t m0 = (int64_t)blockIdx.x * C::BM;
-  const int64_t n0 = (int64_t)blockIdx.y * C::BN;
-  for (int t = threadIdx.x; t < C::BM; t += C::NT) {
-    int tc = -1;
-    if (m0 + t < M) {
-      const int64_t tg = targets[m0 + t];
-      if (tg >= n0 && tg < n0 + C::BN && tg < V) tc = (int)(tg - n0);
-    }
-    tgt_s[t] = tc;
-  }
+  static_assert(sizeof(float2) * C::WM * C::BN <= C::LDS_BYTES, "partials do not fit");
+  float2(*red)[C::BN] = reinterpret_cast<float2(*)[C::BN]>(smem);
+  int vt, mt;
+  gemm::group_tile(gemm::xcd_order(blockIdx.x, vtiles * mtiles), vtiles, mtiles,
+                   gemm::kTileGroup, vt, mt);
+  const int64_t v0 = (int64_t)vt * C::BM;
+  const int64_t m0 = (int64_t)mt * C::BN;
   floatx16 acc[C::TM][C::TN];
-  gemm::mainloop<C, BUF>(H, D, W, D, M, V, D, m0, n0, smem, acc);
+  gemm::mainloop<C, BUF>(W, D, H, D, V, M, D, v0, m0, smem, acc);
 
-  const int l = threadIdx.x & 63;
+  const int l = threadIdx.x & 63, half = l >> 5;
   const int w = threadIdx.x >> 6, wm = w / C::WN, wn = w % C::WN;
+  // vocabulary row of acc[i][*][r]: v0 + wm * WTM + 4 * half + i * 32 + 8 * (r / 4) + r % 4
+  const int64_t vrow0 = v0 + wm * C::WTM + 4 * half;
+  // offsets >= vlim are past the vocabulary (32-bit: the compares stay cheap)
+  const int vlim = (int)(V - vrow0 < C::WTM ? V - vrow0 : C::WTM);
 #pragma unroll
-  for (int i = 0; i < C::TM; ++i)
+  for (int j = 0; j < C::TN; ++j) {
+    const int tl = wn * C::WTN + j * 32 + (l & 31);
+    const int64_t tok = m0 + tl;
+    float mx = -INFINITY;
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      float mx = -INFINITY;
+    for (int i = 0; i < C::TM; ++i)
 #pragma unroll
-      for (int j = 0; j < C::TN; ++j)
-        if (n0 + gemm::acc_col<C>(wn, j) < V) mx = fmaxf(mx, acc[i][j][r]);
-      mx = half_wave_max(mx);
-      if ((l & 31) == 0) redm[gemm::acc_row<C>(wm, i, r)][wn] = mx;
-    }
-  __syncthreads();
-#pragma unroll
-  for (int i = 0; i < C::TM; ++i)
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int lr = gemm::acc_row<C>(wm, i, r);
-      float bm = redm[lr][0];
-#pragma unroll
-      for (int q = 1; q < C::WN; ++q) bm = fmaxf(bm, redm[lr][q]);
-      float s = 0.f;
-#pragma unroll
-      for (int j = 0; j < C::TN; ++j) {
-        const int lc = gemm::acc_col<C>(wn, j);
-        if (n0 + lc < V) s += exp_f32(acc[i][j][r] - bm);
-        if (lc == tgt_s[lr]) tgt_logit[m0 + lr] = acc[i][j][r];
+      for (int r = 0; r < 16; ++r) {
+        const int o = i * 32 + 8 * (r >> 2) + (r & 3);
+        mx = fmaxf(mx, o < vlim ? acc[i][j][r] : -INFINITY);
       }
-      s = half_wave_sum(s);
-      if ((l & 31) == 0) reds[lr][wn] = s;
-    }
-  __syncthreads();
-  for (int t = threadIdx.x; t < C::BM; t += C::NT) {
-    if (m0 + t >= M) continue;
-    // every wave's sum is taken relative to the same block-row max
-    float bm = redm[t][0], s = reds[t][0];
+    mx = fmaxf(mx, __shfl_xor(mx, 32));
+    float s = 0.f;
 #pragma unroll
-    for (int q = 1; q < C::WN; ++q) {
-      bm = fmaxf(bm, redm[t][q]);
-      s += reds[t][q];
+    for (int i = 0; i < C::TM; ++i)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int o = i * 32 + 8 * (r >> 2) + (r & 3);
+        const float e = exp_f32(acc[i][j][r] - mx);
+        s += o < vlim ? e : 0.f;
+      }
+    s += __shfl_xor(s, 32);
+    if (half == 0) red[wm][tl] = make_float2(mx, s);
+
+    // the target logit, from the one lane that holds it
+    if (tok < M) {
+      const int64_t loc64 = targets[tok] - (v0 + wm * C::WTM);
+      const int loc = (int)(loc64 >= 0 && loc64 < C::WTM ? loc64 : -1);
+      if (loc >= 0 && ((loc >> 2) & 1) == half) {
+        const int want = ((loc >> 5) << 4) | (((loc & 31) >> 3) << 2) | (loc & 3);
+        float z = 0.f;
+#pragma unroll
+        for (int i = 0; i < C::TM; ++i)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) z = (i * 16 + r == want) ? acc[i][j][r] : z;
+        tgt_logit[tok] = z;
+      }
     }
-    stats[(m0 + t) * ntiles + blockIdx.y] = make_float2(bm, s);
+  }
+  __syncthreads();
+  for (int t = threadIdx.x; t < C::BN; t += C::NT) {
+    const int64_t tok = m0 + t;
+    if (tok >= M) continue;
+    float2 a = red[0][t];
+#pragma unroll
+    for (int q = 1; q < C::WM; ++q) a = combine_stats(a, red[q][t]);
+    stats[(int64_t)vt * M + tok] = a;
   }
 }
 
 // ---------------------------------------------------------------------------
-// lse per row (one wavefront per row)
+// lse per token: a block takes 64 tokens; its 4 wavefronts each combine every
+// 4th vocabulary tile of the 64 tokens (consecutive tokens per lane, so the
+// loads are contiguous), then wavefront 0 combines the 4 parts in order.
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void ce_lse_kernel(
+constexpr int kLseRows = 64, kLseParts = 4;
+
+__global__ __launch_bounds__(kLseRows * kLseParts) void ce_lse_kernel(
     const float2 *__restrict__ stats, int ntiles, const float *tgt_logit,
     const int64_t *targets, int64_t M, int64_t V, int64_t ignore_index,
     float *lse, int *tcol, float *loss_row, int *flags) {
-  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-  const int l = threadIdx.x & 63;
-  if (row >= M) return;
-  const float2 *sr = stats + row * ntiles;
-  float mx = -INFINITY;
-  for (int t = l; t < ntiles; t += 64) mx = fmaxf(mx, sr[t].x);
-  mx = wave_max(mx);
-  float s = 0.f;
-  for (int t = l; t < ntiles; t += 64) s += sr[t].y * exp_f32(sr[t].x - mx);
-  s = wave_sum(s);
-  if (l == 0) {
-    const float ls = mx + log_f32(s);
-    const int64_t tg = targets[row];
-    const bool in_range = tg >= 0 && tg < V;
-    const bool valid = tg != ignore_index && in_range;
-    lse[row] = ls;
-    tcol[row] = valid ? (int)tg : -1;
-    loss_row[row] = valid ? ls - tgt_logit[row] : 0.f;
-    flags[row] = (valid ? 1 : 0) | ((tg != ignore_index && !in_range) ? 2 : 0);
-  }
+  __shared__ float2 part[kLseParts][kLseRows];
+  const int rl = threadIdx.x % kLseRows, q = threadIdx.x / kLseRows;
+  const int64_t row = (int64_t)blockIdx.x * kLseRows + rl;
+  float2 a = make_float2(-INFINITY, 0.f);
+  if (row < M)
+    for (int t = q; t < ntiles; t += kLseParts) a = combine_stats(a, stats[(int64_t)t * M + row]);
+  part[q][rl] = a;
+  __syncthreads();
+  if (q != 0 || row >= M) return;
+#pragma unroll
+  for (int k = 1; k < kLseParts; ++k) a = combine_stats(a, part[k][rl]);
+  const float ls = a.x + log_f32(a.y);
+  const int64_t tg = targets[row];
+  const bool in_range = tg >= 0 && tg < V;
+  const bool valid = tg != ignore_index && in_range;
+  lse[row] = ls;
+  tcol[row] = valid ? (int)tg : -1;
+  loss_row[row] = valid ? ls - tgt_logit[row] : 0.f;
+  flags[row] = (valid ? 1 : 0) | ((tg != ignore_index && !in_range) ? 2 : 0);
 }
 
 // ---------------------------------------------------------------------------
@@ -246,71 +330,78 @@ __global__ __launch_bounds__(kLossThreads) void ce_loss_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// probability epilogue: P = inv * (softmax - onehot) for one vocab chunk
+// probability epilogue: P = inv * (softmax - onehot) for one vocabulary
+// chunk, from the transposed product acc = Wc_tile H_tile^T (rows: chunk
+// columns, columns: tokens).  Each lane's TN tokens bring their lse, target
+// and scale in registers.  Writes P [M, ldp] (token rows; columns [Vc, kpad)
+// zero) with one 8-byte store per 4 consecutive chunk columns, and
+// PT [Vc, ldpt] (chunk-column rows; tokens [M, ldpt) zero) with 2-byte
+// stores that the 32 lanes of a half-wave make contiguous.
 // ---------------------------------------------------------------------------
-template <class C, bool BUF>
+template <class C, bool BUF, bool SB>
 __global__ NF_GEMM_BOUNDS(C) void ce_prob_kernel(
-    const typename C::TI *H, const typename C::TI *Wc, int64_t M, int64_t Vc,
-    int64_t D, int64_t vbase, const int *tcol, const float *lse,
-    const float *inv_ptr, typename C::TI *P, int64_t ldp, int64_t kpad,
-    typename C::TI *PT, int64_t ldpt) {
+    const typename C::TI *Wc, const typename C::TI *H, int64_t Vc, int64_t M, int64_t D,
+    int64_t vbase, const int *tcol, const float *lse, const float *inv_ptr,
+    typename C::TI *P, int64_t ldp, int64_t kpad, typename C::TI *PT, int64_t ldpt, int vtiles,
+    int mtiles) {
   using TI = typename C::TI;
-  constexpr int TP = C::BM + 16;  // transposed-tile pitch (elements)
-  constexpr int kTile = C::BN * TP * (int)sizeof(TI);
-  __shared__ __attribute__((aligned(16))) char smem[kTile > C::LDS_BYTES ? kTile : C::LDS_BYTES];
-  __shared__ int tc_s[C::BM];
-  __shared__ float lse_s[C::BM];
-  const int64_t m0 = (int64_t)blockIdx.x * C::BM;
-  const int64_t n0 = (int64_t)blockIdx.y * C::BN;
-  for (int t = threadIdx.x; t < C::BM; t += C::NT) {
-    const bool in = m0 + t < M;
-    tc_s[t] = in ? tcol[m0 + t] : -1;
-    lse_s[t] = in ? lse[m0 + t] : 0.f;
-  }
+  constexpr int ES = (int)sizeof(TI);
+  __shared__ __attribute__((aligned(16))) char smem[C::LDS_BYTES];
+  int vt, mt;
+  gemm::group_tile(gemm::xcd_order(blockIdx.x, vtiles * mtiles), vtiles, mtiles,
+                   gemm::kTileGroup, vt, mt);
+  const int64_t v0 = (int64_t)vt * C::BM;
+  const int64_t m0 = (int64_t)mt * C::BN;
   floatx16 acc[C::TM][C::TN];
-  gemm::mainloop<C, BUF>(H, D, Wc, D, M, Vc, D, m0, n0, smem, acc);
+  gemm::mainloop<C, BUF>(Wc, D, H, D, Vc, M, D, v0, m0, smem, acc);
   const float inv = *inv_ptr;
 
-  TI *tile = reinterpret_cast<TI *>(smem);  // [BN][TP]: tile[col][row]
+  const int l = threadIdx.x & 63, half = l >> 5;
   const int w = threadIdx.x >> 6, wm = w / C::WN, wn = w % C::WN;
+  const int64_t crow0 = v0 + wm * C::WTM + 4 * half;  // chunk column of (i = 0, r = 0)
+  OutBuf<SB> pout, ptout;
+  pout.init(P, M * ldp * ES);
+  ptout.init(PT, Vc * ldpt * ES);
 #pragma unroll
-  for (int i = 0; i < C::TM; ++i)
+  for (int j = 0; j < C::TN; ++j) {
+    const int64_t tok = m0 + wn * C::WTN + j * 32 + (l & 31);
+    const int tc = tok < M ? tcol[tok] : -1;
+    const float ls = tok < M ? lse[tok] : 0.f;
+    const float sc = tc >= 0 ? inv : 0.f;
+    const int64_t tloc = (int64_t)tc - vbase - crow0;  // target's offset from crow0
 #pragma unroll
-    for (int j = 0; j < C::TN; ++j) {
-      const int lc = gemm::acc_col<C>(wn, j);
-      const int64_t col = n0 + lc;
-      const int64_t gcol = vbase + col;
+    for (int i = 0; i < C::TM; ++i)
 #pragma unroll
-      for (int rg = 0; rg < 4; ++rg) {
-        const int lr0 = gemm::acc_row<C>(wm, i, rg * 4);  // rows lr0 .. lr0 + 3
-        TI pv[4];
+      for (int g = 0; g < 4; ++g) {
+        const int o = i * 32 + 8 * g;  // offset of r = 4g from crow0
+        float p[4];
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-          const int lr = lr0 + q;
-          const int tc = tc_s[lr];
-          float p = 0.f;
-          if (tc >= 0 && col < Vc) {
-            p = exp_f32(acc[i][j][rg * 4 + q] - lse_s[lr]);
-            if (gcol == tc) p -= 1.f;
-            p *= inv;
-          }
-          pv[q] = static_cast<TI>(p);
-          if (m0 + lr < M && col < kpad) P[(m0 + lr) * ldp + col] = pv[q];
+          const float e = exp_f32(acc[i][j][4 * g + q] - ls) - (tloc == o + q ? 1.f : 0.f);
+          p[q] = (sc != 0.f && crow0 + o + q < Vc) ? e * sc : 0.f;
         }
+        TI pv[4];
 #pragma unroll
-        for (int q = 0; q < 4; ++q) tile[lc * TP + lr0 + q] = pv[q];
+        for (int q = 0; q < 4; ++q) pv[q] = static_cast<TI>(p[q]);
+        const int64_t c = crow0 + o;
+        if constexpr (ES == 2) {
+          u32x2 packed;
+          __builtin_memcpy(&packed, pv, 8);
+          pout.st64((tok * ldp + c) * ES, tok < M && c < kpad, packed);
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            uint16_t bits;
+            __builtin_memcpy(&bits, &pv[q], 2);
+            ptout.st16(((c + q) * ldpt + tok) * ES, c + q < Vc && tok < ldpt, bits);
+          }
+        } else {
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            pout.st32((tok * ldp + c + q) * ES, tok < M && c + q < kpad, p[q]);
+            ptout.st32(((c + q) * ldpt + tok) * ES, c + q < Vc && tok < ldpt, p[q]);
+          }
+        }
       }
-    }
-  __syncthreads();
-  // P^T rows (vocabulary entries) of this tile: BM contiguous tokens each
-  constexpr int VPR = C::BM * sizeof(TI) / 16;  // 16-byte vectors per row
-  for (int v = threadIdx.x; v < C::BN * VPR; v += C::NT) {
-    const int c = v / VPR, seg = v % VPR;
-    const int64_t vr = n0 + c;                        // P^T row
-    const int64_t tok = m0 + seg * (16 / sizeof(TI)); // first token
-    if (vr < Vc && tok < ldpt)
-      *reinterpret_cast<u32x4 *>(PT + vr * ldpt + tok) =
-          *reinterpret_cast<const u32x4 *>(tile + c * TP + seg * (16 / sizeof(TI)));
   }
 }
 
@@ -376,13 +467,13 @@ inline Layout make_layout(int64_t M, int64_t D, int64_t V, int64_t vocab_chunk, 
   L.ldht = round_up(M, 8);
   L.vc = round_up(vocab_chunk < V ? vocab_chunk : V, 8);
   L.ldp = L.vc;
-  L.ntiles = (V + MainCfg<bf16>::BN - 1) / MainCfg<bf16>::BN;
-  if (es == 4) L.ntiles = (V + MainCfg<float>::BN - 1) / MainCfg<float>::BN;
+  L.ntiles = (V + MainCfg<bf16>::BM - 1) / MainCfg<bf16>::BM;  // vocabulary tiles
+  if (es == 4) L.ntiles = (V + MainCfg<float>::BM - 1) / MainCfg<float>::BM;
   size_t o = 0;
   auto take = [&](size_t bytes) { const size_t at = o; o = align256(o + bytes); return at; };
   L.off_wt = take((size_t)D * L.ldwt * es);
   L.off_ht = take((size_t)D * L.ldht * es);
-  L.off_stats = take((size_t)M * L.ntiles * sizeof(float2));
+  L.off_stats = take((size_t)L.ntiles * M * sizeof(float2));  // [ntiles][M]
   L.off_tgt = take((size_t)M * sizeof(float));
   L.off_lse = take((size_t)M * sizeof(float));
   L.off_tcol = take((size_t)M * sizeof(int));
@@ -421,10 +512,15 @@ int launch_gemm_store(const GemmJob<typename C::TI> &j0, const GemmJob<typename 
   if (total == 0) return NF_OK;
   if (total > 0x7fffffffLL) return set_error(NF_ERR_ARG, "gemm: too many tiles");
   const dim3 grid((unsigned)total);
-  if (job_buf_ok(j0) && job_buf_ok(j1))
-    gemm_store_kernel<C, true><<<grid, C::NT, 0, s>>>(j0, j1);
+  const bool sb = (j0.tiles == 0 || sb_ok(j0.M * j0.ldc * (int64_t)sizeof(float))) &&
+                  (j1.tiles == 0 || sb_ok(j1.M * j1.ldc * (int64_t)sizeof(float)));
+  const bool buf = job_buf_ok(j0) && job_buf_ok(j1);
+  if (buf && sb)
+    gemm_store_kernel<C, true, true><<<grid, C::NT, 0, s>>>(j0, j1);
+  else if (buf)
+    gemm_store_kernel<C, true, false><<<grid, C::NT, 0, s>>>(j0, j1);
   else
-    gemm_store_kernel<C, false><<<grid, C::NT, 0, s>>>(j0, j1);
+    gemm_store_kernel<C, false, false><<<grid, C::NT, 0, s>>>(j0, j1);
   return check_launch("gemm_store");
 }
 
@@ -459,16 +555,20 @@ int ce_run(const TI *H, const TI *W, const int64_t *targets, int64_t M, int64_t 
   if ((e = launch_transpose<U>(W, V, D, D, Wt, L.ldwt, s))) return e;
   if ((e = launch_transpose<U>(H, M, D, D, Ht, L.ldht, s))) return e;
 
+  // stats: blocks (vocabulary tile, token tile); the product is W H^T
   const bool vk = buf_ok<TI>(H, D, M, D) && buf_ok<TI>(W, D, V, D);
-  dim3 gs((unsigned)((M + C::BM - 1) / C::BM), (unsigned)L.ntiles);
+  const int mtiles = (int)((M + C::BN - 1) / C::BN);
+  const unsigned gs = (unsigned)(L.ntiles * mtiles);
   if (vk)
-    ce_stats_kernel<C, true><<<gs, C::NT, 0, s>>>(H, W, M, V, D, targets, stats, tgt, (int)L.ntiles);
+    ce_stats_kernel<C, true><<<gs, C::NT, 0, s>>>(W, H, V, M, D, targets, stats, tgt,
+                                                  (int)L.ntiles, mtiles);
   else
-    ce_stats_kernel<C, false><<<gs, C::NT, 0, s>>>(H, W, M, V, D, targets, stats, tgt, (int)L.ntiles);
+    ce_stats_kernel<C, false><<<gs, C::NT, 0, s>>>(W, H, V, M, D, targets, stats, tgt,
+                                                   (int)L.ntiles, mtiles);
   if ((e = check_launch("ce_stats"))) return e;
 
-  ce_lse_kernel<<<(unsigned)((M + 3) / 4), 256, 0, s>>>(stats, (int)L.ntiles, tgt, targets, M, V,
-                                                       ignore_index, lse, tcol, loss_row, flags);
+  ce_lse_kernel<<<(unsigned)((M + kLseRows - 1) / kLseRows), kLseRows * kLseParts, 0, s>>>(
+      stats, (int)L.ntiles, tgt, targets, M, V, ignore_index, lse, tcol, loss_row, flags);
   if ((e = check_launch("ce_lse"))) return e;
   ce_loss_kernel<<<1, kLossThreads, 0, s>>>(loss_row, flags, M, loss, inv, bad);
   if ((e = check_launch("ce_loss"))) return e;
@@ -477,13 +577,23 @@ int ce_run(const TI *H, const TI *W, const int64_t *targets, int64_t M, int64_t 
     const int64_t vc = (V - vb < L.vc) ? V - vb : L.vc;  // columns in this chunk
     const int64_t kpad = round_up(vc, 8);
     const TI *Wc = W + vb * D;
-    dim3 gp((unsigned)((M + C::BM - 1) / C::BM), (unsigned)((vc + C::BN - 1) / C::BN));
-    if (vk && buf_ok<TI>(Wc, D, vc, D))
-      ce_prob_kernel<C, true><<<gp, C::NT, 0, s>>>(H, Wc, M, vc, D, vb, tcol, lse, inv, P, L.ldp,
-                                                   kpad, PT, L.ldht);
+    // blocks (chunk-column tile, token tile); the product is W_c H^T
+    const int vtiles = (int)((vc + C::BM - 1) / C::BM);
+    const unsigned gp = (unsigned)(vtiles * mtiles);
+    const bool sb = sb_ok(M * L.ldp * (int64_t)sizeof(TI)) &&
+                    sb_ok(vc * L.ldht * (int64_t)sizeof(TI));
+    const bool vb_ok = vk && buf_ok<TI>(Wc, D, vc, D);
+    if (vb_ok && sb)
+      ce_prob_kernel<C, true, true><<<gp, C::NT, 0, s>>>(Wc, H, vc, M, D, vb, tcol, lse, inv, P,
+                                                         L.ldp, kpad, PT, L.ldht, vtiles, mtiles);
+    else if (vb_ok)
+      ce_prob_kernel<C, true, false><<<gp, C::NT, 0, s>>>(Wc, H, vc, M, D, vb, tcol, lse, inv, P,
+                                                          L.ldp, kpad, PT, L.ldht, vtiles,
+                                                          mtiles);
     else
-      ce_prob_kernel<C, false><<<gp, C::NT, 0, s>>>(H, Wc, M, vc, D, vb, tcol, lse, inv, P, L.ldp,
-                                                    kpad, PT, L.ldht);
+      ce_prob_kernel<C, false, false><<<gp, C::NT, 0, s>>>(Wc, H, vc, M, D, vb, tcol, lse, inv,
+                                                           P, L.ldp, kpad, PT, L.ldht, vtiles,
+                                                           mtiles);
     if ((e = check_launch("ce_prob"))) return e;
     // dW[vb:vb+vc, :] = P_c^T H   (K = tokens, zero-padded to ldht) and
     // dH += P_c W_c               (K = chunk columns, zero-padded to kpad)

@@ -15,12 +15,12 @@
 //    32 f32), loaded into registers and written to LDS with a 144-byte row
 //    pitch, which makes both the 16-byte row writes and the 16-byte MFMA
 //    operand reads (eight lanes, eight distinct rows) bank-conflict free.
-//  * DCfg (bf16): a K-stage is 64 bytes of every tile row (32 bf16), copied
-//    global -> LDS by the buffer unit (buffer_load_dwordx4 ... lds) with no
-//    register staging, four stages in flight.  One such load writes 1 KB
-//    contiguously (lane i at +16 i), i.e. 16 unpadded 64-byte rows; the
-//    16-byte vectors of row r are stored XOR-swizzled (slot = kvec ^
-//    ((r >> 2) & 3)), which keeps the MFMA operand reads conflict free.
+//  * DCfg (bf16): a K-stage is BK = 32 or 64 k of every tile row (64 or 128
+//    bytes), copied global -> LDS by the buffer unit (buffer_load_dwordx4 ...
+//    lds) with no register staging.  One such load writes 1 KB contiguously
+//    (lane i at +16 i), i.e. 16 or 8 unpadded rows; the 16-byte vectors of a
+//    row are stored XOR-swizzled by row (dtl_slot), which keeps the MFMA
+//    operand reads conflict free.
 #pragma once
 
 #include "nf_device.h"
@@ -65,8 +65,9 @@ struct Cfg {
   static_assert((BM * KV) % NT == 0 && (BN * KV) % NT == 0, "loader mismatch");
 };
 
-// Direct-to-LDS bf16 configuration (see the file comment).
-template <int BM_, int BN_, int WM_, int WN_, int STAGES_ = 4>
+// Direct-to-LDS bf16 configuration (see the file comment): BK k per stage
+// (32 or 64: LDS rows of 64 or 128 bytes), STAGES stage buffers.
+template <int BM_, int BN_, int WM_, int WN_, int STAGES_ = 2, int BK_ = 64>
 struct DCfg {
   using TI = bf16;
   static constexpr bool DTL = true;
@@ -76,15 +77,19 @@ struct DCfg {
   static constexpr int WTM = BM / WM, WTN = BN / WN;
   static constexpr int TM = WTM / 32, TN = WTN / 32;
   static constexpr int VE = 8;                    // bf16 per 16-byte vector
-  static constexpr int BK = 32;                   // k per stage: 64-byte LDS rows
-  static constexpr int ROW = 64;
+  static constexpr int BK = BK_;                  // k per stage
+  static constexpr int KVEC = BK / 8;             // 16-byte vectors per LDS row
+  static constexpr int ROW = BK * 2;              // LDS row, bytes
+  static constexpr int RPC = 64 / KVEC;           // rows per 1 KB direct copy
+  static constexpr int KG = BK / 16;              // MFMA k-groups per stage
   static constexpr int STAGE = (BM + BN) * ROW;
   static constexpr int LDS_BYTES = STAGES * STAGE;
-  static constexpr int ACW = BM / 16 / NW;        // 1 KB A chunks per wave per stage
-  static constexpr int BCW = BN / 16 / NW;        // 1 KB B chunks per wave per stage
+  static constexpr int ACW = BM / RPC / NW;       // 1 KB A copies per wave per stage
+  static constexpr int BCW = BN / RPC / NW;       // 1 KB B copies per wave per stage
   static constexpr int PF = 0;
+  static_assert(BK == 32 || BK == 64, "BK is 32 or 64");
   static_assert(BM % (WM * 32) == 0 && BN % (WN * 32) == 0, "tile/wave mismatch");
-  static_assert((BM / 16) % NW == 0 && (BN / 16) % NW == 0, "chunk/wave mismatch");
+  static_assert((BM / RPC) % NW == 0 && (BN / RPC) % NW == 0, "chunk/wave mismatch");
   static_assert(WTM % 16 == 0 && WTN % 16 == 0, "swizzle assumes 16-row alignment");
   static_assert(STAGES >= 2 && STAGES <= 5 && (STAGES - 1) * (ACW + BCW) <= 63,
                 "vmcnt range");
@@ -263,24 +268,39 @@ __device__ __forceinline__ void compute_stage(const char *stage, int wm, int wn,
 
 // ---- direct-to-LDS path (DCfg) ----------------------------------------------
 
-// Lane l of a 1 KB chunk load covers tile row (chunk * 16 + l / 4) and LDS
-// slot l % 4, which holds k-vector (l % 4) ^ ((l >> 4) & 3) of that row.
-__device__ __forceinline__ int dtl_row(int l) { return l >> 2; }
-__device__ __forceinline__ int dtl_kvec(int l) { return (l & 3) ^ ((l >> 4) & 3); }
+// A K-stage row of the tile holds KVEC = BK / 8 16-byte k-vectors; one 1 KB
+// direct copy covers RPC = 64 / KVEC consecutive rows, lane l writing LDS
+// slot (l % KVEC) of row (l / KVEC).  Slots are XOR-swizzled by row so the
+// 32 rows an MFMA operand read touches at one k-vector spread over all banks:
+//   KVEC 4 (64-byte rows):  slot = kvec ^ ((row >> 2) & 3)
+//   KVEC 8 (128-byte rows): slot = kvec ^ ((row >> 1) & 7)
+// (both maps are involutions, so the same formula gives kvec from slot).
+template <class C>
+__device__ __forceinline__ int dtl_slot(int row, int kv) {
+  if constexpr (C::KVEC == 4)
+    return kv ^ ((row >> 2) & 3);
+  else
+    return kv ^ ((row >> 1) & 7);
+}
 
 typedef __attribute__((address_space(3))) void *lds_ptr_t;
 
-// One operand (A or B) of the block tile: CW chunks per wavefront.
+// One operand (A or B) of the block tile: CW chunks per wavefront.  Chunk
+// g = wave * CW + c covers tile rows [g * RPC, g * RPC + RPC); the lane's
+// swizzled k-vector depends only on the parity of g (dtl_slot of row
+// g * RPC + l / KVEC), so two base offsets describe all chunks and a chunk's
+// offset is base[g & 1] + c * RPC rows.
 template <class C, int CW>
 struct DtlOperand {
   using TI = typename C::TI;
   const TI *base;
   int64_t ld, rows, K;
   __amdgpu_buffer_rsrc_t rsrc;
-  uint32_t off[CW];  // byte offset of this lane's vector at k = 0, or kOob
-  bool row_in[CW];
-  int lds_off[CW];   // chunk offset inside the operand's LDS region
-  int kvec;
+  uint32_t off_p[2];  // byte offset at k = 0 of chunk parity p (rows assumed in range)
+  int kvec_p[2];      // k-vector this lane copies for chunk parity p
+  int lrow;           // l / KVEC: the lane's row inside a chunk
+  int rows_left;      // rows from this wave's first chunk on that exist (clamped)
+  uint32_t cstride;   // bytes between the first rows of consecutive chunks
   static constexpr uint32_t kOob = 0x80000000u;
 
   __device__ __forceinline__ void init(const TI *p, int64_t ld_, int64_t rows_, int64_t K_,
@@ -290,25 +310,29 @@ struct DtlOperand {
                                              (int)(rows_ * ld_ * (int64_t)sizeof(TI)),
                                              0x00020000);
     const int l = threadIdx.x & 63;
-    kvec = dtl_kvec(l);
+    lrow = l / C::KVEC;
+    const int g0 = wave * CW;
+    const int64_t first = r0 + (int64_t)g0 * C::RPC;  // first row of chunk g0
+    const int64_t left = rows_ - first;
+    rows_left = (int)(left < 0 ? 0 : (left > CW * C::RPC ? CW * C::RPC : left));
+    cstride = (uint32_t)((int64_t)C::RPC * ld_ * (int64_t)sizeof(TI));
 #pragma unroll
-    for (int c = 0; c < CW; ++c) {
-      const int g = wave * CW + c;  // chunk index inside the tile
-      const int64_t row = r0 + g * 16 + dtl_row(l);
-      row_in[c] = row < rows_;
-      off[c] = row_in[c] ? (uint32_t)((row * ld_ + kvec * C::VE) * (int64_t)sizeof(TI)) : kOob;
-      lds_off[c] = g * 1024;
+    for (int q = 0; q < 2; ++q) {  // q: chunk g0 + q's parity
+      kvec_p[q] = dtl_slot<C>((g0 + q) * C::RPC + lrow, l % C::KVEC);
+      // chunk c's offset is off_p[c & 1] + c * cstride
+      off_p[q] = (uint32_t)(((first + lrow) * ld_ + kvec_p[q] * C::VE) * (int64_t)sizeof(TI));
     }
   }
   // copy the stage starting at k0 into `region` (this operand's part of a stage)
-  __device__ __forceinline__ void issue(int64_t k0, char *region) const {
-    const bool kin = k0 + kvec * C::VE < K;
+  __device__ __forceinline__ void issue(int64_t k0, char *region, int wave) const {
     const uint32_t kb = (uint32_t)(k0 * (int64_t)sizeof(TI));
+    const bool kin0 = k0 + kvec_p[0] * C::VE < K, kin1 = k0 + kvec_p[1] * C::VE < K;
 #pragma unroll
     for (int c = 0; c < CW; ++c) {
-      const uint32_t o = (kin && row_in[c]) ? off[c] + kb : kOob;
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (lds_ptr_t)(region + lds_off[c]), 16, o, 0,
-                                               0, 0);
+      const bool in = lrow + c * C::RPC < rows_left && ((c & 1) ? kin1 : kin0);
+      const uint32_t o = off_p[c & 1] + (uint32_t)c * cstride + kb;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          rsrc, (lds_ptr_t)(region + (wave * CW + c) * 1024), 16, in ? o : kOob, 0, 0, 0);
     }
   }
   // the same copy through registers and ds_write (any alignment, any K)
@@ -317,8 +341,8 @@ struct DtlOperand {
 #pragma unroll
     for (int c = 0; c < CW; ++c) {
       const int g = wave * CW + c;
-      const u32x4 v = load_vec<TI, false>(base, ld, r0 + g * 16 + dtl_row(l), rows,
-                                          k0 + kvec * C::VE, K);
+      const u32x4 v = load_vec<TI, false>(base, ld, r0 + g * C::RPC + lrow, rows,
+                                          k0 + kvec_p[c & 1] * C::VE, K);
       *reinterpret_cast<u32x4 *>(region + g * 1024 + l * 16) = v;
     }
   }
@@ -353,13 +377,14 @@ __device__ __forceinline__ void wait_stage(int n_after) {
   }
 }
 
-// Operands of one 16-wide k-group (0 or 1) of a stage, for this lane.
+// Operands of one 16-wide k-group of a stage, for this lane: k-vector
+// 2 * kg + (lane / 32) of rows (lane % 32) + 32 i.  Tile row offsets are
+// multiples of 16, so the swizzle only depends on lane % 32.
 template <class C>
 __device__ __forceinline__ void read_kgroup_dtl(const char *stage, int wm, int wn, int kg,
                                                 u32x4 (&a)[C::TM], u32x4 (&b)[C::TN]) {
   const int l = threadIdx.x & 63;
-  // slot of this lane's k-vector: kvec = 2 kg + l / 32, swizzled by row
-  const int sw = (((2 * kg + (l >> 5)) ^ ((l >> 2) & 3)) * 16);
+  const int sw = dtl_slot<C>(l & 31, 2 * kg + (l >> 5)) * 16;
   const char *as = stage + (wm * C::WTM + (l & 31)) * C::ROW + sw;
   const char *bs = stage + (C::BM + wn * C::WTN + (l & 31)) * C::ROW + sw;
 #pragma unroll
@@ -368,7 +393,7 @@ __device__ __forceinline__ void read_kgroup_dtl(const char *stage, int wm, int w
   for (int j = 0; j < C::TN; ++j) b[j] = *reinterpret_cast<const u32x4 *>(bs + j * 32 * C::ROW);
 }
 
-template <class C, bool BUF>
+template <class C, bool BUF, bool ZERO>
 __device__ __forceinline__ void mainloop_dtl(const bf16 *A, int64_t lda, const bf16 *B,
                                              int64_t ldb, int64_t M, int64_t N, int64_t K,
                                              int64_t m0, int64_t n0, char *smem,
@@ -376,12 +401,14 @@ __device__ __forceinline__ void mainloop_dtl(const bf16 *A, int64_t lda, const b
   const int w = threadIdx.x >> 6;
   const int wave = __builtin_amdgcn_readfirstlane(w);
   const int wm = w / C::WN, wn = w % C::WN;
+  if constexpr (ZERO) {
 #pragma unroll
-  for (int i = 0; i < C::TM; ++i)
+    for (int i = 0; i < C::TM; ++i)
 #pragma unroll
-    for (int j = 0; j < C::TN; ++j)
+      for (int j = 0; j < C::TN; ++j)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+        for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+  }
   DtlOperand<C, C::ACW> opa;
   DtlOperand<C, C::BCW> opb;
   opa.init(A, lda, M, K, m0, wave);
@@ -391,51 +418,63 @@ __device__ __forceinline__ void mainloop_dtl(const bf16 *A, int64_t lda, const b
   if constexpr (BUF) {
     // Stage kt lives in buffer kt % STAGES.  Every buffer is filled up front;
     // buffer kt % STAGES is refilled with stage kt + STAGES right after the
-    // barrier that follows the last read of stage kt.  The operands of
-    // k-group 1 of stage kt and of k-group 0 of stage kt + 1 are read from
-    // LDS while the MFMAs of the other register set run.
+    // barrier that follows the last read of stage kt.  The operands of the
+    // KG k-groups of a stage alternate between two register sets, each read
+    // from LDS while the MFMAs of the other run; the last k-group's MFMAs
+    // cover the wait for the next stage and the read of its k-group 0.
 #pragma unroll
     for (int s = 0; s < C::STAGES; ++s)
       if (s < nk) {
         char *st = smem + s * C::STAGE;
-        opa.issue((int64_t)s * C::BK, st);
-        opb.issue((int64_t)s * C::BK, st + C::BM * C::ROW);
+        opa.issue((int64_t)s * C::BK, st, wave);
+        opb.issue((int64_t)s * C::BK, st + C::BM * C::ROW, wave);
       }
     if (nk > 0) {
       wait_stage<C>(nk - 1 < C::STAGES - 1 ? (int)(nk - 1) : C::STAGES - 1);
       read_kgroup_dtl<C>(smem, wm, wn, 0, a0, b0);
     }
     int cur = 0;  // buffer of stage kt
-    for (int64_t kt = 0; kt + 1 < nk; ++kt) {
-      read_kgroup_dtl<C>(smem + cur * C::STAGE, wm, wn, 1, a1, b1);
-      mfma_block<C>(a0, b0, acc);
-      interleave_hint<C>();
-      const int64_t later = nk - 2 - kt;  // stages issued beyond kt + 1
-      wait_stage<C>(later < C::STAGES - 2 ? (int)later : C::STAGES - 2);
-      if (kt + C::STAGES < nk) {
-        char *re = smem + cur * C::STAGE;
-        opa.issue((kt + C::STAGES) * C::BK, re);
-        opb.issue((kt + C::STAGES) * C::BK, re + C::BM * C::ROW);
+    static_assert(C::KG % 2 == 0, "k-groups alternate register sets in pairs");
+    for (int64_t kt = 0; kt < nk; ++kt) {
+      const char *st = smem + cur * C::STAGE;
+#pragma unroll
+      for (int kg = 0; kg + 1 < C::KG; kg += 2) {
+        read_kgroup_dtl<C>(st, wm, wn, kg + 1, a1, b1);
+        mfma_block<C>(a0, b0, acc);
+        interleave_hint<C>();
+        if (kg + 2 < C::KG) {
+          read_kgroup_dtl<C>(st, wm, wn, kg + 2, a0, b0);
+          mfma_block<C>(a1, b1, acc);
+          interleave_hint<C>();
+        }
       }
-      cur = cur + 1 == C::STAGES ? 0 : cur + 1;
-      read_kgroup_dtl<C>(smem + cur * C::STAGE, wm, wn, 0, a0, b0);
+      // the last k-group (in a1, b1) covers the stage hand-over
+      if (kt + 1 < nk) {
+        const int64_t later = nk - 2 - kt;  // stages issued beyond kt + 1
+        wait_stage<C>(later < C::STAGES - 2 ? (int)later : C::STAGES - 2);
+        if (kt + C::STAGES < nk) {
+          char *re = smem + cur * C::STAGE;
+          opa.issue((kt + C::STAGES) * C::BK, re, wave);
+          opb.issue((kt + C::STAGES) * C::BK, re + C::BM * C::ROW, wave);
+        }
+        cur = cur + 1 == C::STAGES ? 0 : cur + 1;
+        read_kgroup_dtl<C>(smem + cur * C::STAGE, wm, wn, 0, a0, b0);
+      }
       mfma_block<C>(a1, b1, acc);
       interleave_hint<C>();
-    }
-    if (nk > 0) {  // last stage: no further copies to wait for
-      read_kgroup_dtl<C>(smem + cur * C::STAGE, wm, wn, 1, a1, b1);
-      mfma_block<C>(a0, b0, acc);
-      mfma_block<C>(a1, b1, acc);
     }
   } else {
     for (int64_t kt = 0; kt < nk; ++kt) {
       opa.copy_sync(kt * C::BK, m0, wave, smem);
       opb.copy_sync(kt * C::BK, n0, wave, smem + C::BM * C::ROW);
       __syncthreads();
-      read_kgroup_dtl<C>(smem, wm, wn, 0, a0, b0);
-      read_kgroup_dtl<C>(smem, wm, wn, 1, a1, b1);
-      mfma_block<C>(a0, b0, acc);
-      mfma_block<C>(a1, b1, acc);
+#pragma unroll
+      for (int kg = 0; kg < C::KG; kg += 2) {
+        read_kgroup_dtl<C>(smem, wm, wn, kg, a0, b0);
+        read_kgroup_dtl<C>(smem, wm, wn, kg + 1, a1, b1);
+        mfma_block<C>(a0, b0, acc);
+        mfma_block<C>(a1, b1, acc);
+      }
       __syncthreads();
     }
   }
@@ -451,24 +490,27 @@ __device__ __forceinline__ void mainloop_dtl(const bf16 *A, int64_t lda, const b
 // stage k is computed: large wave tiles (and a second wavefront per SIMD)
 // cover the latency, and a second set would not fit beside the accumulators.
 // Ends with a barrier, so the caller may reuse smem for its epilogue.
-template <class C, bool BUF>
+// ZERO: start from acc = 0; otherwise the caller has loaded acc (C += A B^T).
+template <class C, bool BUF, bool ZERO = true>
 __device__ __forceinline__ void mainloop(const typename C::TI *A, int64_t lda,
                                          const typename C::TI *B, int64_t ldb,
                                          int64_t M, int64_t N, int64_t K,
                                          int64_t m0, int64_t n0, char *smem,
                                          floatx16 (&acc)[C::TM][C::TN]) {
   if constexpr (C::DTL) {
-    mainloop_dtl<C, BUF>(A, lda, B, ldb, M, N, K, m0, n0, smem, acc);
+    mainloop_dtl<C, BUF, ZERO>(A, lda, B, ldb, M, N, K, m0, n0, smem, acc);
     return;
   } else {
   const int w = threadIdx.x >> 6;
   const int wm = w / C::WN, wn = w % C::WN;
+  if constexpr (ZERO) {
 #pragma unroll
-  for (int i = 0; i < C::TM; ++i)
+    for (int i = 0; i < C::TM; ++i)
 #pragma unroll
-    for (int j = 0; j < C::TN; ++j)
+      for (int j = 0; j < C::TN; ++j)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+        for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+  }
 
   Operand<C, BUF> opa, opb;
   opa.init(A, lda, M, K, m0);
@@ -522,6 +564,32 @@ __device__ __forceinline__ void mainloop(const typename C::TI *A, int64_t lda,
   }
   }
 }
+
+// Output tile of a one-dimensional grid's block b, for `total` = tiles_m *
+// tiles_n tiles.  Workgroups are dealt to the 8 XCDs round-robin (block b to
+// XCD b % 8) and each XCD has its own L2, so XCD x is given a contiguous
+// range of a grouped tile order (a bijection of [0, total)): the order walks
+// groups of G tile rows, row-fastest inside a group (group_tile), so the
+// ~32 blocks an XCD runs at once cover a G x (32 / G) rectangle and share
+// its A and B K-slices in that L2.  xcd_order gives block b's position in
+// that order.
+constexpr int kXcds = 8;
+__device__ __forceinline__ int xcd_order(int b, int total) {
+  const int q = total / kXcds, r = total % kXcds;
+  const int x = b % kXcds, loc = b / kXcds;
+  return x * q + (x < r ? x : r) + loc;
+}
+// Tile (tm, tn) at position k of the grouped order over tiles_m x tiles_n.
+__device__ __forceinline__ void group_tile(int k, int tiles_m, int tiles_n, int G, int &tm,
+                                           int &tn) {
+  const int per_group = G * tiles_n;
+  const int grp = k / per_group, in = k % per_group;
+  const int first = grp * G;
+  const int rows = tiles_m - first < G ? tiles_m - first : G;
+  tm = first + in % rows;
+  tn = in / rows;
+}
+constexpr int kTileGroup = 4;
 
 // Position of accumulator element (i, j, r) of this lane inside the block
 // tile: local row and local column.
