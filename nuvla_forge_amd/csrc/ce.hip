@@ -428,6 +428,43 @@ __global__ __launch_bounds__(256) void transpose_pad_kernel(
   }
 }
 
+// 16-bit elements, 16-byte accesses: a 64 x 64 tile is read as 8-element row
+// vectors and written as 8-element column vectors through LDS.  Requires
+// Cn, ldi, ldo multiples of 8 and 16-byte aligned bases (a vector is then
+// wholly inside or outside the matrix).
+constexpr int kTpPitch = 66;  // LDS row pitch in elements (spreads column reads over banks)
+
+__global__ __launch_bounds__(256) void transpose16_kernel(
+    const uint16_t *__restrict__ in, int64_t R, int64_t Cn, int64_t ldi,
+    uint16_t *__restrict__ out, int64_t ldo) {
+  __shared__ uint16_t tile[64 * kTpPitch];
+  const int t = threadIdx.x;
+  const int64_t r0 = (int64_t)blockIdx.x * 64, c0 = (int64_t)blockIdx.y * 64;
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int row = t / 8 + 32 * i, vec = t % 8;
+    const int64_t r = r0 + row, c = c0 + 8 * vec;
+    u32x4 v = {0u, 0u, 0u, 0u};
+    if (r < R && c < Cn) v = *reinterpret_cast<const u32x4 *>(in + r * ldi + c);
+    uint16_t e[8];
+    __builtin_memcpy(e, &v, 16);
+#pragma unroll
+    for (int q = 0; q < 8; ++q) tile[row * kTpPitch + 8 * vec + q] = e[q];
+  }
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int oc = t / 8 + 32 * i, seg = t % 8;
+    const int64_t c = c0 + oc, r = r0 + 8 * seg;
+    uint16_t e[8];
+#pragma unroll
+    for (int q = 0; q < 8; ++q) e[q] = tile[(8 * seg + q) * kTpPitch + oc];
+    u32x4 v;
+    __builtin_memcpy(&v, e, 16);
+    if (c < Cn && r < ldo) *reinterpret_cast<u32x4 *>(out + c * ldo + r) = v;
+  }
+}
+
 // ---------------------------------------------------------------------------
 // backward scale + cast
 // ---------------------------------------------------------------------------
@@ -528,7 +565,12 @@ template <typename T>
 int launch_transpose(const void *in, int64_t R, int64_t Cn, int64_t ldi, void *out,
                      int64_t ldo, hipStream_t s) {
   dim3 grid((unsigned)((ldo + 63) / 64), (unsigned)((Cn + 63) / 64));
-  transpose_pad_kernel<T><<<grid, 256, 0, s>>>((const T *)in, R, Cn, ldi, (T *)out, ldo);
+  if (sizeof(T) == 2 && Cn % 8 == 0 && ldi % 8 == 0 && ldo % 8 == 0 && aligned16(in) &&
+      aligned16(out))
+    transpose16_kernel<<<grid, 256, 0, s>>>((const uint16_t *)in, R, Cn, ldi, (uint16_t *)out,
+                                            ldo);
+  else
+    transpose_pad_kernel<T><<<grid, 256, 0, s>>>((const T *)in, R, Cn, ldi, (T *)out, ldo);
   return check_launch("transpose");
 }
 
