@@ -26,7 +26,10 @@ Timing:
     forward + autograd backward) on the host cores for the same workload.
   * extra: SwiGLU bf16 [8192, 4096], chunked CE bf16 M4096 D2048
     V32000 with 409 ignored rows (configs[3], tokens/s and MFMA fraction of
-    2.5 PFLOP/s on 6*M_valid*V*D), the cfg5 stress chain, their CPU baselines.
+    2.5 PFLOP/s on 6*M_valid*V*D), the cfg5 stress chain, their CPU baselines;
+    the two callers at the reference's model shape: the DiT seam (B8 T6 N384,
+    autocast dtypes, chunk(6) views) and the reasoning-head CE (M512 D384
+    V32000, bf16 hidden, fp32 lm_head), each beside its eager formulation.
 """
 
 from __future__ import annotations
@@ -54,7 +57,8 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-extra", action="store_true", help="headline workload only")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baselines")
-    ap.add_argument("--only", choices=("swiglu", "ce", "stress", "traffic"), default=None,
+    ap.add_argument("--only", choices=("swiglu", "ce", "stress", "traffic", "dit", "head"),
+                    default=None,
                     help="run one secondary workload alone (for profiling) and print its "
                          "record instead of the headline line")
     ap.add_argument("--json-out", default=None, help="also write the JSON record here")
@@ -444,6 +448,77 @@ def bench_stress(args, dev):
             "hbm_frac": alg / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS}
 
 
+def bench_dit_seam(args, dev, b=8, t=6, n=384):
+    """The adaLN seam at the reference's DiT shape (model/dit.py:144-175,
+    NuVLAConfig: width 384, horizon 6, batch 8) with the autocast mix the
+    block passes: fp32 residual x, bf16 branch output y, bf16 conditioning as
+    chunk(6) views of one [B, 6N] projection, fp32 norm weight.  Launch-bound:
+    reported as microseconds per fwd+bwd, fused vs the eager formulation."""
+    import torch
+
+    from nuvla_forge_amd.kernels import fused_adaln_residual_rmsnorm
+
+    g = torch.Generator().manual_seed(40)
+    x = torch.randn(b * t, n, generator=g).to(dev)
+    y = torch.randn(b * t, n, generator=g).to(torch.bfloat16).to(dev)
+    cond = (torch.randn(b, 6 * n, generator=g) * 0.1).to(torch.bfloat16).to(dev)
+    w = (1 + 0.02 * torch.randn(n, generator=g)).to(dev)
+    dh = torch.randn(b * t, n, generator=g).to(dev)
+    dout = torch.randn(b * t, n, generator=g).to(dev)
+
+    def make(force):
+        leaves = [x.detach().requires_grad_(True), y.detach().requires_grad_(True),
+                  cond.detach().requires_grad_(True), w.detach().requires_grad_(True)]
+
+        def step():
+            lx, ly, lc, lw = leaves
+            _, scale, gate, _, _, shift = lc.chunk(6, dim=-1)
+            h, out = fused_adaln_residual_rmsnorm(lx, ly, gate, lw, scale, shift,
+                                                  tokens_per_sample=t, force_reference=force)
+            return (h, out, *torch.autograd.grad([h, out], leaves, [dh, dout]))
+
+        return step
+
+    fused_ms, _, _ = time_graph(lambda: make(False), args.steps, args.warmup)
+    eager_ms, _, _ = time_graph(lambda: make(True), args.steps, args.warmup)
+    return {"b": b, "t": t, "n": n, "fused_us": fused_ms * 1e3, "eager_us": eager_ms * 1e3,
+            "speedup": eager_ms / fused_ms}
+
+
+def bench_ce_reasoning_head(args, dev, m=512, d=384, v=32000):
+    """The reasoning head at the reference's model shape (model/nuvla.py:150-164:
+    batch 8 x 64 text tokens, width 384, vocabulary 32000, chunk_size 1024):
+    bf16 hidden, fp32 lm_head, under bf16 autocast; fused vs the reference's
+    eager chunk loop, tokens/s of forward + backward."""
+    import torch
+
+    from nuvla_forge_amd.kernels import chunked_cross_entropy
+
+    g = torch.Generator().manual_seed(41)
+    hid = torch.randn(m, d, generator=g).to(torch.bfloat16).to(dev)
+    w = (torch.randn(v, d, generator=g) * 0.02).to(dev)
+    tgt = torch.randint(0, v, (m,), generator=g)
+    tgt[::7] = -100
+    tgt = tgt.to(dev)
+
+    def make(force):
+        lh, lw = hid.detach().requires_grad_(True), w.detach().requires_grad_(True)
+
+        def step():
+            with torch.autocast("cuda", dtype=torch.bfloat16):
+                loss = chunked_cross_entropy(lh, lw, tgt, chunk_size=1024, force_reference=force)
+            return (loss, *torch.autograd.grad(loss, [lh, lw]))
+
+        return step
+
+    steps, warm = max(5, args.steps // 5), max(2, args.warmup // 5)
+    fused_ms, _, _ = time_graph(lambda: make(False), steps, warm)
+    eager_ms = time_eager(make(True), steps, warm)  # the eager loop syncs on n_valid
+    return {"m": m, "d": d, "v": v, "fused_ms": fused_ms, "eager_ms": eager_ms,
+            "tokens_per_s": m / (fused_ms * 1e-3), "eager_tokens_per_s": m / (eager_ms * 1e-3),
+            "speedup": eager_ms / fused_ms}
+
+
 # ---------------------------------------------------------------------------
 # CPU baselines (the reference's eager PyTorch path, oracle/torch_cpu.py)
 # ---------------------------------------------------------------------------
@@ -503,7 +578,8 @@ def main() -> int:
     log(f"device: {torch.cuda.get_device_name(0)}  torch {torch.__version__}")
     if args.only:
         fn = {"swiglu": bench_swiglu, "ce": bench_ce, "stress": bench_stress,
-              "traffic": bench_traffic}[args.only]
+              "traffic": bench_traffic, "dit": bench_dit_seam,
+              "head": bench_ce_reasoning_head}[args.only]
         print(json.dumps({"workload": args.only, **fn(args, dev)}), flush=True)
         return 0
 
@@ -522,6 +598,12 @@ def main() -> int:
         log("stress chain cfg5 ...")
         extra["stress_cfg5"] = bench_stress(args, dev)
         log(f"  {extra['stress_cfg5']}")
+        log("DiT seam at model shape ...")
+        extra["dit_seam_model_shape"] = bench_dit_seam(args, dev)
+        log(f"  {extra['dit_seam_model_shape']}")
+        log("reasoning-head CE at model shape ...")
+        extra["ce_reasoning_head"] = bench_ce_reasoning_head(args, dev)
+        log(f"  {extra['ce_reasoning_head']}")
 
     cpu = None
     if not args.no_cpu:

@@ -111,6 +111,9 @@ inline bool sb_ok(int64_t bytes) { return bytes < ((int64_t)1 << 31) - 64; }
 // loads its C tile into the accumulators before the K loop, so the load
 // latency overlaps the first operand copies and the epilogue only stores.
 // ---------------------------------------------------------------------------
+// A job with ksplit > 1 divides K into slices of kslice (a multiple of the
+// stage width): block (tile, s) writes the partial product over slice s to
+// part[s] ([M, N], dense) and splitk_reduce_kernel adds the slices in order.
 template <typename TI>
 struct GemmJob {
   const TI *A;
@@ -118,8 +121,11 @@ struct GemmJob {
   float *C;
   int64_t lda, ldb, ldc, M, N, K;
   int accumulate;
-  int tiles_m;  // tiles along M
-  int tiles;    // tiles of this job
+  int tiles_m;   // tiles along M
+  int tiles;     // blocks of this job: tiles_m * tiles_n * ksplit
+  int ksplit;    // K slices (1: no split)
+  int64_t kslice;
+  float *part;   // [ksplit, M, N] partial products when ksplit > 1
 };
 
 template <class C, bool BUF, bool SB>
@@ -130,13 +136,20 @@ __global__ NF_GEMM_BOUNDS(C) void gemm_store_kernel(GemmJob<typename C::TI> j0,
   const bool second = t >= j0.tiles;
   const GemmJob<typename C::TI> &j = second ? j1 : j0;
   if (second) t -= j0.tiles;
+  const int per_split = j.tiles / j.ksplit;
+  const int ks = t / per_split;  // K slice of this block
   int tm, tn;
-  gemm::group_tile(t, j.tiles_m, j.tiles / j.tiles_m, gemm::kTileGroup, tm, tn);
+  gemm::group_tile(t % per_split, j.tiles_m, per_split / j.tiles_m, gemm::kTileGroup, tm, tn);
   const int64_t m0 = (int64_t)tm * C::BM;
   const int64_t n0 = (int64_t)tn * C::BN;
-  const int64_t M = j.M, N = j.N, ldc = j.ldc;
+  const int64_t M = j.M, N = j.N;
+  const bool split = j.ksplit > 1;
+  const int64_t k0 = ks * j.kslice;
+  const int64_t klen = j.K - k0 < j.kslice ? j.K - k0 : j.kslice;
+  const int64_t ldc = split ? N : j.ldc;
+  const int accumulate = split ? 0 : j.accumulate;
   OutBuf<SB> out;
-  out.init(j.C, M * ldc * (int64_t)sizeof(float));
+  out.init(split ? j.part + ks * M * N : j.C, M * ldc * (int64_t)sizeof(float));
   const int w = threadIdx.x >> 6, wm = w / C::WN, wn = w % C::WN;
   // element (i, jj, r) of this lane sits at byte offset base + i * 32 rows
   // + 8 * (r / 4) + (r % 4) rows + jj * 32 columns
@@ -151,10 +164,10 @@ __global__ NF_GEMM_BOUNDS(C) void gemm_store_kernel(GemmJob<typename C::TI> j0,
       for (int r = 0; r < 16; ++r) {
         const int dr = i * 32 + 8 * (r >> 2) + (r & 3);
         const bool ok = row0 + dr < M && col0 + jj * 32 < N;
-        acc[i][jj][r] = j.accumulate ? out.ld32(((row0 + dr) * ldc + col0 + jj * 32) * 4, ok)
-                                     : 0.f;
+        acc[i][jj][r] = accumulate ? out.ld32(((row0 + dr) * ldc + col0 + jj * 32) * 4, ok)
+                                   : 0.f;
       }
-  gemm::mainloop<C, BUF, false>(j.A, j.lda, j.B, j.ldb, M, N, j.K, m0, n0, smem, acc);
+  gemm::mainloop<C, BUF, false>(j.A + k0, j.lda, j.B + k0, j.ldb, M, N, klen, m0, n0, smem, acc);
 #pragma unroll
   for (int i = 0; i < C::TM; ++i)
 #pragma unroll
@@ -165,6 +178,21 @@ __global__ NF_GEMM_BOUNDS(C) void gemm_store_kernel(GemmJob<typename C::TI> j0,
         const bool ok = row0 + dr < M && col0 + jj * 32 < N;
         out.st32(((row0 + dr) * ldc + col0 + jj * 32) * 4, ok, acc[i][jj][r]);
       }
+}
+
+// C[m, n] (+)= sum over s = 0 .. S-1 of part[s, m, n], in that order.
+__global__ __launch_bounds__(256) void splitk_reduce_kernel(const float *__restrict__ part,
+                                                            int S, int64_t M, int64_t N,
+                                                            float *C, int64_t ldc,
+                                                            int accumulate) {
+  const int64_t total = M * N;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total;
+       i += (int64_t)gridDim.x * 256) {
+    float a = 0.f;
+    for (int k = 0; k < S; ++k) a += part[k * total + i];
+    float *p = C + (i / N) * ldc + i % N;
+    *p = accumulate ? *p + a : a;
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -492,11 +520,50 @@ __global__ __launch_bounds__(256) void scale_cast_kernel(
 inline int64_t round_up(int64_t x, int64_t m) { return (x + m - 1) / m * m; }
 inline size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
+// K split of a vocabulary chunk's dH product.  The chunk's dW blocks (K =
+// tokens) and dH blocks (K = chunk columns) run in one launch; when that
+// launch is one partial wave and the dH blocks are the longer ones (few
+// tokens, a long chunk: the reasoning head's M 512 x D 384 with the whole
+// vocabulary in one chunk has 4 dH tiles of K 32000 beside 250 dW tiles of
+// K 512), dH is split along K into slices about as long as a dW block's K
+// (at least 512), keeping the launch within ~512 blocks.
+struct Split {
+  int S;
+  int64_t kslice;
+};
+template <class C>
+inline Split dh_split(int64_t vc, int64_t M, int64_t D) {
+  const int64_t tn = (D + C::BN - 1) / C::BN;
+  const int64_t tw = (vc + C::BM - 1) / C::BM * tn, th = (M + C::BM - 1) / C::BM * tn;
+  const int64_t K = round_up(vc, 8), kw = round_up(M, 8);
+  int64_t S = 1;
+  if (tw + th < 256) {
+    const int64_t balance = (K + (kw > 512 ? kw : 512) - 1) / (kw > 512 ? kw : 512);
+    const int64_t fill = (512 - tw) / th;
+    S = balance < fill ? balance : fill;
+    if (S > 64) S = 64;
+    if (S < 1) S = 1;
+  }
+  const int64_t kslice = round_up((K + S - 1) / S, C::BK);
+  return {(int)((K + kslice - 1) / kslice), kslice};
+}
+
 struct Layout {
   int64_t ldwt, ldht, vc, ldp, ntiles;
   size_t off_wt, off_ht, off_stats, off_tgt, off_lse, off_tcol, off_loss, off_flags,
-      off_scal, off_p, off_pt, total;
+      off_scal, off_p, off_pt, off_part, total;
 };
+
+template <class C>
+inline size_t partial_bytes(int64_t M, int64_t D, int64_t V, int64_t vc) {
+  size_t most = 0;
+  for (int64_t vb = 0; vb < V; vb += vc) {
+    const Split sp = dh_split<C>(V - vb < vc ? V - vb : vc, M, D);
+    const size_t b = sp.S > 1 ? (size_t)sp.S * M * D * sizeof(float) : 0;
+    if (b > most) most = b;
+  }
+  return most;
+}
 
 inline Layout make_layout(int64_t M, int64_t D, int64_t V, int64_t vocab_chunk, int es) {
   Layout L{};
@@ -506,6 +573,8 @@ inline Layout make_layout(int64_t M, int64_t D, int64_t V, int64_t vocab_chunk, 
   L.ldp = L.vc;
   L.ntiles = (V + MainCfg<bf16>::BM - 1) / MainCfg<bf16>::BM;  // vocabulary tiles
   if (es == 4) L.ntiles = (V + MainCfg<float>::BM - 1) / MainCfg<float>::BM;
+  const size_t part = es == 2 ? partial_bytes<MainCfg<bf16>>(M, D, V, L.vc)
+                              : partial_bytes<MainCfg<float>>(M, D, V, L.vc);
   size_t o = 0;
   auto take = [&](size_t bytes) { const size_t at = o; o = align256(o + bytes); return at; };
   L.off_wt = take((size_t)D * L.ldwt * es);
@@ -519,6 +588,7 @@ inline Layout make_layout(int64_t M, int64_t D, int64_t V, int64_t vocab_chunk, 
   L.off_scal = take(64);
   L.off_p = take((size_t)M * L.ldp * es);
   L.off_pt = take((size_t)L.vc * L.ldht * es);
+  L.off_part = take(part);
   L.total = o;
   return L;
 }
@@ -533,6 +603,9 @@ GemmJob<typename C::TI> make_job(const typename C::TI *A, int64_t lda, const typ
   j.accumulate = accumulate;
   j.tiles_m = (int)((M + C::BM - 1) / C::BM);
   j.tiles = j.tiles_m * (int)((N + C::BN - 1) / C::BN);
+  j.ksplit = 1;
+  j.kslice = K;
+  j.part = nullptr;
   return j;
 }
 
@@ -640,8 +713,22 @@ int ce_run(const TI *H, const TI *W, const int64_t *targets, int64_t M, int64_t 
     // dW[vb:vb+vc, :] = P_c^T H   (K = tokens, zero-padded to ldht) and
     // dH += P_c W_c               (K = chunk columns, zero-padded to kpad)
     const auto jw = make_job<C>(PT, L.ldht, Ht, L.ldht, dW + vb * D, D, vc, D, L.ldht, 0);
-    const auto jh = make_job<C>(P, L.ldp, Wt + vb, L.ldwt, dH, D, M, D, kpad, vb > 0 ? 1 : 0);
+    auto jh = make_job<C>(P, L.ldp, Wt + vb, L.ldwt, dH, D, M, D, kpad, vb > 0 ? 1 : 0);
+    const Split sp = dh_split<C>(vc, M, D);
+    if (sp.S > 1) {
+      jh.ksplit = sp.S;
+      jh.kslice = sp.kslice;
+      jh.part = reinterpret_cast<float *>(ws + L.off_part);
+      jh.tiles *= sp.S;
+    }
     if ((e = launch_gemm_store<C>(jw, jh, s))) return e;
+    if (sp.S > 1) {
+      int64_t blocks = (M * D + 255) / 256;
+      if (blocks > 2048) blocks = 2048;
+      splitk_reduce_kernel<<<(unsigned)blocks, 256, 0, s>>>(jh.part, sp.S, M, D, dH, D,
+                                                           jh.accumulate);
+      if ((e = check_launch("splitk_reduce"))) return e;
+    }
   }
   return NF_OK;
 }

@@ -158,3 +158,77 @@ def test_ce_cfg4_bf16_full_size_and_deterministic(cuda):
     assert on.rel_err(dh.float().cpu().numpy(), dho) < 2e-2
     assert on.rel_err(dw.float().cpu().numpy(), dwo) < 2e-2
     assert np.all(dh.float().cpu().numpy()[(tgt == -100).cpu().numpy()] == 0)
+
+
+def _reasoning_head_inputs(dev, seed=8):
+    """The reasoning head at the reference's model shape (model/nuvla.py:150-164,
+    NuVLAConfig :26-44): batch 8 x 64 text tokens = 512 rows, width 384,
+    vocabulary 32000; hidden states bf16 (autocast activations), lm_head an
+    fp32 Parameter, every 7th target ignored."""
+    g = gen(seed)
+    hid = randn((512, 384), g, torch.bfloat16, dev).requires_grad_(True)
+    lm_head = torch.nn.Parameter(randn((32000, 384), g, torch.float32, dev, std=0.02))
+    tgt = torch.randint(0, 32000, (512,), generator=g)
+    tgt[::7] = -100
+    return hid, lm_head, tgt.to(dev)
+
+
+def test_ce_reasoning_head_model_shape_under_autocast(cuda):
+    """bf16 hidden with an fp32 lm_head under bf16 autocast computes in bf16
+    (as the reference's autocast-ed F.linear does) and returns each gradient
+    in its input's dtype; parity against the fp64 oracle on the bf16-rounded
+    operands at the bf16 tolerance."""
+    note("ce reasoning head M512 D384 V32000 bf16/fp32 autocast")
+    hid, lm_head, tgt = _reasoning_head_inputs(cuda)
+    with torch.autocast("cuda", dtype=torch.bfloat16):
+        loss = chunked_cross_entropy(hid, lm_head, tgt, chunk_size=1024)
+    loss.backward()
+    torch.cuda.synchronize()
+    assert loss.dtype == torch.float32
+    assert hid.grad.dtype == torch.bfloat16 and lm_head.grad.dtype == torch.float32
+    lo, dho, dwo = on.ce_forward_backward(np64(hid), np64(lm_head.detach().to(torch.bfloat16)),
+                                          tgt.cpu().numpy())
+    assert abs(float(loss) - lo) / lo < 2e-2
+    assert on.rel_err(np64(hid.grad), dho) < 2e-2
+    assert on.rel_err(np64(lm_head.grad), dwo) < 2e-2
+    assert not hid.grad[::7].any()
+
+
+def test_ce_reasoning_head_step_replays_in_a_graph(cuda):
+    """The device path needs no host synchronisation (the reference's
+    n_valid .item(), chunked_ce.py:126, is gone): forward + backward of the
+    reasoning head capture into one HIP graph, and every replay, with eager
+    work and synchronisations between replays, reproduces the eager step
+    bit for bit."""
+    note("ce reasoning head graph capture")
+    hid0, lm0, tgt = _reasoning_head_inputs(cuda, seed=9)
+
+    def make():
+        h = hid0.detach().requires_grad_(True)
+        w = torch.nn.Parameter(lm0.detach().clone())
+
+        def step():
+            with torch.autocast("cuda", dtype=torch.bfloat16):
+                loss = chunked_cross_entropy(h, w, tgt, chunk_size=1024)
+            gh, gw = torch.autograd.grad(loss, [h, w])
+            return loss, gh, gw
+
+        return step
+
+    eager = [t.clone() for t in make()()]
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        step = make()
+        step()
+    side.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=side):
+        outs = step()
+    torch.cuda.current_stream().wait_stream(side)
+    for i in range(3):
+        graph.replay()
+        torch.cuda.synchronize()
+        assert all(torch.equal(a, b) for a, b in zip(outs, eager)), f"replay {i}"
+        make()()  # eager work between replays
+        torch.cuda.synchronize()
