@@ -520,32 +520,52 @@ __global__ __launch_bounds__(256) void scale_cast_kernel(
 inline int64_t round_up(int64_t x, int64_t m) { return (x + m - 1) / m * m; }
 inline size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
-// K split of a vocabulary chunk's dH product.  The chunk's dW blocks (K =
-// tokens) and dH blocks (K = chunk columns) run in one launch; when that
-// launch is one partial wave and the dH blocks are the longer ones (few
-// tokens, a long chunk: the reasoning head's M 512 x D 384 with the whole
-// vocabulary in one chunk has 4 dH tiles of K 32000 beside 250 dW tiles of
-// K 512), dH is split along K into slices about as long as a dW block's K
-// (at least 512), keeping the launch within ~512 blocks.
+// K splits of a vocabulary chunk's two gradient products.  The chunk's dW
+// blocks (K = tokens) and dH blocks (K = chunk columns) run in one launch.
+// When that launch fits in one wave of the 256 CUs, its time is the longest
+// block's K; splitting the job with the longer K into S slices shortens it
+// at the cost of more blocks.  S is chosen (1 .. 64) to minimise
+// waves(blocks) x longest slice, ties to fewer slices: e.g. the reasoning
+// head (M 512, D 384, the whole vocabulary in one chunk: 4 dH tiles of K
+// 32000 beside 250 dW tiles of K 512) splits dH 63 ways, M 16384 with D 384
+// and 2048-column chunks (16 dW tiles of K 16384) splits dW 8 ways, and the
+// BASELINE shape (128 + 128 tiles of K 4096) is not split.  Slices are summed
+// by splitk_reduce_kernel in a fixed order.
 struct Split {
   int S;
   int64_t kslice;
 };
+struct SplitPlan {
+  Split w, h;  // dW, dH
+};
 template <class C>
-inline Split dh_split(int64_t vc, int64_t M, int64_t D) {
+inline Split best_split(int64_t t_short, int64_t k_short, int64_t t_long, int64_t k_long) {
+  Split best{1, k_long};
+  int64_t best_t = -1;
+  for (int64_t S = 1; S <= 64; ++S) {
+    const int64_t ks = round_up((k_long + S - 1) / S, C::BK);
+    const int64_t se = (k_long + ks - 1) / ks;
+    const int64_t waves = (t_short + t_long * se + 255) / 256;
+    const int64_t t = waves * (k_short > ks ? k_short : ks);
+    if (best_t < 0 || t < best_t) {
+      best_t = t;
+      best = {(int)se, ks};
+    }
+  }
+  return best;
+}
+template <class C>
+inline SplitPlan chunk_split(int64_t vc, int64_t M, int64_t D) {
   const int64_t tn = (D + C::BN - 1) / C::BN;
   const int64_t tw = (vc + C::BM - 1) / C::BM * tn, th = (M + C::BM - 1) / C::BM * tn;
-  const int64_t K = round_up(vc, 8), kw = round_up(M, 8);
-  int64_t S = 1;
-  if (tw + th < 256) {
-    const int64_t balance = (K + (kw > 512 ? kw : 512) - 1) / (kw > 512 ? kw : 512);
-    const int64_t fill = (512 - tw) / th;
-    S = balance < fill ? balance : fill;
-    if (S > 64) S = 64;
-    if (S < 1) S = 1;
-  }
-  const int64_t kslice = round_up((K + S - 1) / S, C::BK);
-  return {(int)((K + kslice - 1) / kslice), kslice};
+  const int64_t kh = round_up(vc, 8), kw = round_up(M, 8);
+  SplitPlan p{{1, kw}, {1, kh}};
+  if (tw + th >= 256) return p;  // a full wave or more: the blocks already balance
+  if (kh >= kw)
+    p.h = best_split<C>(tw, kw, th, kh);
+  else
+    p.w = best_split<C>(th, kh, tw, kw);
+  return p;
 }
 
 struct Layout {
@@ -558,8 +578,11 @@ template <class C>
 inline size_t partial_bytes(int64_t M, int64_t D, int64_t V, int64_t vc) {
   size_t most = 0;
   for (int64_t vb = 0; vb < V; vb += vc) {
-    const Split sp = dh_split<C>(V - vb < vc ? V - vb : vc, M, D);
-    const size_t b = sp.S > 1 ? (size_t)sp.S * M * D * sizeof(float) : 0;
+    const int64_t c = V - vb < vc ? V - vb : vc;
+    const SplitPlan sp = chunk_split<C>(c, M, D);
+    const size_t bw = sp.w.S > 1 ? (size_t)sp.w.S * c * D * sizeof(float) : 0;
+    const size_t bh = sp.h.S > 1 ? (size_t)sp.h.S * M * D * sizeof(float) : 0;
+    const size_t b = bw > bh ? bw : bh;  // at most one of the two is split
     if (b > most) most = b;
   }
   return most;
@@ -712,21 +735,26 @@ int ce_run(const TI *H, const TI *W, const int64_t *targets, int64_t M, int64_t 
     if ((e = check_launch("ce_prob"))) return e;
     // dW[vb:vb+vc, :] = P_c^T H   (K = tokens, zero-padded to ldht) and
     // dH += P_c W_c               (K = chunk columns, zero-padded to kpad)
-    const auto jw = make_job<C>(PT, L.ldht, Ht, L.ldht, dW + vb * D, D, vc, D, L.ldht, 0);
+    auto jw = make_job<C>(PT, L.ldht, Ht, L.ldht, dW + vb * D, D, vc, D, L.ldht, 0);
     auto jh = make_job<C>(P, L.ldp, Wt + vb, L.ldwt, dH, D, M, D, kpad, vb > 0 ? 1 : 0);
-    const Split sp = dh_split<C>(vc, M, D);
-    if (sp.S > 1) {
-      jh.ksplit = sp.S;
-      jh.kslice = sp.kslice;
-      jh.part = reinterpret_cast<float *>(ws + L.off_part);
-      jh.tiles *= sp.S;
+    const SplitPlan sp = chunk_split<C>(vc, M, D);
+    float *part = reinterpret_cast<float *>(ws + L.off_part);
+    for (auto *jp : {&jw, &jh}) {
+      const Split &q = jp == &jw ? sp.w : sp.h;
+      if (q.S > 1) {
+        jp->ksplit = q.S;
+        jp->kslice = q.kslice;
+        jp->part = part;
+        jp->tiles *= q.S;
+      }
     }
     if ((e = launch_gemm_store<C>(jw, jh, s))) return e;
-    if (sp.S > 1) {
-      int64_t blocks = (M * D + 255) / 256;
+    for (const auto *jp : {&jw, &jh}) {
+      if (jp->ksplit <= 1) continue;
+      int64_t blocks = (jp->M * D + 255) / 256;
       if (blocks > 2048) blocks = 2048;
-      splitk_reduce_kernel<<<(unsigned)blocks, 256, 0, s>>>(jh.part, sp.S, M, D, dH, D,
-                                                           jh.accumulate);
+      splitk_reduce_kernel<<<(unsigned)blocks, 256, 0, s>>>(jp->part, jp->ksplit, jp->M, D,
+                                                           jp->C, D, jp->accumulate);
       if ((e = check_launch("splitk_reduce"))) return e;
     }
   }
