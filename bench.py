@@ -29,7 +29,8 @@ Timing:
     2.5 PFLOP/s on 6*M_valid*V*D), the cfg5 stress chain, their CPU baselines;
     the two callers at the reference's model shape: the DiT seam (B8 T6 N384,
     autocast dtypes, chunk(6) views) and the reasoning-head CE (M512 D384
-    V32000, bf16 hidden, fp32 lm_head), each beside its eager formulation.
+    V32000, bf16 hidden, fp32 lm_head), each beside its eager formulation;
+    SwiGLU in the gate/up GEMM epilogue at the encoder MLP shape.
 """
 
 from __future__ import annotations
@@ -57,7 +58,8 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-extra", action="store_true", help="headline workload only")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baselines")
-    ap.add_argument("--only", choices=("swiglu", "ce", "stress", "traffic", "dit", "head"),
+    ap.add_argument("--only", choices=("swiglu", "ce", "stress", "traffic", "dit", "head",
+                                       "gateup"),
                     default=None,
                     help="run one secondary workload alone (for profiling) and print its "
                          "record instead of the headline line")
@@ -519,6 +521,47 @@ def bench_ce_reasoning_head(args, dev, m=512, d=384, v=32000):
             "speedup": eager_ms / fused_ms}
 
 
+def bench_gate_up(args, dev, m=8 * 6 * 196, d=384, h=1536):
+    """SwiGLU in the gate/up GEMM epilogue at the reference's encoder MLP
+    shape (TransformerBlock's SwiGLUMLP(384, 1536), model/nuvla.py:47-59,
+    over batch 8 x 6 views x 196 patches): fused_gate_up_swiglu vs the
+    reference's composition (two Linears + fused SwiGLU) and the eager one,
+    bf16, forward alone and forward + backward."""
+    import torch
+    import torch.nn.functional as F
+
+    from nuvla_forge_amd.kernels import fused_gate_up_swiglu, fused_swiglu
+
+    g = torch.Generator().manual_seed(42)
+    x = torch.randn(m, d, generator=g).to(torch.bfloat16).to(dev)
+    wg = (torch.randn(h, d, generator=g) * d ** -0.5).to(torch.bfloat16).to(dev)
+    wu = (torch.randn(h, d, generator=g) * d ** -0.5).to(torch.bfloat16).to(dev)
+    dact = torch.randn(m, h, generator=g).to(torch.bfloat16).to(dev)
+    paths = {
+        "fused_gemm_epilogue": lambda a, b, c: fused_gate_up_swiglu(a, b, c),
+        "linears_plus_fused_swiglu": lambda a, b, c: fused_swiglu(F.linear(a, b), F.linear(a, c)),
+        "eager": lambda a, b, c: F.silu(F.linear(a, b)) * F.linear(a, c),
+    }
+    out = {"m": m, "d": d, "h": h}
+    for name, fn in paths.items():
+        def make_fwd(fn=fn):
+            return lambda: (fn(x, wg, wu),)
+
+        def make_step(fn=fn):
+            leaves = [t.detach().requires_grad_(True) for t in (x, wg, wu)]
+
+            def step():
+                act = fn(*leaves)
+                return (act, *torch.autograd.grad(act, leaves, dact))
+
+            return step
+
+        out[name + "_fwd_us"] = time_graph(make_fwd, args.steps, args.warmup)[0] * 1e3
+        out[name + "_fwdbwd_us"] = time_graph(make_step, args.steps, args.warmup)[0] * 1e3
+    out["gemm_tflops_fused_fwd"] = 4 * m * d * h / (out["fused_gemm_epilogue_fwd_us"] * 1e-6) / 1e12
+    return out
+
+
 # ---------------------------------------------------------------------------
 # CPU baselines (the reference's eager PyTorch path, oracle/torch_cpu.py)
 # ---------------------------------------------------------------------------
@@ -579,7 +622,7 @@ def main() -> int:
     if args.only:
         fn = {"swiglu": bench_swiglu, "ce": bench_ce, "stress": bench_stress,
               "traffic": bench_traffic, "dit": bench_dit_seam,
-              "head": bench_ce_reasoning_head}[args.only]
+              "head": bench_ce_reasoning_head, "gateup": bench_gate_up}[args.only]
         print(json.dumps({"workload": args.only, **fn(args, dev)}), flush=True)
         return 0
 
@@ -604,6 +647,9 @@ def main() -> int:
         log("reasoning-head CE at model shape ...")
         extra["ce_reasoning_head"] = bench_ce_reasoning_head(args, dev)
         log(f"  {extra['ce_reasoning_head']}")
+        log("SwiGLU in the gate/up GEMM epilogue ...")
+        extra["swiglu_gate_up_gemm"] = bench_gate_up(args, dev)
+        log(f"  {extra['swiglu_gate_up_gemm']}")
 
     cpu = None
     if not args.no_cpu:

@@ -66,6 +66,23 @@ int nf_swiglu_bwd(const void *dout, const void *a, const void *b, void *da,
                   void *db, int64_t n, int dtype, void *stream);
 
 /* ------------------------------------------------------------------------
+ * Gate/up projection with the SwiGLU epilogue: one MFMA GEMM computing
+ *   a = x W_gate^T,  b = x W_up^T,  act = silu(a) * b     (fp32 accumulate)
+ * No kernel of the reference computes this: it replaces the two Linear calls
+ * and the fused_swiglu call of SwiGLUMLP.forward
+ * (nuvla_forge/model/dit.py:104-110), whose a and b round-trip HBM.
+ * x [M, D] (row stride ldx), w_gate / w_up [H, D] (row stride ldw, the
+ * nn.Linear weight layout, used in place), a / b / act [M, H] (row stride
+ * ldo).  a and b are written (rounded to bf16, for the backward) only when
+ * both are non-null.  bf16 only (NF_ERR_DTYPE otherwise); every operand and
+ * output under 2 GiB.
+ * ---------------------------------------------------------------------- */
+int nf_gemm_swiglu(const void *x, int64_t ldx, const void *w_gate,
+                   const void *w_up, int64_t ldw, void *a, void *b, void *act,
+                   int64_t ldo, int64_t M, int64_t D, int64_t H, int dtype,
+                   void *stream);
+
+/* ------------------------------------------------------------------------
  * adaLN-Zero seam: gated residual add, RMSNorm, modulation.  Row m of the
  * [M, N] activations belongs to sample m / T (M = B * T).
  *   h   = x + gate[b] * y                                  (stored as dt_x)

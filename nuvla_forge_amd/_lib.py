@@ -54,6 +54,9 @@ SIGNATURES = {
     ),
     "nf_scale_cast": (_I32, [_P, _P, _P, _I64, _I32, _P]),
     "nf_gemm_nt": (_I32, [_P, _I64, _P, _I64, _P, _I64, _I64, _I64, _I64, _I32, _P]),
+    "nf_gemm_swiglu": (
+        _I32, [_P, _I64, _P, _P, _I64, _P, _P, _P, _I64, _I64, _I64, _I64, _I32, _P],
+    ),
 }
 
 _lib: ctypes.CDLL | None = None

@@ -294,7 +294,7 @@ template <class C, int CW>
 struct DtlOperand {
   using TI = typename C::TI;
   const TI *base;
-  int64_t ld, rows, K;
+  int64_t ld, rows, K, r0;  // r0: matrix row of tile row 0
   __amdgpu_buffer_rsrc_t rsrc;
   uint32_t off_p[2];  // byte offset at k = 0 of chunk parity p (rows assumed in range)
   int kvec_p[2];      // k-vector this lane copies for chunk parity p
@@ -304,15 +304,15 @@ struct DtlOperand {
   static constexpr uint32_t kOob = 0x80000000u;
 
   __device__ __forceinline__ void init(const TI *p, int64_t ld_, int64_t rows_, int64_t K_,
-                                       int64_t r0, int wave) {
-    base = p; ld = ld_; rows = rows_; K = K_;
+                                       int64_t r0_, int wave) {
+    base = p; ld = ld_; rows = rows_; K = K_; r0 = r0_;
     rsrc = __builtin_amdgcn_make_buffer_rsrc(const_cast<TI *>(p), (short)0,
                                              (int)(rows_ * ld_ * (int64_t)sizeof(TI)),
                                              0x00020000);
     const int l = threadIdx.x & 63;
     lrow = l / C::KVEC;
     const int g0 = wave * CW;
-    const int64_t first = r0 + (int64_t)g0 * C::RPC;  // first row of chunk g0
+    const int64_t first = r0_ + (int64_t)g0 * C::RPC;  // first row of chunk g0
     const int64_t left = rows_ - first;
     rows_left = (int)(left < 0 ? 0 : (left > CW * C::RPC ? CW * C::RPC : left));
     cstride = (uint32_t)((int64_t)C::RPC * ld_ * (int64_t)sizeof(TI));
@@ -336,7 +336,7 @@ struct DtlOperand {
     }
   }
   // the same copy through registers and ds_write (any alignment, any K)
-  __device__ __forceinline__ void copy_sync(int64_t k0, int64_t r0, int wave, char *region) const {
+  __device__ __forceinline__ void copy_sync(int64_t k0, int wave, char *region) const {
     const int l = threadIdx.x & 63;
 #pragma unroll
     for (int c = 0; c < CW; ++c) {
@@ -393,14 +393,17 @@ __device__ __forceinline__ void read_kgroup_dtl(const char *stage, int wm, int w
   for (int j = 0; j < C::TN; ++j) b[j] = *reinterpret_cast<const u32x4 *>(bs + j * 32 * C::ROW);
 }
 
+template <class C, bool BUF>
+__device__ __forceinline__ void mainloop_dtl_ops(const DtlOperand<C, C::ACW> &opa,
+                                                 const DtlOperand<C, C::BCW> &opb, int64_t K,
+                                                 char *smem, floatx16 (&acc)[C::TM][C::TN]);
+
 template <class C, bool BUF, bool ZERO>
 __device__ __forceinline__ void mainloop_dtl(const bf16 *A, int64_t lda, const bf16 *B,
                                              int64_t ldb, int64_t M, int64_t N, int64_t K,
                                              int64_t m0, int64_t n0, char *smem,
                                              floatx16 (&acc)[C::TM][C::TN]) {
-  const int w = threadIdx.x >> 6;
-  const int wave = __builtin_amdgcn_readfirstlane(w);
-  const int wm = w / C::WN, wn = w % C::WN;
+  const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
   if constexpr (ZERO) {
 #pragma unroll
     for (int i = 0; i < C::TM; ++i)
@@ -413,6 +416,18 @@ __device__ __forceinline__ void mainloop_dtl(const bf16 *A, int64_t lda, const b
   DtlOperand<C, C::BCW> opb;
   opa.init(A, lda, M, K, m0, wave);
   opb.init(B, ldb, N, K, n0, wave);
+  mainloop_dtl_ops<C, BUF>(opa, opb, K, smem, acc);
+}
+
+// The K loop over operands the caller has set up (a kernel may point each
+// wavefront's share of a tile at a different matrix).  acc is not cleared.
+template <class C, bool BUF>
+__device__ __forceinline__ void mainloop_dtl_ops(const DtlOperand<C, C::ACW> &opa,
+                                                 const DtlOperand<C, C::BCW> &opb, int64_t K,
+                                                 char *smem, floatx16 (&acc)[C::TM][C::TN]) {
+  const int w = threadIdx.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(w);
+  const int wm = w / C::WN, wn = w % C::WN;
   const int64_t nk = (K + C::BK - 1) / C::BK;
   u32x4 a0[C::TM], b0[C::TN], a1[C::TM], b1[C::TN];
   if constexpr (BUF) {
@@ -465,8 +480,8 @@ __device__ __forceinline__ void mainloop_dtl(const bf16 *A, int64_t lda, const b
     }
   } else {
     for (int64_t kt = 0; kt < nk; ++kt) {
-      opa.copy_sync(kt * C::BK, m0, wave, smem);
-      opb.copy_sync(kt * C::BK, n0, wave, smem + C::BM * C::ROW);
+      opa.copy_sync(kt * C::BK, wave, smem);
+      opb.copy_sync(kt * C::BK, wave, smem + C::BM * C::ROW);
       __syncthreads();
 #pragma unroll
       for (int kg = 0; kg < C::KG; kg += 2) {

@@ -1,0 +1,141 @@
+// SwiGLU as the epilogue of the gate/up projection GEMM:
+//   a = x W_gate^T,  b = x W_up^T,  act = silu(a) * b
+// in one MFMA kernel (the reference's SwiGLUMLP runs two GEMMs that write a
+// and b to HBM and a SwiGLU kernel that reads them back, model/dit.py:96-110).
+//
+// Tiling.  A 256 x 256 block tile of the combined product x [W_gate; W_up]^T
+// covers 256 tokens and 128 hidden units: tile columns 64 q .. 64 q + 31 are
+// gate units u0 + 32 q .. + 31 and columns 64 q + 32 .. 64 q + 63 the up
+// projections of the same units (u0 = 128 * tile column).  The direct-to-LDS
+// loader hands each wavefront 32 consecutive tile rows of the B operand, so
+// wavefront w simply copies its rows from W_up (w odd) or W_gate (w even):
+// the interleave costs nothing and the weights are used in place.  With 8
+// wavefronts of 128 x 64, a lane's two 32-column accumulator tiles are then
+// a and b of the same (token, unit) pairs, and the epilogue is element-wise
+// in registers: fp32 silu(a) * b rounded once, plus a and b rounded to the
+// input type (what the backward needs; the caller may skip them).
+#include "gemm_core.h"
+
+namespace nf {
+namespace swiglu_gemm {
+
+using C = gemm::DCfg<256, 256, 2, 4, 2, 64>;
+using gemm::floatx16;
+static_assert(C::BN == 256 && C::NW == 8 && C::WM == 2 && C::WN == 4, "tiling assumed below");
+static_assert(C::BCW * C::RPC == 32, "each wavefront must copy one 32-row group of B");
+static_assert(C::TN == 2, "a lane's two column tiles are the gate and up halves");
+
+constexpr uint32_t kOob = 0x80000000u;
+
+struct Args {
+  const bf16 *x;
+  const bf16 *wg;
+  const bf16 *wu;
+  bf16 *a;    // [M, ldo] or null
+  bf16 *b;    // [M, ldo] or null
+  bf16 *act;  // [M, ldo]
+  int64_t ldx, ldw, ldo, M, D, H;
+  int tiles_m, tiles_n;
+};
+
+// 2-byte store through a buffer resource over a [M, ldo] output; masked
+// elements get an out-of-range offset (dropped by the buffer unit).
+__device__ __forceinline__ void st_bf16(__amdgpu_buffer_rsrc_t r, uint32_t off, bool ok, float v) {
+  const bf16 h = static_cast<bf16>(v);
+  uint16_t bits;
+  __builtin_memcpy(&bits, &h, 2);
+  __builtin_amdgcn_raw_buffer_store_b16(bits, r, ok ? off : kOob, 0, 0);
+}
+
+template <bool BUF>
+__global__ NF_GEMM_BOUNDS(C) void gate_up_swiglu_kernel(Args p) {
+  __shared__ __attribute__((aligned(16))) char smem[C::LDS_BYTES];
+  int tm, tn;
+  gemm::group_tile(gemm::xcd_order(blockIdx.x, p.tiles_m * p.tiles_n), p.tiles_m, p.tiles_n,
+                   gemm::kTileGroup, tm, tn);
+  const int64_t m0 = (int64_t)tm * C::BM;
+  const int64_t u0 = (int64_t)tn * (C::BN / 2);  // first hidden unit of the tile
+  const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+
+  floatx16 acc[C::TM][C::TN];
+#pragma unroll
+  for (int i = 0; i < C::TM; ++i)
+#pragma unroll
+    for (int j = 0; j < C::TN; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+  gemm::DtlOperand<C, C::ACW> opa;
+  gemm::DtlOperand<C, C::BCW> opb;
+  opa.init(p.x, p.ldx, p.M, p.D, m0, wave);
+  // wavefront w copies tile rows 32 w .. 32 w + 31: units u0 + 32 (w / 2) + 0..31
+  // of W_up (w odd) or W_gate (w even); r0 makes tile row 32 w that matrix row
+  const int64_t unit0 = u0 + 32 * (wave >> 1);
+  opb.init((wave & 1) ? p.wu : p.wg, p.ldw, p.H, p.D, unit0 - 32 * wave, wave);
+  gemm::mainloop_dtl_ops<C, BUF>(opa, opb, p.D, smem, acc);
+
+  const int l = threadIdx.x & 63;
+  const int w = threadIdx.x >> 6, wm = w / C::WN, wn = w % C::WN;
+  const int64_t unit = u0 + 32 * wn + (l & 31);
+  const int64_t row0 = m0 + wm * C::WTM + 4 * (l >> 5);
+  const int64_t bytes = p.M * p.ldo * 2;
+  const __amdgpu_buffer_rsrc_t ract =
+      __builtin_amdgcn_make_buffer_rsrc(p.act, (short)0, (int)bytes, 0x00020000);
+  __amdgpu_buffer_rsrc_t ra = ract, rb = ract;
+  if (p.a) ra = __builtin_amdgcn_make_buffer_rsrc(p.a, (short)0, (int)bytes, 0x00020000);
+  if (p.b) rb = __builtin_amdgcn_make_buffer_rsrc(p.b, (short)0, (int)bytes, 0x00020000);
+  const bool save = p.a != nullptr;
+#pragma unroll
+  for (int i = 0; i < C::TM; ++i)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int64_t row = row0 + i * 32 + 8 * (r >> 2) + (r & 3);
+      const bool ok = row < p.M && unit < p.H;
+      const uint32_t off = (uint32_t)((row * p.ldo + unit) * 2);
+      const float av = acc[i][0][r], bv = acc[i][1][r];
+      st_bf16(ract, off, ok, av * sigmoid(av) * bv);
+      if (save) {
+        st_bf16(ra, off, ok, av);
+        st_bf16(rb, off, ok, bv);
+      }
+    }
+}
+
+}  // namespace swiglu_gemm
+}  // namespace nf
+
+using namespace nf;
+
+extern "C" int nf_gemm_swiglu(const void *x, int64_t ldx, const void *w_gate, const void *w_up,
+                              int64_t ldw, void *a, void *b, void *act, int64_t ldo, int64_t M,
+                              int64_t D, int64_t H, int dtype, void *stream) {
+  using namespace nf::swiglu_gemm;
+  if (M < 0 || D <= 0 || H <= 0)
+    return set_error(NF_ERR_ARG, "nf_gemm_swiglu: bad shape M=%lld D=%lld H=%lld",
+                     (long long)M, (long long)D, (long long)H);
+  if (M == 0) return NF_OK;
+  if (dtype != NF_DTYPE_BF16)
+    return set_error(NF_ERR_DTYPE, "nf_gemm_swiglu: dtype %d unsupported (bf16 only)", dtype);
+  if (!x || !w_gate || !w_up || !act || (!a) != (!b))
+    return set_error(NF_ERR_ARG, "nf_gemm_swiglu: null pointer (a and b: both or neither)");
+  if (ldx < D || ldw < D || ldo < H)
+    return set_error(NF_ERR_ARG, "nf_gemm_swiglu: bad leading dimension");
+  // 32-bit buffer offsets: every operand and output under 2 GiB
+  const int64_t lim = ((int64_t)1 << 31) - 64;
+  if (M * ldx * 2 >= lim || H * ldw * 2 >= lim || M * ldo * 2 >= lim)
+    return set_error(NF_ERR_ARG, "nf_gemm_swiglu: an operand exceeds 2 GiB");
+  const int64_t tiles_m = (M + C::BM - 1) / C::BM, tiles_n = (H + C::BN / 2 - 1) / (C::BN / 2);
+  if (tiles_m * tiles_n > 0x7fffffffLL)
+    return set_error(NF_ERR_ARG, "nf_gemm_swiglu: grid too large");
+  Args args{static_cast<const bf16 *>(x), static_cast<const bf16 *>(w_gate),
+            static_cast<const bf16 *>(w_up), static_cast<bf16 *>(a), static_cast<bf16 *>(b),
+            static_cast<bf16 *>(act), ldx, ldw, ldo, M, D, H, (int)tiles_m, (int)tiles_n};
+  const bool buf = D % 8 == 0 && ldx % 8 == 0 && ldw % 8 == 0 && aligned16(x) &&
+                   aligned16(w_gate) && aligned16(w_up);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const unsigned grid = (unsigned)(tiles_m * tiles_n);
+  if (buf)
+    gate_up_swiglu_kernel<true><<<grid, C::NT, 0, s>>>(args);
+  else
+    gate_up_swiglu_kernel<false><<<grid, C::NT, 0, s>>>(args);
+  return check_launch("nf_gemm_swiglu");
+}

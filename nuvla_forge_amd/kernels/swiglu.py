@@ -6,11 +6,16 @@ swiglu.py:66-92) and the same ``fused_swiglu(a, b, force_reference=False)``
 entry point (swiglu.py:95-106).  The forward and backward are the HIP kernels
 ``nf_swiglu_fwd`` / ``nf_swiglu_bwd``; the backward recomputes the sigmoid
 from ``a`` instead of storing it.
+
+Beyond the reference: ``fused_gate_up_swiglu`` moves the SwiGLU into the
+epilogue of the gate/up projection GEMM (``nf_gemm_swiglu``), so a and b
+never make the HBM round trip between the projections and the activation.
 """
 
 from __future__ import annotations
 
 import torch
+import torch.nn.functional as F
 
 from .. import _lib
 from .reference import swiglu_ref
@@ -60,6 +65,98 @@ class _FusedSwiGLU(torch.autograd.Function):
                 "nf_swiglu_bwd",
             )
         return da, db
+
+
+class _FusedGateUpSwiGLU(torch.autograd.Function):
+    """act = silu(x W_gate^T) * (x W_up^T) with the SwiGLU in the GEMM epilogue.
+
+    forward: one ``nf_gemm_swiglu`` launch writes act and the bf16 a, b the
+    backward needs.  backward: ``nf_swiglu_bwd`` forms da, db from a, b and
+    dact (sigmoid recomputed), then the plain products dx = da W_gate +
+    db W_up, dW_gate = da^T x, dW_up = db^T x run as library GEMMs.
+    """
+
+    @staticmethod
+    def forward(ctx, x, w_gate, w_up):
+        m, d = x.shape
+        h = w_gate.shape[0]
+        a = torch.empty((m, h), dtype=torch.bfloat16, device=x.device)
+        b = torch.empty_like(a)
+        act = torch.empty_like(a)
+        L = _lib.lib()
+        with device_of(x):
+            _lib.check(
+                L.nf_gemm_swiglu(x.data_ptr(), x.stride(0), w_gate.data_ptr(), w_up.data_ptr(),
+                                 w_gate.stride(0), a.data_ptr(), b.data_ptr(), act.data_ptr(),
+                                 h, m, d, h, _lib.dtype_code(torch.bfloat16),
+                                 _lib.stream_of(x)),
+                "nf_gemm_swiglu",
+            )
+        ctx.save_for_backward(x, w_gate, w_up, a, b)
+        return act
+
+    @staticmethod
+    def backward(ctx, dact):
+        x, w_gate, w_up, a, b = ctx.saved_tensors
+        dact = dact.to(torch.bfloat16).contiguous()
+        da, db = torch.empty_like(a), torch.empty_like(b)
+        L = _lib.lib()
+        with device_of(a):
+            _lib.check(
+                L.nf_swiglu_bwd(dact.data_ptr(), a.data_ptr(), b.data_ptr(), da.data_ptr(),
+                                db.data_ptr(), a.numel(), _lib.dtype_code(a), _lib.stream_of(a)),
+                "nf_swiglu_bwd",
+            )
+        need = ctx.needs_input_grad
+        dx = torch.addmm(torch.mm(da, w_gate), db, w_up) if need[0] else None
+        dwg = torch.mm(da.t(), x) if need[1] else None
+        dwu = torch.mm(db.t(), x) if need[2] else None
+        return dx, dwg, dwu
+
+
+def _gate_up_eager(x, w_gate, w_up):
+    return F.silu(F.linear(x, w_gate)) * F.linear(x, w_up)
+
+
+def fused_gate_up_swiglu(x: torch.Tensor, w_gate: torch.Tensor, w_up: torch.Tensor,
+                         force_reference: bool = False) -> torch.Tensor:
+    """``silu(x @ w_gate.T) * (x @ w_up.T)``: the gate/up half of a SwiGLU MLP
+    (the reference's ``SwiGLUMLP``, model/dit.py:96-110) with the SwiGLU fused
+    into the projection GEMM's epilogue.
+
+    Args:
+        x: [..., D] activations on a ROCm device.
+        w_gate, w_up: [H, D] projection weights (``nn.Linear.weight``).
+        force_reference: run the eager formulation (two Linears + silu * mul).
+
+    The fused kernel computes in bf16 with fp32 accumulation: it runs when
+    the inputs are bf16, or under bf16 autocast (as the Linears would); other
+    dtypes take the two Linears and the fused SwiGLU kernel.  Gradients come
+    back in each input's dtype.
+    """
+    if force_reference:
+        return _gate_up_eager(x, w_gate, w_up)
+    require_device(x, "fused_gate_up_swiglu")
+    if w_gate.shape != w_up.shape or w_gate.dim() != 2 or x.shape[-1] != w_gate.shape[1]:
+        raise ValueError(f"fused_gate_up_swiglu: x [..., D] and weights [H, D] expected, got "
+                         f"{tuple(x.shape)}, {tuple(w_gate.shape)}, {tuple(w_up.shape)}")
+    autocast_bf16 = (torch.is_autocast_enabled(x.device.type)
+                     and torch.get_autocast_dtype(x.device.type) == torch.bfloat16)
+    all_bf16 = x.dtype == w_gate.dtype == w_up.dtype == torch.bfloat16
+    if not (all_bf16 or autocast_bf16):
+        return fused_swiglu(F.linear(x, w_gate), F.linear(x, w_up))
+    lead = x.shape[:-1]
+    x2 = x.reshape(-1, x.shape[-1])
+    with torch.autocast(x.device.type, enabled=False):
+        act = _FusedGateUpSwiGLU.apply(
+            _rows_bf16(x2), _rows_bf16(w_gate), _rows_bf16(w_up))
+    return act.reshape(*lead, w_gate.shape[0])
+
+
+def _rows_bf16(t: torch.Tensor) -> torch.Tensor:
+    """bf16 with unit-stride rows (a differentiable cast / copy only when needed)."""
+    t = t.to(torch.bfloat16)
+    return t if t.stride(-1) == 1 else t.contiguous()
 
 
 def fused_swiglu(a: torch.Tensor, b: torch.Tensor, force_reference: bool = False) -> torch.Tensor:

@@ -65,6 +65,27 @@ def test_swiglu_argument_validation():
     assert L.nf_swiglu_bwd(FAKE, FAKE, FAKE, FAKE, FAKE, 0, 1, None) == NF_OK  # empty: no launch
 
 
+def test_gemm_swiglu_argument_validation():
+    L = _lib.lib()
+    # x, ldx, w_gate, w_up, ldw, a, b, act, ldo, M, D, H, dtype, stream
+    ok = [FAKE, 64, FAKE, FAKE, 64, FAKE, FAKE, FAKE, 128, 16, 64, 128, 1, None]
+    bad_dtype = list(ok)
+    bad_dtype[12] = 0
+    assert L.nf_gemm_swiglu(*bad_dtype) == NF_ERR_DTYPE and "bf16 only" in _err()
+    one_saved = list(ok)
+    one_saved[6] = None  # a without b
+    assert L.nf_gemm_swiglu(*one_saved) == NF_ERR_ARG and "both or neither" in _err()
+    short_ldo = list(ok)
+    short_ldo[8] = 100  # ldo < H
+    assert L.nf_gemm_swiglu(*short_ldo) == NF_ERR_ARG and "leading dimension" in _err()
+    neg = list(ok)
+    neg[11] = 0  # H = 0
+    assert L.nf_gemm_swiglu(*neg) == NF_ERR_ARG and "bad shape" in _err()
+    empty = list(ok)
+    empty[9] = 0  # M = 0: nothing to do, no launch
+    assert L.nf_gemm_swiglu(*empty) == NF_OK
+
+
 def test_adaln_argument_validation():
     L = _lib.lib()
     args = [FAKE, 1024, FAKE, 1024, FAKE, 1024, FAKE, FAKE, 1024, FAKE, 1024, FAKE, FAKE, FAKE]
