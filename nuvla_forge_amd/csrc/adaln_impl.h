@@ -11,9 +11,11 @@
 // WPR == 1 the row's sum of squares is a pure DPP wavefront reduction; with
 // WPR > 1 the per-wave sums meet in LDS.
 //
-// Forward.  Each row group walks a contiguous run of rows, issuing the loads
-// of row r+1 before working on row r (two rows of x, y in flight per
-// wavefront) and keeping the per-sample conditioning in registers while the
+// Forward.  Each row group walks a contiguous run of rows.  When the run lies
+// in one sample (16-bit inputs), it is taken in batches of RB rows whose
+// loads are all issued before any math and whose RB sums of squares share one
+// LDS round; otherwise row by row, issuing the loads of row r+1 before working
+// on row r and keeping the per-sample conditioning in registers while the
 // sample does not change.
 //
 // Backward.  Block (b, j) owns a contiguous run of rows of sample b; its G row
@@ -71,16 +73,18 @@ struct BwdArgs {
   int dt_gate, dt_weight, dt_scale;
 };
 
-template <int WPR>
+// Block shapes: a row is owned by R = 64 * WPR threads, a block holds
+// G = BLK / R row groups, BLK = max(R, MINB).
+template <int WPR, int MINB = 256>
 struct FwdShape {
   static constexpr int R = 64 * WPR;
-  static constexpr int BLK = R < 256 ? 256 : R;
+  static constexpr int BLK = R < MINB ? MINB : R;
   static constexpr int G = BLK / R;
 };
-template <int WPR>
+template <int WPR, int MINB = 512>
 struct BwdShape {
   static constexpr int R = 64 * WPR;
-  static constexpr int BLK = R < 512 ? 512 : R;
+  static constexpr int BLK = R < MINB ? MINB : R;
   static constexpr int G = BLK / R;
 };
 
@@ -107,13 +111,36 @@ __device__ __forceinline__ float row_sum(float v, float *red, int g, int rt) {
   }
 }
 
+// row_sum for RB rows at once: one LDS round (two barriers) for all RB sums.
+// `red` holds G * WPR * RB floats.
+template <int WPR, int RB>
+__device__ __forceinline__ void row_sum_batch(float (&v)[RB], float *red, int g, int rt) {
+#pragma unroll
+  for (int q = 0; q < RB; ++q) v[q] = wave_sum(v[q]);
+  if constexpr (WPR > 1) {
+    if ((rt & 63) == 0) {
+#pragma unroll
+      for (int q = 0; q < RB; ++q) red[(g * WPR + (rt >> 6)) * RB + q] = v[q];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int q = 0; q < RB; ++q) {
+      float t = 0.f;
+#pragma unroll
+      for (int i = 0; i < WPR; ++i) t += red[(g * WPR + i) * RB + q];
+      v[q] = t;
+    }
+    __syncthreads();
+  }
+}
+
 // ---------------------------------------------------------------------------
 // forward
 // ---------------------------------------------------------------------------
-template <typename TX, typename TY, int K, int WPR, bool VEC, bool NT>
-__global__ __launch_bounds__(FwdShape<WPR>::BLK) void adaln_fwd_kernel(
+template <typename TX, typename TY, int K, int WPR, bool VEC, bool NT, int MINB = 256>
+__global__ __launch_bounds__((FwdShape<WPR, MINB>::BLK)) void adaln_fwd_kernel(
     FwdArgs p) {
-  using S = FwdShape<WPR>;
+  using S = FwdShape<WPR, MINB>;
   __shared__ float red[S::G * WPR];
   const int g = threadIdx.x / S::R;
   const int rt = threadIdx.x % S::R;
@@ -212,6 +239,100 @@ __global__ __launch_bounds__(FwdShape<WPR>::BLK) void adaln_fwd_kernel(
   }
 }
 
+// Forward in batches of RB rows: every row group's rows lie in one sample
+// (the host uses it only when T is a multiple of rows_per_group), so the
+// conditioning is loaded once; each batch issues all its x / y loads before
+// any math (2 * RB * K loads in flight per thread) and reduces its RB sums of
+// squares with one LDS round.
+template <typename TX, typename TY, int K, int WPR, bool VEC, bool NT, int RB>
+__global__ __launch_bounds__(FwdShape<WPR>::BLK) void adaln_fwd_batch_kernel(FwdArgs p) {
+  using S = FwdShape<WPR>;
+  __shared__ float red[S::G * WPR * RB];
+  const int g = threadIdx.x / S::R;
+  const int rt = threadIdx.x % S::R;
+  const int64_t first = ((int64_t)blockIdx.x * S::G + g) * p.rows_per_group;
+  const int64_t last = first + p.rows_per_group < p.M ? first + p.rows_per_group : p.M;
+  const TX *const xp = static_cast<const TX *>(p.x);
+  const TY *const yp = static_cast<const TY *>(p.y);
+
+  float gv[K][8], wo[K][8], shv[K][8];
+  if (first < last) {
+    const int64_t b = first / p.T;
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+      const int col = (k * S::R + rt) * 8;
+      const int valid = chunk_valid(p.N, col);
+      float wv[8], sv[8];
+      if (valid > 0) {
+        load8_dyn<VEC>(p.weight, p.dt_weight, col, valid, wv);
+        load8_dyn<VEC>(p.gate, p.dt_gate, b * p.ld_gate + col, valid, gv[k]);
+        load8_dyn<VEC>(p.scale, p.dt_scale, b * p.ld_scale + col, valid, sv);
+        load8_dyn<VEC>(p.shift, p.dt_shift, b * p.ld_shift + col, valid, shv[k]);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) wo[k][i] = wv[i] * (1.f + sv[i]);
+      }
+    }
+  }
+  for (int r = 0; r < p.rows_per_group; r += RB) {
+    Raw8<TX> xs[RB][K];
+    Raw8<TY> ys[RB][K];
+#pragma unroll
+    for (int q = 0; q < RB; ++q) {
+      const int64_t row = first + r + q;
+#pragma unroll
+      for (int k = 0; k < K; ++k) {
+        const int col = (k * S::R + rt) * 8;
+        const int valid = row < last ? chunk_valid(p.N, col) : 0;
+        if (valid > 0) {
+          xs[q][k].template load<VEC>(xp + row * p.ld_x + col, valid);
+          ys[q][k].template load<VEC>(yp + row * p.ld_y + col, valid);
+        } else {
+          xs[q][k].zero();
+          ys[q][k].zero();
+        }
+      }
+    }
+    float hv[RB][K][8], ss[RB];
+#pragma unroll
+    for (int q = 0; q < RB; ++q) {
+      const int64_t row = first + r + q;
+      ss[q] = 0.f;
+#pragma unroll
+      for (int k = 0; k < K; ++k) {
+        const int col = (k * S::R + rt) * 8;
+        const int valid = row < last ? chunk_valid(p.N, col) : 0;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          hv[q][k][i] = valid > 0 ? xs[q][k][i] + gv[k][i] * ys[q][k][i] : 0.f;
+          ss[q] += hv[q][k][i] * hv[q][k][i];
+        }
+        if (valid > 0)
+          store8_hint<TX, VEC, NT>(static_cast<TX *>(p.h) + row * (int64_t)p.N + col, valid,
+                                   hv[q][k]);
+      }
+    }
+    row_sum_batch<WPR, RB>(ss, red, g, rt);
+#pragma unroll
+    for (int q = 0; q < RB; ++q) {
+      const int64_t row = first + r + q;
+      const float rstd = 1.f / __builtin_sqrtf(ss[q] / (float)p.N + p.eps);
+      if (row < last && rt == 0) p.rstd[row] = rstd;
+#pragma unroll
+      for (int k = 0; k < K; ++k) {
+        const int col = (k * S::R + rt) * 8;
+        const int valid = row < last ? chunk_valid(p.N, col) : 0;
+        if (valid > 0) {
+          float o[8];
+#pragma unroll
+          for (int i = 0; i < 8; ++i) o[i] = (hv[q][k][i] * rstd) * wo[k][i] + shv[k][i];
+          store8_hint<TX, VEC, NT>(static_cast<TX *>(p.out) + row * (int64_t)p.N + col, valid,
+                                   o);
+        }
+      }
+    }
+  }
+}
+
 // ---------------------------------------------------------------------------
 // backward: per-row gradients + per-block partial rows
 // ---------------------------------------------------------------------------
@@ -259,11 +380,16 @@ struct BwdRow {
   Raw8<TY> y[K];
 };
 
-template <typename TX, typename TY, int K, int WPR, bool VEC, bool NT, bool PF>
-__global__ __launch_bounds__(BwdShape<WPR>::BLK) void adaln_bwd_kernel(
+// RB > 1: rows are taken in batches of RB per row group, all their loads
+// issued before any math, the RB row dot products reduced with one LDS round
+// (PF is then unused).  The per-row arithmetic and the accumulation order are
+// those of RB = 1, so the results are bit-identical.
+template <typename TX, typename TY, int K, int WPR, bool VEC, bool NT, bool PF, int MINB = 512,
+          int RB = 1>
+__global__ __launch_bounds__((BwdShape<WPR, MINB>::BLK)) void adaln_bwd_kernel(
     BwdArgs p) {
-  using S = BwdShape<WPR>;
-  __shared__ float red[S::G * WPR];
+  using S = BwdShape<WPR, MINB>;
+  __shared__ float red[S::G * WPR * RB];
   // combine buffer for the G row groups: (G - 1) x (R * K * 8) floats
   __shared__ float comb[S::G > 1 ? (S::G - 1) * S::R * K * 8 : 1];
 
@@ -327,9 +453,62 @@ __global__ __launch_bounds__(BwdShape<WPR>::BLK) void adaln_bwd_kernel(
 
   const int64_t nrows = t1 > t0 ? t1 - t0 : 0;
   const int64_t iters = (nrows + S::G - 1) / S::G;
+  if constexpr (RB > 1) {
+    for (int64_t it = 0; it < iters; it += RB) {
+      BwdRow<TX, TY, K> rw[RB];
+      float rs[RB], dot[RB];
+#pragma unroll
+      for (int q = 0; q < RB; ++q) load_row(t0 + (it + q) * S::G + g, rw[q]);
+#pragma unroll
+      for (int q = 0; q < RB; ++q) {
+        const int64_t t = t0 + (it + q) * S::G + g;
+        rs[q] = t < t1 ? p.rstd[b * p.T + t] : 0.f;
+      }
+      float xh[RB][K][8];
+#pragma unroll
+      for (int q = 0; q < RB; ++q) {
+        dot[q] = 0.f;
+#pragma unroll
+        for (int k = 0; k < K; ++k)
+#pragma unroll
+          for (int i = 0; i < 8; ++i) {
+            xh[q][k][i] = (rw[q].x[k][i] + gv[k][i] * rw[q].y[k][i]) * rs[q];
+            dot[q] += (rw[q].dout[k][i] * wo[k][i]) * xh[q][k][i];
+          }
+      }
+      row_sum_batch<WPR, RB>(dot, red, g, rt);
+#pragma unroll
+      for (int q = 0; q < RB; ++q) {
+        const int64_t t = t0 + (it + q) * S::G + g;
+        const int64_t row = b * p.T + t;
+        const float c = dot[q] / (float)p.N;
+#pragma unroll
+        for (int k = 0; k < K; ++k) {
+          const int col = (k * S::R + rt) * 8;
+          const int valid = t < t1 ? chunk_valid(p.N, col) : 0;
+          if (valid > 0) {
+            float dh[8], dyv[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+              const float d = rw[q].dout[k][i];
+              dh[i] = rw[q].dh[k][i] + rs[q] * (d * wo[k][i] - xh[q][k][i] * c);
+              dyv[i] = dh[i] * gv[k][i];
+              accA[k][i] += d * xh[q][k][i];
+              accS[k][i] += d;
+              accG[k][i] += dh[i] * rw[q].y[k][i];
+            }
+            store8_hint<TX, VEC, NT>(static_cast<TX *>(p.dx) + row * (int64_t)p.N + col, valid,
+                                     dh);
+            store8_hint<TY, VEC, NT>(static_cast<TY *>(p.dy) + row * (int64_t)p.N + col, valid,
+                                     dyv);
+          }
+        }
+      }
+    }
+  }
   BwdRow<TX, TY, K> cur, nxt;
-  if (PF && iters > 0) load_row(t0 + g, cur);
-  for (int64_t it = 0; it < iters; ++it) {
+  if (PF && RB == 1 && iters > 0) load_row(t0 + g, cur);
+  for (int64_t it = 0; RB == 1 && it < iters; ++it) {
     const int64_t t = t0 + it * S::G + g;
     const bool active = t < t1;
     const int64_t row = b * p.T + t;
@@ -469,9 +648,26 @@ inline unsigned fwd_grid(const Plan &pl, int64_t M) {
 constexpr bool kFwdNT = true;
 constexpr bool kBwdNT = true;
 
+// The batched forward (adaln_fwd_batch_kernel) takes RB rows per step: 4 with
+// one 8-element chunk per thread, 2 with two; 16-bit x and y only (fp32 rows
+// would not fit the registers), and only when every row group's rows lie in
+// one sample and split into whole batches.  Measured at bf16 [8192, 1024]:
+// 10.5 us against 12.3 us for the one-row-at-a-time kernel, bit-identical.
+template <typename TX, typename TY, int K>
+constexpr int fwd_batch_rows() {
+  return (sizeof(TX) == 2 && sizeof(TY) == 2) ? (K == 1 ? 4 : 2) : 1;
+}
 template <typename TX, typename TY, bool VEC, int WPR, int K>
 int launch_fwd_t(const FwdArgs &a, const Plan &pl, hipStream_t s) {
   using S = FwdShape<WPR>;
+  constexpr int RB = fwd_batch_rows<TX, TY, K>();
+  if constexpr (VEC && RB > 1) {
+    if (a.rows_per_group % RB == 0 && a.T % a.rows_per_group == 0) {
+      adaln_fwd_batch_kernel<TX, TY, K, WPR, VEC, kFwdNT, RB>
+          <<<fwd_grid(pl, a.M), S::BLK, 0, s>>>(a);
+      return check_launch("nf_adaln_fwd");
+    }
+  }
   adaln_fwd_kernel<TX, TY, K, WPR, VEC, kFwdNT><<<fwd_grid(pl, a.M), S::BLK, 0, s>>>(a);
   return check_launch("nf_adaln_fwd");
 }
