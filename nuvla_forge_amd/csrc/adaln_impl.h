@@ -582,9 +582,13 @@ struct Plan {
 // N >= 1024 are split over >= 2 wavefronts in the forward and the backward
 // keeps one 8-element chunk per thread (up to 16 wavefronts per row).
 // Forward: each row group walks clamp(M / 2048, 1, 8) consecutive rows.
-// Backward: ~512 blocks of 512 threads (2 per CU), each a run of one
-// sample's rows, so the partial rows stay a few percent of the traffic.
-constexpr int kBwdBlocksTarget = 512;
+// Backward: ~256 blocks of 512 threads (1 per CU), each a run of one
+// sample's rows; with 16-bit rows every row group keeps 4 rows in flight
+// (adaln_bwd_kernel RB = 4), which hides the latency the 2-per-CU launch
+// hid, and the partial rows (B * J * 3 * N floats written, then reduced)
+// are half those of 512 blocks.  bf16 [8192, 1024]: 18.8 us for RB = 4 with
+// 32 blocks per sample against 19.4 us for RB = 1 with 64.
+constexpr int kBwdBlocksTarget = 256;
 // adaln_reduce_kernel stages at most 1024 partial rows of whole samples per
 // round, so one sample may contribute at most 1024 of them.
 constexpr int kMaxBlocksPerSample = 1024;
@@ -671,12 +675,22 @@ int launch_fwd_t(const FwdArgs &a, const Plan &pl, hipStream_t s) {
   adaln_fwd_kernel<TX, TY, K, WPR, VEC, kFwdNT><<<fwd_grid(pl, a.M), S::BLK, 0, s>>>(a);
   return check_launch("nf_adaln_fwd");
 }
+// Backward rows in flight per row group: 4 for 16-bit rows of one 8-element
+// chunk per thread, else 1 (with the next-row prefetch when a thread holds
+// two chunks per row).
+template <typename TX, typename TY, int K>
+constexpr int bwd_batch_rows() {
+  return (sizeof(TX) == 2 && sizeof(TY) == 2 && K == 1) ? 4 : 1;
+}
 template <typename TX, typename TY, bool VEC, int WPR, int K>
 int launch_bwd_t(const BwdArgs &a, int64_t B, hipStream_t s) {
   using S = BwdShape<WPR>;
   const unsigned grid = (unsigned)(B * a.J);
-  // next-row prefetch pays only when a thread holds two chunks per row
-  adaln_bwd_kernel<TX, TY, K, WPR, VEC, kBwdNT, (K > 1)><<<grid, S::BLK, 0, s>>>(a);
+  constexpr int RB = VEC ? bwd_batch_rows<TX, TY, K>() : 1;
+  if constexpr (RB > 1)
+    adaln_bwd_kernel<TX, TY, K, WPR, VEC, kBwdNT, false, 512, RB><<<grid, S::BLK, 0, s>>>(a);
+  else
+    adaln_bwd_kernel<TX, TY, K, WPR, VEC, kBwdNT, (K > 1)><<<grid, S::BLK, 0, s>>>(a);
   return check_launch("nf_adaln_bwd");
 }
 
