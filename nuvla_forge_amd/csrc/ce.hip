@@ -100,6 +100,12 @@ struct OutBuf {
     else if (ok)
       *reinterpret_cast<u32x2 *>(base + off) = v;
   }
+  __device__ __forceinline__ void st128(int64_t off, bool ok, u32x4 v) const {
+    if constexpr (SB)
+      __builtin_amdgcn_raw_buffer_store_b128(v, rsrc, ok ? (uint32_t)off : kOobOffset, 0, 0);
+    else if (ok)
+      *reinterpret_cast<u32x4 *>(base + off) = v;
+  }
 };
 
 inline bool sb_ok(int64_t bytes) { return bytes < ((int64_t)1 << 31) - 64; }
@@ -362,10 +368,20 @@ __global__ __launch_bounds__(kLossThreads) void ce_loss_kernel(
 // chunk, from the transposed product acc = Wc_tile H_tile^T (rows: chunk
 // columns, columns: tokens).  Each lane's TN tokens bring their lse, target
 // and scale in registers.  Writes P [M, ldp] (token rows; columns [Vc, kpad)
-// zero) with one 8-byte store per 4 consecutive chunk columns, and
-// PT [Vc, ldpt] (chunk-column rows; tokens [M, ldpt) zero) with 2-byte
-// stores that the 32 lanes of a half-wave make contiguous.
+// zero) and PT [Vc, ldpt] (chunk-column rows; tokens [M, ldpt) zero).
+//
+// 16-bit tiles of 256 x 256 go through LDS (free once the K loop ends): the
+// lanes write their values as a [token][chunk column] tile, 4 columns (8
+// bytes) at a time, and both outputs then leave as 16-byte row vectors, P
+// from the tile's rows and PT from its columns (8 two-byte LDS reads per
+// vector).  A lane's own values would give 8-byte P stores spread over 64
+// rows and 2-byte PT stores.  Element (t, c) sits at byte
+// t * 512 + 2 * (c ^ prob_swz(t)): the XOR term moves whole 8-element
+// vectors, so rows still read as vectors, and spreads the column reads of a
+// half-wave (tokens 8 l + k, l < 32) over the banks.
 // ---------------------------------------------------------------------------
+__device__ __forceinline__ int prob_swz(int t) { return 8 * (((t >> 3) ^ (t & 7)) & 31); }
+
 template <class C, bool BUF, bool SB>
 __global__ NF_GEMM_BOUNDS(C) void ce_prob_kernel(
     const typename C::TI *Wc, const typename C::TI *H, int64_t Vc, int64_t M, int64_t D,
@@ -390,6 +406,8 @@ __global__ NF_GEMM_BOUNDS(C) void ce_prob_kernel(
   OutBuf<SB> pout, ptout;
   pout.init(P, M * ldp * ES);
   ptout.init(PT, Vc * ldpt * ES);
+  constexpr bool kStaged = ES == 2 && C::BM == 256 && C::BN == 256 && C::NT == 512 &&
+                           C::LDS_BYTES >= 256 * 512;
 #pragma unroll
   for (int j = 0; j < C::TN; ++j) {
     const int64_t tok = m0 + wn * C::WTN + j * 32 + (l & 31);
@@ -412,7 +430,13 @@ __global__ NF_GEMM_BOUNDS(C) void ce_prob_kernel(
 #pragma unroll
         for (int q = 0; q < 4; ++q) pv[q] = static_cast<TI>(p[q]);
         const int64_t c = crow0 + o;
-        if constexpr (ES == 2) {
+        if constexpr (kStaged) {
+          const int t = wn * C::WTN + j * 32 + (l & 31);  // tile token
+          const int cl = wm * C::WTM + 4 * half + o;       // tile chunk column
+          u32x2 packed;
+          __builtin_memcpy(&packed, pv, 8);
+          *reinterpret_cast<u32x2 *>(smem + t * 512 + 2 * (cl ^ prob_swz(t))) = packed;
+        } else if constexpr (ES == 2) {
           u32x2 packed;
           __builtin_memcpy(&packed, pv, 8);
           pout.st64((tok * ldp + c) * ES, tok < M && c < kpad, packed);
@@ -430,6 +454,35 @@ __global__ NF_GEMM_BOUNDS(C) void ce_prob_kernel(
           }
         }
       }
+  }
+  if constexpr (kStaged) {
+    __syncthreads();
+    // Out-of-range tokens and chunk columns hold zeros in the tile; a vector
+    // is stored when its first element is in range (kpad and ldpt are
+    // multiples of 8, so a vector is wholly inside or outside).  Wavefront w
+    // stores tile rows (P) and tile columns (PT) 32 w .. 32 w + 31, two per
+    // instruction, one per half-wave.
+    const int hv = l >> 5, c8 = 8 * (l & 31);
+#pragma unroll 4
+    for (int it = 0; it < 16; ++it) {
+      const int t = 32 * w + 2 * it + hv;
+      const u32x4 v = *reinterpret_cast<const u32x4 *>(smem + t * 512 + 2 * (c8 ^ prob_swz(t)));
+      const int64_t tok = m0 + t, c = v0 + c8;
+      pout.st128((tok * ldp + c) * ES, tok < M && c < kpad, v);
+    }
+#pragma unroll 4
+    for (int it = 0; it < 16; ++it) {
+      const int c = 32 * w + 2 * it + hv;
+      uint16_t e[8];
+#pragma unroll
+      for (int k = 0; k < 8; ++k)
+        e[k] = *reinterpret_cast<const uint16_t *>(smem + (c8 + k) * 512 +
+                                                   2 * (c ^ prob_swz(c8 + k)));
+      u32x4 v;
+      __builtin_memcpy(&v, e, 16);
+      const int64_t crow = v0 + c, tok = m0 + c8;
+      ptout.st128((crow * ldpt + tok) * ES, crow < Vc && tok < ldpt, v);
+    }
   }
 }
 
