@@ -240,8 +240,19 @@ __global__ NF_GEMM_BOUNDS(C) void ce_stats_kernel(
   const int w = threadIdx.x >> 6, wm = w / C::WN, wn = w % C::WN;
   // vocabulary row of acc[i][*][r]: v0 + wm * WTM + 4 * half + i * 32 + 8 * (r / 4) + r % 4
   const int64_t vrow0 = v0 + wm * C::WTM + 4 * half;
-  // offsets >= vlim are past the vocabulary (32-bit: the compares stay cheap)
-  const int vlim = (int)(V - vrow0 < C::WTM ? V - vrow0 : C::WTM);
+  // Rows past the vocabulary (only in a wavefront whose rows reach V) are set
+  // to -inf once, so the max and the sum below need no per-element masks
+  // (masks kept live across both loops would cost 64 scalar register pairs).
+  if (v0 + wm * C::WTM + C::WTM > V) {
+    const int vlim = (int)(V - vrow0 < C::WTM ? V - vrow0 : C::WTM);
+#pragma unroll
+    for (int i = 0; i < C::TM; ++i)
+#pragma unroll
+      for (int j = 0; j < C::TN; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+          if (i * 32 + 8 * (r >> 2) + (r & 3) >= vlim) acc[i][j][r] = -INFINITY;
+  }
 #pragma unroll
   for (int j = 0; j < C::TN; ++j) {
     const int tl = wn * C::WTN + j * 32 + (l & 31);
@@ -250,20 +261,15 @@ __global__ NF_GEMM_BOUNDS(C) void ce_stats_kernel(
 #pragma unroll
     for (int i = 0; i < C::TM; ++i)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int o = i * 32 + 8 * (r >> 2) + (r & 3);
-        mx = fmaxf(mx, o < vlim ? acc[i][j][r] : -INFINITY);
-      }
+      for (int r = 0; r < 16; ++r) mx = fmaxf(mx, acc[i][j][r]);
     mx = fmaxf(mx, __shfl_xor(mx, 32));
+    // a column with no row inside the vocabulary keeps (-inf, 0)
+    const float mref = mx == -INFINITY ? 0.f : mx;
     float s = 0.f;
 #pragma unroll
     for (int i = 0; i < C::TM; ++i)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int o = i * 32 + 8 * (r >> 2) + (r & 3);
-        const float e = exp_f32(acc[i][j][r] - mx);
-        s += o < vlim ? e : 0.f;
-      }
+      for (int r = 0; r < 16; ++r) s += exp_f32(acc[i][j][r] - mref);
     s += __shfl_xor(s, 32);
     if (half == 0) red[wm][tl] = make_float2(mx, s);
 
@@ -408,13 +414,29 @@ __global__ NF_GEMM_BOUNDS(C) void ce_prob_kernel(
   ptout.init(PT, Vc * ldpt * ES);
   constexpr bool kStaged = ES == 2 && C::BM == 256 && C::BN == 256 && C::NT == 512 &&
                            C::LDS_BYTES >= 256 * 512;
+  // Rows past the chunk (only in a wavefront whose rows reach Vc) are set to
+  // -inf once, so their probabilities come out 0 without per-element masks
+  // (masks kept live through the loop would cost 64 scalar register pairs).
+  if (v0 + wm * C::WTM + C::WTM > Vc) {
+    const int vlim = (int)(Vc - crow0 < C::WTM ? Vc - crow0 : C::WTM);
+#pragma unroll
+    for (int i = 0; i < C::TM; ++i)
+#pragma unroll
+      for (int j = 0; j < C::TN; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+          if (i * 32 + 8 * (r >> 2) + (r & 3) >= vlim) acc[i][j][r] = -INFINITY;
+  }
 #pragma unroll
   for (int j = 0; j < C::TN; ++j) {
     const int64_t tok = m0 + wn * C::WTN + j * 32 + (l & 31);
     const int tc = tok < M ? tcol[tok] : -1;
     const float ls = tok < M ? lse[tok] : 0.f;
-    const float sc = tc >= 0 ? inv : 0.f;
-    const int64_t tloc = (int64_t)tc - vbase - crow0;  // target's offset from crow0
+    const bool keep = tc >= 0;  // counted token: P row = inv * (softmax - onehot)
+    // the target's offset from crow0 when it lies in this chunk's Vc columns,
+    // else -1 (a row past Vc may be a later chunk's column: no onehot there)
+    const int64_t tin = (int64_t)tc - vbase;
+    const int tloc = (keep && tin >= 0 && tin < Vc) ? (int)(tin - crow0) : -1;
 #pragma unroll
     for (int i = 0; i < C::TM; ++i)
 #pragma unroll
@@ -424,7 +446,7 @@ __global__ NF_GEMM_BOUNDS(C) void ce_prob_kernel(
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
           const float e = exp_f32(acc[i][j][4 * g + q] - ls) - (tloc == o + q ? 1.f : 0.f);
-          p[q] = (sc != 0.f && crow0 + o + q < Vc) ? e * sc : 0.f;
+          p[q] = keep ? e * inv : 0.f;
         }
         TI pv[4];
 #pragma unroll

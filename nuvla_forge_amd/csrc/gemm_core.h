@@ -465,8 +465,13 @@ __device__ __forceinline__ void mainloop_dtl_ops(const DtlOperand<C, C::ACW> &op
       }
       // the last k-group (in a1, b1) covers the stage hand-over
       if (kt + 1 < nk) {
-        const int64_t later = nk - 2 - kt;  // stages issued beyond kt + 1
-        wait_stage<C>(later < C::STAGES - 2 ? (int)later : C::STAGES - 2);
+        if constexpr (C::STAGES == 2) {
+          // stage kt + 1 is the only one in flight: wait for all of it
+          wait_vm_barrier<0>();
+        } else {
+          const int64_t later = nk - 2 - kt;  // stages issued beyond kt + 1 (>= 0)
+          wait_stage<C>(later < C::STAGES - 2 ? (int)later : C::STAGES - 2);
+        }
         if (kt + C::STAGES < nk) {
           char *re = smem + cur * C::STAGE;
           opa.issue((kt + C::STAGES) * C::BK, re, wave);
