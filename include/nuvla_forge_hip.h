@@ -142,26 +142,57 @@ int nf_adaln_bwd_reduce(void *workspace, size_t workspace_bytes,
                         void *stream);
 
 /* ------------------------------------------------------------------------
- * Chunked cross entropy with the gradient formed during the forward pass.
+ * Chunked cross entropy.
  *   logits = hidden @ weight^T          ([M, V], never materialised)
  *   lse    = logsumexp_v logits         (fp32)
  *   n      = #(targets != ignore_index);  inv = 1 / max(n, 1)
  *   loss   = inv * sum_{valid m} (lse[m] - logits[m, t_m])   (fp32 scalar)
- *   dhidden= inv * (softmax - onehot) @ weight        (fp32 [M, D])
- *   dweight= inv * (softmax - onehot)^T @ hidden      (fp32 [V, D])
- * Ignored rows contribute no loss and no gradient; an all-ignored batch
- * gives loss 0 and zero gradients.  Targets outside [0, V) other than
- * ignore_index are recorded in *bad_targets (device int32, may be NULL)
- * and treated as ignored.
- * `vocab_chunk` columns of the softmax gradient exist at a time (bf16 or
- * fp32 like the inputs), so memory is O(M * vocab_chunk), not O(M * V).
- * Replaces _ChunkedCrossEntropy.forward and the `_ce_fwd_bwd` kernel,
- * nuvla_forge/kernels/chunked_ce.py:49-98 and :120-172 (the reference
- * chunks rows of M; the result does not depend on either chunking beyond
- * fp rounding).
+ *   dhidden= g * inv * (softmax - onehot) @ weight        ([M, D])
+ *   dweight= g * inv * (softmax - onehot)^T @ hidden      ([V, D])
+ * with g the loss's upstream gradient.  Ignored rows contribute no loss and
+ * no gradient; an all-ignored batch gives loss 0 and zero gradients.
+ * Targets outside [0, V) other than ignore_index are counted in
+ * *bad_targets (device int32, may be NULL) and treated as ignored.
  * hidden [M, D] and weight [V, D] are contiguous and share `dtype`
  * (NF_DTYPE_BF16 uses bf16 MFMA with fp32 accumulation, NF_DTYPE_F32 uses
- * fp32 MFMA).  targets is int64 [M].  loss, dhidden, dweight are fp32. */
+ * fp32 MFMA).  targets is int64 [M].
+ *
+ * nf_ce_fwd computes the loss and fills `state` (nf_ce_state_bytes(M),
+ * 16-byte aligned: per-row lse and target column, inv), which the caller
+ * keeps for nf_ce_bwd; `workspace` (nf_ce_fwd_workspace) is scratch.
+ * Replaces _ChunkedCrossEntropy.forward's loss and the lse / loss part of
+ * the `_ce_fwd_bwd` kernel, nuvla_forge/kernels/chunked_ce.py:49-98 and
+ * :120-172.
+ *
+ * nf_ce_bwd forms the gradients from `state`: `vocab_chunk` columns of
+ * (softmax - onehot) exist at a time (bf16 or fp32 like the inputs), so
+ * memory is O(M * vocab_chunk), not O(M * V); the reference chunks rows of
+ * M, and the result does not depend on either chunking beyond fp rounding.
+ * grad_output is a device fp32 scalar (NULL: 1).  dhidden and dweight are
+ * written in dt_hidden and dt_weight (fp32, bf16 or fp16: the callers'
+ * types), already scaled.  Replaces the gradient half of `_ce_fwd_bwd` and
+ * _ChunkedCrossEntropy.backward's scaling and casts, chunked_ce.py:174-182
+ * (the reference forms the fp32 gradients in the forward pass and keeps
+ * them until the backward).
+ * ---------------------------------------------------------------------- */
+size_t nf_ce_state_bytes(int64_t M);
+size_t nf_ce_fwd_workspace(int64_t M, int64_t D, int64_t V, int dtype);
+int nf_ce_fwd(const void *hidden, const void *weight, const int64_t *targets,
+              int64_t M, int64_t D, int64_t V, int64_t ignore_index, int dtype,
+              float *loss, int32_t *bad_targets, void *state,
+              size_t state_bytes, void *workspace, size_t workspace_bytes,
+              void *stream);
+size_t nf_ce_bwd_workspace(int64_t M, int64_t D, int64_t V,
+                           int64_t vocab_chunk, int dtype);
+int nf_ce_bwd(const void *hidden, const void *weight, int64_t M, int64_t D,
+              int64_t V, int64_t vocab_chunk, int dtype, const void *state,
+              size_t state_bytes, const float *grad_output, void *dhidden,
+              int dt_hidden, void *dweight, int dt_weight, void *workspace,
+              size_t workspace_bytes, void *stream);
+
+/* Both in one call, the reference's structure (_ce_fwd_bwd,
+ * chunked_ce.py:49-98): loss and the unscaled fp32 gradients.  `workspace`
+ * (nf_ce_workspace) holds the state and the scratch of both halves. */
 size_t nf_ce_workspace(int64_t M, int64_t D, int64_t V, int64_t vocab_chunk,
                        int dtype);
 int nf_ce_fwd_bwd(const void *hidden, const void *weight,
@@ -170,12 +201,6 @@ int nf_ce_fwd_bwd(const void *hidden, const void *weight,
                   float *loss, float *dhidden, float *dweight,
                   int32_t *bad_targets, void *workspace,
                   size_t workspace_bytes, void *stream);
-
-/* CE backward: dst[i] = (dtype)(src[i] * (*grad_output)) for n fp32 elements,
- * grad_output being a device fp32 scalar.  Replaces the scaling and casts in
- * _ChunkedCrossEntropy.backward, nuvla_forge/kernels/chunked_ce.py:174-182. */
-int nf_scale_cast(const float *src, const float *grad_output, void *dst,
-                  int64_t n, int dtype, void *stream);
 
 /* ------------------------------------------------------------------------
  * Test hook with no counterpart in the reference: C[M, N] (fp32, row stride

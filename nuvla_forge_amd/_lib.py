@@ -46,13 +46,23 @@ SIGNATURES = {
         [_P, _SZ, _P, _P, _I64, _P, _P, _P, _P, _I64, _I64, _I64,
          _I32, _I32, _I32, _I32, _P],
     ),
+    "nf_ce_state_bytes": (_SZ, [_I64]),
+    "nf_ce_fwd_workspace": (_SZ, [_I64, _I64, _I64, _I32]),
+    "nf_ce_fwd": (
+        _I32,
+        [_P, _P, _P, _I64, _I64, _I64, _I64, _I32, _P, _P, _P, _SZ, _P, _SZ, _P],
+    ),
+    "nf_ce_bwd_workspace": (_SZ, [_I64, _I64, _I64, _I64, _I32]),
+    "nf_ce_bwd": (
+        _I32,
+        [_P, _P, _I64, _I64, _I64, _I64, _I32, _P, _SZ, _P, _P, _I32, _P, _I32, _P, _SZ, _P],
+    ),
     "nf_ce_workspace": (_SZ, [_I64, _I64, _I64, _I64, _I32]),
     "nf_ce_fwd_bwd": (
         _I32,
         [_P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I32, _P, _P, _P, _P, _P,
          _SZ, _P],
     ),
-    "nf_scale_cast": (_I32, [_P, _P, _P, _I64, _I32, _P]),
     "nf_gemm_nt": (_I32, [_P, _I64, _P, _I64, _P, _I64, _I64, _I64, _I64, _I32, _P]),
     "nf_gemm_swiglu": (
         _I32, [_P, _I64, _P, _P, _I64, _P, _P, _P, _I64, _I64, _I64, _I64, _I32, _P],

@@ -1,23 +1,27 @@
-// Chunked cross entropy with the gradient formed in the forward pass, on the
-// MFMA GEMM core of gemm_core.h.
+// Chunked cross entropy on the MFMA GEMM core of gemm_core.h, in two calls
+// (all on the caller's stream, fixed reduction orders throughout).
 //
-// Pipeline (all on the caller's stream, fixed reduction orders throughout):
-//   1. transpose  W [V, D] -> Wt [D, ldwt],  H [M, D] -> Ht [D, ldht]
-//      (zero-padded columns), so every GEMM below is K-contiguous (NT).
-//   2. ce_stats:  S^T = W H^T tile by tile; per (vocabulary tile, token) the
+// Forward (nf_ce_fwd):
+//   1. ce_stats:  S^T = W H^T tile by tile; per (vocabulary tile, token) the
 //      max and sum of exp(S - max), plus S[m, t_m] for the target column.
 //      S itself is never stored.
-//   3. ce_lse:    lse[m] = combine of the tile partials (fixed order);
+//   2. ce_lse:    lse[m] = combine of the tile partials (fixed order);
 //                 loss_row[m] = lse - S[m, t_m] for valid rows.
-//   4. ce_loss:   one block: n_valid, loss = sum(loss_row) / max(n, 1),
+//   3. ce_loss:   one block: n_valid, loss = sum(loss_row) / max(n, 1),
 //                 inv = 1 / max(n, 1).
+//   lse, the target columns and inv are the state the backward reads.
+// Backward (nf_ce_bwd, with the loss's grad_output g):
+//   4. transpose  W [V, D] -> Wt [D, ldwt],  H [M, D] -> Ht [D, ldht]
+//      (zero-padded columns), so every GEMM below is K-contiguous (NT).
 //   5. per vocabulary chunk c of `vocab_chunk` columns:
 //      ce_prob:  recompute S_c^T = W_c H^T; P_c = inv * (softmax - onehot)
 //                (0 for ignored rows) in the input type, written row-major
 //                [M, Vc] and transposed [Vc, M];
-//      dW_c  = P_c^T H        (gemm_store, K = M)   -> dweight rows of c
-//      dH   += P_c   W_c      (gemm_store, K = Vc)  -> dhidden (chunk 0
-//                                                     writes, later add)
+//      dW_c  = g * P_c^T H    (gemm_store, K = M)   -> dweight rows of c, in
+//                                                     dweight's type
+//      dH   += P_c   W_c      (gemm_store, K = Vc)  -> an fp32 accumulator;
+//                                                     the last chunk writes
+//                                                     g * dH in dhidden's type
 // Memory is O(M * vocab_chunk) for P; the [M, V] logits never exist.
 #include <type_traits>
 
@@ -111,28 +115,48 @@ struct OutBuf {
 inline bool sb_ok(int64_t bytes) { return bytes < ((int64_t)1 << 31) - 64; }
 
 // ---------------------------------------------------------------------------
-// plain store epilogue, C[m, n] (+)= acc, for one or two independent GEMMs in
-// one launch (the dW and dH products of a vocabulary chunk: each alone is too
-// few 256x256 tiles to fill the chip, together they do).  An accumulating job
-// loads its C tile into the accumulators before the K loop, so the load
-// latency overlaps the first operand copies and the epilogue only stores.
+// plain store epilogue, C[m, n] = scale * (Cin[m, n] + A B^T), for one or two
+// independent GEMMs in one launch (the dW and dH products of a vocabulary
+// chunk: each alone is too few 256x256 tiles to fill the chip, together they
+// do).  A job with Cin loads that fp32 tile into the accumulators before the
+// K loop, so the load latency overlaps the first operand copies and the
+// epilogue only stores.  C has element type cdt (fp32, bf16 or fp16: the
+// last product of a gradient goes straight to the caller's type) and
+// scale, when given, is a device fp32 scalar (the loss's grad_output).
 // ---------------------------------------------------------------------------
 // A job with ksplit > 1 divides K into slices of kslice (a multiple of the
 // stage width): block (tile, s) writes the partial product over slice s to
-// part[s] ([M, N], dense) and splitk_reduce_kernel adds the slices in order.
+// part[s] ([M, N], dense, fp32) and splitk_reduce_kernel adds the slices in
+// order, then Cin, scales and converts.
 template <typename TI>
 struct GemmJob {
   const TI *A;
   const TI *B;
-  float *C;
+  const float *Cin;    // fp32 [M, ldc] added to the product, or null
+  void *C;             // [M, ldc] of cdt
+  const float *scale;  // device scalar multiplying the result, or null
   int64_t lda, ldb, ldc, M, N, K;
-  int accumulate;
+  int cdt;       // NF_DTYPE_F32 / BF16 / F16
   int tiles_m;   // tiles along M
   int tiles;     // blocks of this job: tiles_m * tiles_n * ksplit
   int ksplit;    // K slices (1: no split)
   int64_t kslice;
   float *part;   // [ksplit, M, N] partial products when ksplit > 1
 };
+
+__host__ __device__ inline int dtype_bytes(int dt) { return dt == NF_DTYPE_F32 ? 4 : 2; }
+
+__device__ __forceinline__ uint16_t to_half_bits(float v, int dt) {
+  uint16_t bits;
+  if (dt == NF_DTYPE_BF16) {
+    const bf16 h = static_cast<bf16>(v);
+    __builtin_memcpy(&bits, &h, 2);
+  } else {
+    const f16 h = static_cast<f16>(v);
+    __builtin_memcpy(&bits, &h, 2);
+  }
+  return bits;
+}
 
 template <class C, bool BUF, bool SB>
 __global__ NF_GEMM_BOUNDS(C) void gemm_store_kernel(GemmJob<typename C::TI> j0,
@@ -152,10 +176,14 @@ __global__ NF_GEMM_BOUNDS(C) void gemm_store_kernel(GemmJob<typename C::TI> j0,
   const bool split = j.ksplit > 1;
   const int64_t k0 = ks * j.kslice;
   const int64_t klen = j.K - k0 < j.kslice ? j.K - k0 : j.kslice;
+  // a split block writes its fp32 partial densely; the reduce does the rest
   const int64_t ldc = split ? N : j.ldc;
-  const int accumulate = split ? 0 : j.accumulate;
-  OutBuf<SB> out;
-  out.init(split ? j.part + ks * M * N : j.C, M * ldc * (int64_t)sizeof(float));
+  const int cdt = split ? NF_DTYPE_F32 : j.cdt;
+  const bool preload = !split && j.Cin != nullptr;
+  OutBuf<SB> out, cin;
+  out.init(split ? static_cast<void *>(j.part + ks * M * N) : j.C,
+           M * ldc * (int64_t)dtype_bytes(cdt));
+  cin.init(const_cast<float *>(j.Cin), M * ldc * (int64_t)sizeof(float));
   const int w = threadIdx.x >> 6, wm = w / C::WN, wn = w % C::WN;
   // element (i, jj, r) of this lane sits at byte offset base + i * 32 rows
   // + 8 * (r / 4) + (r % 4) rows + jj * 32 columns
@@ -170,34 +198,52 @@ __global__ NF_GEMM_BOUNDS(C) void gemm_store_kernel(GemmJob<typename C::TI> j0,
       for (int r = 0; r < 16; ++r) {
         const int dr = i * 32 + 8 * (r >> 2) + (r & 3);
         const bool ok = row0 + dr < M && col0 + jj * 32 < N;
-        acc[i][jj][r] = accumulate ? out.ld32(((row0 + dr) * ldc + col0 + jj * 32) * 4, ok)
-                                   : 0.f;
+        acc[i][jj][r] = preload ? cin.ld32(((row0 + dr) * ldc + col0 + jj * 32) * 4, ok) : 0.f;
       }
   gemm::mainloop<C, BUF, false>(j.A + k0, j.lda, j.B + k0, j.ldb, M, N, klen, m0, n0, smem, acc);
+  const float g = (!split && j.scale) ? *j.scale : 1.f;
+  if (cdt == NF_DTYPE_F32) {
 #pragma unroll
-  for (int i = 0; i < C::TM; ++i)
+    for (int i = 0; i < C::TM; ++i)
 #pragma unroll
-    for (int jj = 0; jj < C::TN; ++jj)
+      for (int jj = 0; jj < C::TN; ++jj)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int dr = i * 32 + 8 * (r >> 2) + (r & 3);
-        const bool ok = row0 + dr < M && col0 + jj * 32 < N;
-        out.st32(((row0 + dr) * ldc + col0 + jj * 32) * 4, ok, acc[i][jj][r]);
-      }
+        for (int r = 0; r < 16; ++r) {
+          const int dr = i * 32 + 8 * (r >> 2) + (r & 3);
+          const bool ok = row0 + dr < M && col0 + jj * 32 < N;
+          out.st32(((row0 + dr) * ldc + col0 + jj * 32) * 4, ok, acc[i][jj][r] * g);
+        }
+  } else {
+#pragma unroll
+    for (int i = 0; i < C::TM; ++i)
+#pragma unroll
+      for (int jj = 0; jj < C::TN; ++jj)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int dr = i * 32 + 8 * (r >> 2) + (r & 3);
+          const bool ok = row0 + dr < M && col0 + jj * 32 < N;
+          out.st16(((row0 + dr) * ldc + col0 + jj * 32) * 2, ok,
+                   to_half_bits(acc[i][jj][r] * g, cdt));
+        }
+  }
 }
 
-// C[m, n] (+)= sum over s = 0 .. S-1 of part[s, m, n], in that order.
+// C[m, n] = scale * (Cin[m, n] + sum over s = 0 .. S-1 of part[s, m, n]),
+// the slices added in order; C of element type cdt.
 __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float *__restrict__ part,
                                                             int S, int64_t M, int64_t N,
-                                                            float *C, int64_t ldc,
-                                                            int accumulate) {
+                                                            const float *Cin, void *C,
+                                                            int64_t ldc, int cdt,
+                                                            const float *scale) {
   const int64_t total = M * N;
+  const float g = scale ? *scale : 1.f;
   for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total;
        i += (int64_t)gridDim.x * 256) {
     float a = 0.f;
     for (int k = 0; k < S; ++k) a += part[k * total + i];
-    float *p = C + (i / N) * ldc + i % N;
-    *p = accumulate ? *p + a : a;
+    const int64_t o = (i / N) * ldc + i % N;
+    if (Cin) a = Cin[o] + a;
+    store_dyn(C, cdt, o, a * g);
   }
 }
 
@@ -569,27 +615,6 @@ __global__ __launch_bounds__(256) void transpose16_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// backward scale + cast
-// ---------------------------------------------------------------------------
-template <typename T, bool VEC>
-__global__ __launch_bounds__(256) void scale_cast_kernel(
-    const float *__restrict__ src, const float *__restrict__ g,
-    T *__restrict__ dst, int64_t n) {
-  const float gv = *g;
-  const int64_t nchunks = (n + 7) >> 3;
-  for (int64_t c = (int64_t)blockIdx.x * 256 + threadIdx.x; c < nchunks;
-       c += (int64_t)gridDim.x * 256) {
-    const int64_t rem = n - c * 8;
-    const int valid = rem >= 8 ? 8 : (int)rem;
-    float v[8];
-    load8<float, VEC>(src + c * 8, valid, v);
-#pragma unroll
-    for (int i = 0; i < 8; ++i) v[i] *= gv;
-    store8<T, VEC>(dst + c * 8, valid, v);
-  }
-}
-
-// ---------------------------------------------------------------------------
 // host side
 // ---------------------------------------------------------------------------
 inline int64_t round_up(int64_t x, int64_t m) { return (x + m - 1) / m * m; }
@@ -643,11 +668,41 @@ inline SplitPlan chunk_split(int64_t vc, int64_t M, int64_t D) {
   return p;
 }
 
-struct Layout {
-  int64_t ldwt, ldht, vc, ldp, ntiles;
-  size_t off_wt, off_ht, off_stats, off_tgt, off_lse, off_tcol, off_loss, off_flags,
-      off_scal, off_p, off_pt, off_part, total;
+// Per-row state the backward reads: lse [M], the target column [M] (-1: the
+// row has no gradient) and the scalars (inv = 1 / max(n_valid, 1)).
+struct StateLayout {
+  size_t off_lse, off_tcol, off_scal, total;
 };
+inline StateLayout state_layout(int64_t M) {
+  StateLayout L{};
+  size_t o = 0;
+  auto take = [&](size_t bytes) { const size_t at = o; o = align256(o + bytes); return at; };
+  L.off_lse = take((size_t)M * sizeof(float));
+  L.off_tcol = take((size_t)M * sizeof(int));
+  L.off_scal = take(64);
+  L.total = o;
+  return L;
+}
+
+// Forward scratch: per (vocabulary tile, token) stats, the target logits,
+// the row losses and the row flags.
+struct FwdLayout {
+  int64_t ntiles;
+  size_t off_stats, off_tgt, off_loss, off_flags, total;
+};
+inline FwdLayout fwd_layout(int64_t M, int64_t V, int es) {
+  FwdLayout L{};
+  const int64_t bm = es == 2 ? MainCfg<bf16>::BM : MainCfg<float>::BM;
+  L.ntiles = (V + bm - 1) / bm;  // vocabulary tiles
+  size_t o = 0;
+  auto take = [&](size_t bytes) { const size_t at = o; o = align256(o + bytes); return at; };
+  L.off_stats = take((size_t)L.ntiles * M * sizeof(float2));  // [ntiles][M]
+  L.off_tgt = take((size_t)M * sizeof(float));
+  L.off_loss = take((size_t)M * sizeof(float));
+  L.off_flags = take((size_t)M * sizeof(int));
+  L.total = o;
+  return L;
+}
 
 template <class C>
 inline size_t partial_bytes(int64_t M, int64_t D, int64_t V, int64_t vc) {
@@ -663,42 +718,41 @@ inline size_t partial_bytes(int64_t M, int64_t D, int64_t V, int64_t vc) {
   return most;
 }
 
-inline Layout make_layout(int64_t M, int64_t D, int64_t V, int64_t vocab_chunk, int es) {
-  Layout L{};
+// Backward scratch: W^T, H^T, one chunk's P and P^T, split-K partials, and
+// the fp32 dH accumulator when the vocabulary takes more than one chunk.
+struct BwdLayout {
+  int64_t ldwt, ldht, vc, ldp;
+  size_t off_wt, off_ht, off_p, off_pt, off_part, off_dh, total;
+};
+inline BwdLayout bwd_layout(int64_t M, int64_t D, int64_t V, int64_t vocab_chunk, int es) {
+  BwdLayout L{};
   L.ldwt = round_up(V, 8);
   L.ldht = round_up(M, 8);
   L.vc = round_up(vocab_chunk < V ? vocab_chunk : V, 8);
   L.ldp = L.vc;
-  L.ntiles = (V + MainCfg<bf16>::BM - 1) / MainCfg<bf16>::BM;  // vocabulary tiles
-  if (es == 4) L.ntiles = (V + MainCfg<float>::BM - 1) / MainCfg<float>::BM;
   const size_t part = es == 2 ? partial_bytes<MainCfg<bf16>>(M, D, V, L.vc)
                               : partial_bytes<MainCfg<float>>(M, D, V, L.vc);
   size_t o = 0;
   auto take = [&](size_t bytes) { const size_t at = o; o = align256(o + bytes); return at; };
   L.off_wt = take((size_t)D * L.ldwt * es);
   L.off_ht = take((size_t)D * L.ldht * es);
-  L.off_stats = take((size_t)L.ntiles * M * sizeof(float2));  // [ntiles][M]
-  L.off_tgt = take((size_t)M * sizeof(float));
-  L.off_lse = take((size_t)M * sizeof(float));
-  L.off_tcol = take((size_t)M * sizeof(int));
-  L.off_loss = take((size_t)M * sizeof(float));
-  L.off_flags = take((size_t)M * sizeof(int));
-  L.off_scal = take(64);
   L.off_p = take((size_t)M * L.ldp * es);
   L.off_pt = take((size_t)L.vc * L.ldht * es);
   L.off_part = take(part);
+  L.off_dh = take(V > L.vc ? (size_t)M * D * sizeof(float) : 0);
   L.total = o;
   return L;
 }
 
 template <class C>
 GemmJob<typename C::TI> make_job(const typename C::TI *A, int64_t lda, const typename C::TI *B,
-                                 int64_t ldb, float *Cout, int64_t ldc, int64_t M, int64_t N,
-                                 int64_t K, int accumulate) {
+                                 int64_t ldb, const float *Cin, void *Cout, int cdt,
+                                 const float *scale, int64_t ldc, int64_t M, int64_t N,
+                                 int64_t K) {
   GemmJob<typename C::TI> j;
-  j.A = A; j.B = B; j.C = Cout;
+  j.A = A; j.B = B; j.Cin = Cin; j.C = Cout; j.scale = scale;
   j.lda = lda; j.ldb = ldb; j.ldc = ldc; j.M = M; j.N = N; j.K = K;
-  j.accumulate = accumulate;
+  j.cdt = cdt;
   j.tiles_m = (int)((M + C::BM - 1) / C::BM);
   j.tiles = j.tiles_m * (int)((N + C::BN - 1) / C::BN);
   j.ksplit = 1;
@@ -711,8 +765,17 @@ template <typename TI>
 bool job_buf_ok(const GemmJob<TI> &j) {
   return j.tiles == 0 || (buf_ok<TI>(j.A, j.lda, j.M, j.K) && buf_ok<TI>(j.B, j.ldb, j.N, j.K));
 }
+// every buffer the epilogue addresses through a 32-bit offset is under 2 GiB
+template <typename TI>
+bool job_sb_ok(const GemmJob<TI> &j) {
+  if (j.tiles == 0) return true;
+  if (j.ksplit > 1) return sb_ok(j.M * j.N * (int64_t)sizeof(float));
+  return sb_ok(j.M * j.ldc * (int64_t)dtype_bytes(j.cdt)) &&
+         (!j.Cin || sb_ok(j.M * j.ldc * (int64_t)sizeof(float)));
+}
 
-// Both jobs in one grid (j1 may be empty: tiles == 0).
+// Both jobs in one grid (j1 may be empty: tiles == 0), then the split-K
+// reductions of a split job.
 template <class C>
 int launch_gemm_store(const GemmJob<typename C::TI> &j0, const GemmJob<typename C::TI> &j1,
                       hipStream_t s) {
@@ -720,8 +783,7 @@ int launch_gemm_store(const GemmJob<typename C::TI> &j0, const GemmJob<typename 
   if (total == 0) return NF_OK;
   if (total > 0x7fffffffLL) return set_error(NF_ERR_ARG, "gemm: too many tiles");
   const dim3 grid((unsigned)total);
-  const bool sb = (j0.tiles == 0 || sb_ok(j0.M * j0.ldc * (int64_t)sizeof(float))) &&
-                  (j1.tiles == 0 || sb_ok(j1.M * j1.ldc * (int64_t)sizeof(float)));
+  const bool sb = job_sb_ok(j0) && job_sb_ok(j1);
   const bool buf = job_buf_ok(j0) && job_buf_ok(j1);
   if (buf && sb)
     gemm_store_kernel<C, true, true><<<grid, C::NT, 0, s>>>(j0, j1);
@@ -729,7 +791,17 @@ int launch_gemm_store(const GemmJob<typename C::TI> &j0, const GemmJob<typename 
     gemm_store_kernel<C, true, false><<<grid, C::NT, 0, s>>>(j0, j1);
   else
     gemm_store_kernel<C, false, false><<<grid, C::NT, 0, s>>>(j0, j1);
-  return check_launch("gemm_store");
+  if (int e = check_launch("gemm_store")) return e;
+  for (const auto *jp : {&j0, &j1}) {
+    if (jp->tiles == 0 || jp->ksplit <= 1) continue;
+    int64_t blocks = (jp->M * jp->N + 255) / 256;
+    if (blocks > 2048) blocks = 2048;
+    splitk_reduce_kernel<<<(unsigned)blocks, 256, 0, s>>>(jp->part, jp->ksplit, jp->M, jp->N,
+                                                         jp->Cin, jp->C, jp->ldc, jp->cdt,
+                                                         jp->scale);
+    if (int e = check_launch("splitk_reduce")) return e;
+  }
+  return NF_OK;
 }
 
 template <typename T>
@@ -745,30 +817,24 @@ int launch_transpose(const void *in, int64_t R, int64_t Cn, int64_t ldi, void *o
   return check_launch("transpose");
 }
 
+// Forward: stats over the whole vocabulary, per-row lse and loss, the mean.
+// Writes loss, the state (lse, target columns, inv) and the bad-target count.
 template <typename TI>
-int ce_run(const TI *H, const TI *W, const int64_t *targets, int64_t M, int64_t D,
-           int64_t V, int64_t ignore_index, int64_t vocab_chunk, float *loss,
-           float *dH, float *dW, int32_t *bad, char *ws, hipStream_t s) {
+int ce_fwd_run(const TI *H, const TI *W, const int64_t *targets, int64_t M, int64_t D,
+               int64_t V, int64_t ignore_index, float *loss, int32_t *bad, char *state,
+               char *ws, hipStream_t s) {
   using C = MainCfg<TI>;
-  const Layout L = make_layout(M, D, V, vocab_chunk, sizeof(TI));
-  TI *Wt = reinterpret_cast<TI *>(ws + L.off_wt);
-  TI *Ht = reinterpret_cast<TI *>(ws + L.off_ht);
+  const StateLayout S = state_layout(M);
+  const FwdLayout L = fwd_layout(M, V, sizeof(TI));
+  float *lse = reinterpret_cast<float *>(state + S.off_lse);
+  int *tcol = reinterpret_cast<int *>(state + S.off_tcol);
+  float *inv = reinterpret_cast<float *>(state + S.off_scal);
   float2 *stats = reinterpret_cast<float2 *>(ws + L.off_stats);
   float *tgt = reinterpret_cast<float *>(ws + L.off_tgt);
-  float *lse = reinterpret_cast<float *>(ws + L.off_lse);
-  int *tcol = reinterpret_cast<int *>(ws + L.off_tcol);
   float *loss_row = reinterpret_cast<float *>(ws + L.off_loss);
   int *flags = reinterpret_cast<int *>(ws + L.off_flags);
-  float *inv = reinterpret_cast<float *>(ws + L.off_scal);
-  TI *P = reinterpret_cast<TI *>(ws + L.off_p);
-  TI *PT = reinterpret_cast<TI *>(ws + L.off_pt);
   int e;
-
-  using U = typename std::conditional<sizeof(TI) == 2, uint16_t, uint32_t>::type;
-  if ((e = launch_transpose<U>(W, V, D, D, Wt, L.ldwt, s))) return e;
-  if ((e = launch_transpose<U>(H, M, D, D, Ht, L.ldht, s))) return e;
-
-  // stats: blocks (vocabulary tile, token tile); the product is W H^T
+  // blocks (vocabulary tile, token tile); the product is W H^T
   const bool vk = buf_ok<TI>(H, D, M, D) && buf_ok<TI>(W, D, V, D);
   const int mtiles = (int)((M + C::BN - 1) / C::BN);
   const unsigned gs = (unsigned)(L.ntiles * mtiles);
@@ -779,13 +845,40 @@ int ce_run(const TI *H, const TI *W, const int64_t *targets, int64_t M, int64_t 
     ce_stats_kernel<C, false><<<gs, C::NT, 0, s>>>(W, H, V, M, D, targets, stats, tgt,
                                                    (int)L.ntiles, mtiles);
   if ((e = check_launch("ce_stats"))) return e;
-
   ce_lse_kernel<<<(unsigned)((M + kLseRows - 1) / kLseRows), kLseRows * kLseParts, 0, s>>>(
       stats, (int)L.ntiles, tgt, targets, M, V, ignore_index, lse, tcol, loss_row, flags);
   if ((e = check_launch("ce_lse"))) return e;
   ce_loss_kernel<<<1, kLossThreads, 0, s>>>(loss_row, flags, M, loss, inv, bad);
-  if ((e = check_launch("ce_loss"))) return e;
+  return check_launch("ce_loss");
+}
 
+// Backward: per vocabulary chunk, P = inv * (softmax - onehot) from the
+// saved lse, then dW_c = g * P_c^T H and dH (+)= P_c W_c; the last chunk's dH
+// and every dW chunk are written scaled, in the caller's element types.
+template <typename TI>
+int ce_bwd_run(const TI *H, const TI *W, int64_t M, int64_t D, int64_t V, int64_t vocab_chunk,
+               const char *state, const float *g, void *dH, int dt_h, void *dW, int dt_w,
+               char *ws, hipStream_t s) {
+  using C = MainCfg<TI>;
+  const StateLayout S = state_layout(M);
+  const BwdLayout L = bwd_layout(M, D, V, vocab_chunk, sizeof(TI));
+  const float *lse = reinterpret_cast<const float *>(state + S.off_lse);
+  const int *tcol = reinterpret_cast<const int *>(state + S.off_tcol);
+  const float *inv = reinterpret_cast<const float *>(state + S.off_scal);
+  TI *Wt = reinterpret_cast<TI *>(ws + L.off_wt);
+  TI *Ht = reinterpret_cast<TI *>(ws + L.off_ht);
+  TI *P = reinterpret_cast<TI *>(ws + L.off_p);
+  TI *PT = reinterpret_cast<TI *>(ws + L.off_pt);
+  float *part = reinterpret_cast<float *>(ws + L.off_part);
+  float *dh_acc = reinterpret_cast<float *>(ws + L.off_dh);  // used when V > vc
+  int e;
+
+  using U = typename std::conditional<sizeof(TI) == 2, uint16_t, uint32_t>::type;
+  if ((e = launch_transpose<U>(W, V, D, D, Wt, L.ldwt, s))) return e;
+  if ((e = launch_transpose<U>(H, M, D, D, Ht, L.ldht, s))) return e;
+
+  const bool vk = buf_ok<TI>(H, D, M, D) && buf_ok<TI>(W, D, V, D);
+  const int mtiles = (int)((M + C::BN - 1) / C::BN);
   for (int64_t vb = 0; vb < V; vb += L.vc) {
     const int64_t vc = (V - vb < L.vc) ? V - vb : L.vc;  // columns in this chunk
     const int64_t kpad = round_up(vc, 8);
@@ -808,12 +901,16 @@ int ce_run(const TI *H, const TI *W, const int64_t *targets, int64_t M, int64_t 
                                                            P, L.ldp, kpad, PT, L.ldht, vtiles,
                                                            mtiles);
     if ((e = check_launch("ce_prob"))) return e;
-    // dW[vb:vb+vc, :] = P_c^T H   (K = tokens, zero-padded to ldht) and
-    // dH += P_c W_c               (K = chunk columns, zero-padded to kpad)
-    auto jw = make_job<C>(PT, L.ldht, Ht, L.ldht, dW + vb * D, D, vc, D, L.ldht, 0);
-    auto jh = make_job<C>(P, L.ldp, Wt + vb, L.ldwt, dH, D, M, D, kpad, vb > 0 ? 1 : 0);
+    // dW[vb:vb+vc, :] = g * P_c^T H   (K = tokens, zero-padded to ldht), final;
+    // dH (+)= P_c W_c                 (K = chunk columns, zero-padded to kpad)
+    // into the fp32 accumulator, the last chunk scaled into dH itself
+    const bool first = vb == 0, last = vb + L.vc >= V;
+    char *dw_c = static_cast<char *>(dW) + vb * D * dtype_bytes(dt_w);
+    auto jw = make_job<C>(PT, L.ldht, Ht, L.ldht, nullptr, dw_c, dt_w, g, D, vc, D, L.ldht);
+    auto jh = make_job<C>(P, L.ldp, Wt + vb, L.ldwt, first ? nullptr : dh_acc,
+                          last ? dH : static_cast<void *>(dh_acc),
+                          last ? dt_h : NF_DTYPE_F32, last ? g : nullptr, D, M, D, kpad);
     const SplitPlan sp = chunk_split<C>(vc, M, D);
-    float *part = reinterpret_cast<float *>(ws + L.off_part);
     for (auto *jp : {&jw, &jh}) {
       const Split &q = jp == &jw ? sp.w : sp.h;
       if (q.S > 1) {
@@ -824,14 +921,6 @@ int ce_run(const TI *H, const TI *W, const int64_t *targets, int64_t M, int64_t 
       }
     }
     if ((e = launch_gemm_store<C>(jw, jh, s))) return e;
-    for (const auto *jp : {&jw, &jh}) {
-      if (jp->ksplit <= 1) continue;
-      int64_t blocks = (jp->M * D + 255) / 256;
-      if (blocks > 2048) blocks = 2048;
-      splitk_reduce_kernel<<<(unsigned)blocks, 256, 0, s>>>(jp->part, jp->ksplit, jp->M, D,
-                                                           jp->C, D, jp->accumulate);
-      if ((e = check_launch("splitk_reduce"))) return e;
-    }
   }
   return NF_OK;
 }
@@ -842,11 +931,101 @@ int ce_run(const TI *H, const TI *W, const int64_t *targets, int64_t M, int64_t 
 using namespace nf;
 using namespace nf::ce;
 
-extern "C" size_t nf_ce_workspace(int64_t M, int64_t D, int64_t V, int64_t vocab_chunk,
-                                  int dtype) {
+namespace {
+int ce_check_shape(const char *fn, int64_t M, int64_t D, int64_t V) {
+  if (M <= 0 || D <= 0 || V <= 0)
+    return set_error(NF_ERR_ARG, "%s: bad shape M=%lld D=%lld V=%lld", fn, (long long)M,
+                     (long long)D, (long long)V);
+  if (V > 0x7fffffffLL || M > 0x7fffffffLL)
+    return set_error(NF_ERR_ARG, "%s: M or V exceeds int32", fn);
+  return NF_OK;
+}
+int ce_check_dtype(const char *fn, int dtype) {
+  if (dtype != NF_DTYPE_BF16 && dtype != NF_DTYPE_F32)
+    return set_error(NF_ERR_DTYPE, "%s: dtype %d unsupported (bf16 or f32)", fn, dtype);
+  return NF_OK;
+}
+size_t es_of(int dtype) { return dtype == NF_DTYPE_BF16 ? 2 : 4; }
+}  // namespace
+
+extern "C" size_t nf_ce_state_bytes(int64_t M) {
+  return M > 0 ? state_layout(M).total : 0;
+}
+
+extern "C" size_t nf_ce_fwd_workspace(int64_t M, int64_t D, int64_t V, int dtype) {
+  if (M <= 0 || D <= 0 || V <= 0) return 0;
+  if (dtype != NF_DTYPE_BF16 && dtype != NF_DTYPE_F32) return 0;
+  return fwd_layout(M, V, (int)es_of(dtype)).total;
+}
+
+extern "C" size_t nf_ce_bwd_workspace(int64_t M, int64_t D, int64_t V, int64_t vocab_chunk,
+                                      int dtype) {
   if (M <= 0 || D <= 0 || V <= 0 || vocab_chunk <= 0) return 0;
   if (dtype != NF_DTYPE_BF16 && dtype != NF_DTYPE_F32) return 0;
-  return make_layout(M, D, V, vocab_chunk, dtype == NF_DTYPE_BF16 ? 2 : 4).total;
+  return bwd_layout(M, D, V, vocab_chunk, (int)es_of(dtype)).total;
+}
+
+extern "C" int nf_ce_fwd(const void *hidden, const void *weight, const int64_t *targets,
+                         int64_t M, int64_t D, int64_t V, int64_t ignore_index, int dtype,
+                         float *loss, int32_t *bad_targets, void *state, size_t state_bytes,
+                         void *workspace, size_t workspace_bytes, void *stream) {
+  if (int e = ce_check_shape("nf_ce_fwd", M, D, V)) return e;
+  if (!hidden || !weight || !targets || !loss || !state)
+    return set_error(NF_ERR_ARG, "nf_ce_fwd: null pointer");
+  if (int e = ce_check_dtype("nf_ce_fwd", dtype)) return e;
+  const size_t need_s = nf_ce_state_bytes(M), need = nf_ce_fwd_workspace(M, D, V, dtype);
+  if (state_bytes < need_s || !aligned16(state))
+    return set_error(NF_ERR_WORKSPACE, "nf_ce_fwd: state %zu bytes < required %zu",
+                     state_bytes, need_s);
+  if (!workspace || workspace_bytes < need || !aligned16(workspace))
+    return set_error(NF_ERR_WORKSPACE, "nf_ce_fwd: workspace %zu bytes < required %zu",
+                     workspace_bytes, need);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  char *st = static_cast<char *>(state), *ws = static_cast<char *>(workspace);
+  if (dtype == NF_DTYPE_BF16)
+    return ce_fwd_run<bf16>((const bf16 *)hidden, (const bf16 *)weight, targets, M, D, V,
+                            ignore_index, loss, bad_targets, st, ws, s);
+  return ce_fwd_run<float>((const float *)hidden, (const float *)weight, targets, M, D, V,
+                           ignore_index, loss, bad_targets, st, ws, s);
+}
+
+extern "C" int nf_ce_bwd(const void *hidden, const void *weight, int64_t M, int64_t D,
+                         int64_t V, int64_t vocab_chunk, int dtype, const void *state,
+                         size_t state_bytes, const float *grad_output, void *dhidden,
+                         int dt_hidden, void *dweight, int dt_weight, void *workspace,
+                         size_t workspace_bytes, void *stream) {
+  if (int e = ce_check_shape("nf_ce_bwd", M, D, V)) return e;
+  if (vocab_chunk <= 0) return set_error(NF_ERR_ARG, "nf_ce_bwd: vocab_chunk must be > 0");
+  if (!hidden || !weight || !state || !dhidden || !dweight)
+    return set_error(NF_ERR_ARG, "nf_ce_bwd: null pointer");
+  if (int e = ce_check_dtype("nf_ce_bwd", dtype)) return e;
+  if (!is_dtype(dt_hidden) || !is_dtype(dt_weight))
+    return set_error(NF_ERR_DTYPE, "nf_ce_bwd: gradient dtypes %d, %d", dt_hidden, dt_weight);
+  const size_t need_s = nf_ce_state_bytes(M), need = nf_ce_bwd_workspace(M, D, V, vocab_chunk,
+                                                                         dtype);
+  if (state_bytes < need_s || !aligned16(state))
+    return set_error(NF_ERR_WORKSPACE, "nf_ce_bwd: state %zu bytes < required %zu",
+                     state_bytes, need_s);
+  if (!workspace || workspace_bytes < need || !aligned16(workspace))
+    return set_error(NF_ERR_WORKSPACE, "nf_ce_bwd: workspace %zu bytes < required %zu",
+                     workspace_bytes, need);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const char *st = static_cast<const char *>(state);
+  char *ws = static_cast<char *>(workspace);
+  if (dtype == NF_DTYPE_BF16)
+    return ce_bwd_run<bf16>((const bf16 *)hidden, (const bf16 *)weight, M, D, V, vocab_chunk, st,
+                            grad_output, dhidden, dt_hidden, dweight, dt_weight, ws, s);
+  return ce_bwd_run<float>((const float *)hidden, (const float *)weight, M, D, V, vocab_chunk,
+                           st, grad_output, dhidden, dt_hidden, dweight, dt_weight, ws, s);
+}
+
+// one call: [state | forward and backward scratch, overlapped]
+extern "C" size_t nf_ce_workspace(int64_t M, int64_t D, int64_t V, int64_t vocab_chunk,
+                                  int dtype) {
+  const size_t f = nf_ce_fwd_workspace(M, D, V, dtype);
+  const size_t b = nf_ce_bwd_workspace(M, D, V, vocab_chunk, dtype);
+  if (!f || !b) return 0;
+  return nf_ce_state_bytes(M) + (f > b ? f : b);
 }
 
 extern "C" int nf_ce_fwd_bwd(const void *hidden, const void *weight, const int64_t *targets,
@@ -854,56 +1033,22 @@ extern "C" int nf_ce_fwd_bwd(const void *hidden, const void *weight, const int64
                              int64_t vocab_chunk, int dtype, float *loss, float *dhidden,
                              float *dweight, int32_t *bad_targets, void *workspace,
                              size_t workspace_bytes, void *stream) {
-  if (M <= 0 || D <= 0 || V <= 0 || vocab_chunk <= 0)
-    return set_error(NF_ERR_ARG, "nf_ce_fwd_bwd: bad shape M=%lld D=%lld V=%lld chunk=%lld",
-                     (long long)M, (long long)D, (long long)V, (long long)vocab_chunk);
-  if (V > 0x7fffffffLL || M > 0x7fffffffLL)
-    return set_error(NF_ERR_ARG, "nf_ce_fwd_bwd: M or V exceeds int32");
+  if (int e = ce_check_shape("nf_ce_fwd_bwd", M, D, V)) return e;
+  if (vocab_chunk <= 0) return set_error(NF_ERR_ARG, "nf_ce_fwd_bwd: vocab_chunk must be > 0");
   if (!hidden || !weight || !targets || !loss || !dhidden || !dweight)
     return set_error(NF_ERR_ARG, "nf_ce_fwd_bwd: null pointer");
-  if (dtype != NF_DTYPE_BF16 && dtype != NF_DTYPE_F32)
-    return set_error(NF_ERR_DTYPE, "nf_ce_fwd_bwd: dtype %d unsupported (bf16 or f32)", dtype);
+  if (int e = ce_check_dtype("nf_ce_fwd_bwd", dtype)) return e;
   const size_t need = nf_ce_workspace(M, D, V, vocab_chunk, dtype);
   if (!workspace || workspace_bytes < need || !aligned16(workspace))
     return set_error(NF_ERR_WORKSPACE, "nf_ce_fwd_bwd: workspace %zu bytes < required %zu",
                      workspace_bytes, need);
-  hipStream_t s = static_cast<hipStream_t>(stream);
+  const size_t sb = nf_ce_state_bytes(M);
   char *ws = static_cast<char *>(workspace);
-  if (dtype == NF_DTYPE_BF16)
-    return ce_run<bf16>((const bf16 *)hidden, (const bf16 *)weight, targets, M, D, V,
-                        ignore_index, vocab_chunk, loss, dhidden, dweight, bad_targets, ws, s);
-  return ce_run<float>((const float *)hidden, (const float *)weight, targets, M, D, V,
-                       ignore_index, vocab_chunk, loss, dhidden, dweight, bad_targets, ws, s);
-}
-
-extern "C" int nf_scale_cast(const float *src, const float *grad_output, void *dst, int64_t n,
-                             int dtype, void *stream) {
-  if (n < 0) return set_error(NF_ERR_ARG, "nf_scale_cast: n < 0");
-  if (n == 0) return NF_OK;
-  if (!src || !grad_output || !dst) return set_error(NF_ERR_ARG, "nf_scale_cast: null pointer");
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  const bool vec = aligned16(src) && aligned16(dst);
-  const int64_t nchunks = (n + 7) / 8;
-  int64_t blocks = (nchunks + 255) / 256;
-  if (blocks > 4096) blocks = 4096;
-  const unsigned g = (unsigned)blocks;
-  switch (dtype) {
-    case NF_DTYPE_F32:
-      if (vec) scale_cast_kernel<float, true><<<g, 256, 0, s>>>(src, grad_output, (float *)dst, n);
-      else scale_cast_kernel<float, false><<<g, 256, 0, s>>>(src, grad_output, (float *)dst, n);
-      break;
-    case NF_DTYPE_BF16:
-      if (vec) scale_cast_kernel<bf16, true><<<g, 256, 0, s>>>(src, grad_output, (bf16 *)dst, n);
-      else scale_cast_kernel<bf16, false><<<g, 256, 0, s>>>(src, grad_output, (bf16 *)dst, n);
-      break;
-    case NF_DTYPE_F16:
-      if (vec) scale_cast_kernel<f16, true><<<g, 256, 0, s>>>(src, grad_output, (f16 *)dst, n);
-      else scale_cast_kernel<f16, false><<<g, 256, 0, s>>>(src, grad_output, (f16 *)dst, n);
-      break;
-    default:
-      return set_error(NF_ERR_DTYPE, "nf_scale_cast: dtype %d", dtype);
-  }
-  return check_launch("nf_scale_cast");
+  if (int e = nf_ce_fwd(hidden, weight, targets, M, D, V, ignore_index, dtype, loss,
+                        bad_targets, ws, sb, ws + sb, workspace_bytes - sb, stream))
+    return e;
+  return nf_ce_bwd(hidden, weight, M, D, V, vocab_chunk, dtype, ws, sb, nullptr, dhidden,
+                   NF_DTYPE_F32, dweight, NF_DTYPE_F32, ws + sb, workspace_bytes - sb, stream);
 }
 
 extern "C" int nf_gemm_nt(const void *A, int64_t lda, const void *B, int64_t ldb, float *C,
@@ -921,13 +1066,17 @@ extern "C" int nf_gemm_nt(const void *A, int64_t lda, const void *B, int64_t ldb
     using C16 = MainCfg<bf16>;
     const GemmJob<bf16> none{};
     return launch_gemm_store<C16>(
-        make_job<C16>((const bf16 *)A, lda, (const bf16 *)B, ldb, C, ldc, M, N, K, 0), none, s);
+        make_job<C16>((const bf16 *)A, lda, (const bf16 *)B, ldb, nullptr, C, NF_DTYPE_F32,
+                      nullptr, ldc, M, N, K),
+        none, s);
   }
   if (dtype == NF_DTYPE_F32) {
     using C32 = MainCfg<float>;
     const GemmJob<float> none{};
     return launch_gemm_store<C32>(
-        make_job<C32>((const float *)A, lda, (const float *)B, ldb, C, ldc, M, N, K, 0), none, s);
+        make_job<C32>((const float *)A, lda, (const float *)B, ldb, nullptr, C, NF_DTYPE_F32,
+                      nullptr, ldc, M, N, K),
+        none, s);
   }
   return set_error(NF_ERR_DTYPE, "nf_gemm_nt: dtype %d unsupported", dtype);
 }

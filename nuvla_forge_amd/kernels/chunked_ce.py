@@ -7,13 +7,17 @@ returns 6 values, chunked_ce.py:120-182) and the same public
 ``chunked_cross_entropy(hidden, lm_weight, targets, chunk_size=1024,
 ignore_index=-100, force_reference=False)`` (chunked_ce.py:185-208).
 
-Like the reference, the gradient is formed during the forward pass and the
-backward only scales it by ``grad_output`` and casts to the input dtypes.
-The device path is one call, ``nf_ce_fwd_bwd``: logits tiles are produced on
-bf16 (or fp32) MFMA, reduced to per-row log-sum-exp without being stored, and
-recomputed one vocabulary chunk at a time to form ``(softmax - onehot) / n``
-and both gradient GEMMs.  The valid-token count stays on the device, so the
-reference's ``.item()`` host sync is gone.
+The device path is two calls.  ``nf_ce_fwd`` produces logits tiles on bf16
+(or fp32) MFMA and reduces them to per-row log-sum-exp without storing them;
+the loss and a per-row state (lse, target column, 1/n) come out.
+``nf_ce_bwd`` recomputes the logits one vocabulary chunk at a time to form
+``(softmax - onehot) / n`` and both gradient GEMMs, and writes the gradients
+already multiplied by ``grad_output`` in each input's dtype.  The reference
+forms fp32 gradients in the forward pass, keeps them (dW alone is [V, D]
+fp32) until the backward and then scales and casts them; here nothing
+between the two passes is larger than the state, and the results are the
+same.  The valid-token count stays on the device, so the reference's
+``.item()`` host sync is gone.
 
 ``chunk_size`` keeps its meaning as the memory budget: the reference holds a
 [chunk_size, V] fp32 logits tile; this path holds an [M, vc] probability tile
@@ -96,39 +100,64 @@ def _forward_eager(hidden, lm_weight, targets, chunk_size, ignore_index):
     return loss_total, d_hidden, d_weight
 
 
-def _forward_hip(hidden, lm_weight, targets, chunk_size, ignore_index):
+def _forward_hip(hidden, lm_weight, targets, ignore_index):
+    """Loss and the state for ``_backward_hip``: (loss, h, w, state)."""
     m, d = hidden.shape
     v = lm_weight.shape[0]
     cdt = _compute_dtype(hidden, lm_weight)
     h = hidden.to(cdt).contiguous()
     w = lm_weight.to(cdt).contiguous()
-    tg = targets.to(torch.int64).contiguous()
     dev = hidden.device
     loss = torch.empty((), dtype=torch.float32, device=dev)
-    d_hidden = torch.empty((m, d), dtype=torch.float32, device=dev)
-    d_weight = torch.empty((v, d), dtype=torch.float32, device=dev)
-    bad = torch.empty(1, dtype=torch.int32, device=dev)
     if m == 0:
-        loss.zero_(), d_hidden.zero_(), d_weight.zero_()
-        return loss, d_hidden, d_weight
-    vc = vocab_chunk_for(chunk_size, m, v)
+        return loss.zero_(), h, w, None
+    tg = targets.to(torch.int64).contiguous()
+    bad = torch.empty(1, dtype=torch.int32, device=dev)
     L = _lib.lib()
     code = _lib.dtype_code(cdt)
-    ws_bytes = L.nf_ce_workspace(m, d, v, vc, code)
+    st_bytes = L.nf_ce_state_bytes(m)
+    state = torch.empty(st_bytes, dtype=torch.uint8, device=dev)
+    ws_bytes = L.nf_ce_fwd_workspace(m, d, v, code)
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
     with device_of(hidden):
         _lib.check(
-            L.nf_ce_fwd_bwd(h.data_ptr(), w.data_ptr(), tg.data_ptr(), m, d, v, int(ignore_index),
-                            vc, code, loss.data_ptr(), d_hidden.data_ptr(), d_weight.data_ptr(),
-                            bad.data_ptr(), ws.data_ptr(), ws_bytes, _lib.stream_of(hidden)),
-            "nf_ce_fwd_bwd",
+            L.nf_ce_fwd(h.data_ptr(), w.data_ptr(), tg.data_ptr(), m, d, v, int(ignore_index),
+                        code, loss.data_ptr(), bad.data_ptr(), state.data_ptr(), st_bytes,
+                        ws.data_ptr(), ws_bytes, _lib.stream_of(hidden)),
+            "nf_ce_fwd",
         )
     if VALIDATE_TARGETS and not torch.cuda.is_current_stream_capturing():
         nbad = int(bad.item())
         if nbad:
             raise ValueError(f"chunked_cross_entropy: {nbad} target(s) outside [0, {v}) "
                              f"and not ignore_index={ignore_index}")
-    return loss, d_hidden, d_weight
+    return loss, h, w, state
+
+
+def _backward_hip(h, w, state, chunk_size, grad_output, hidden_dtype, weight_dtype):
+    """(grad_output * dL/dhidden, grad_output * dL/dweight) in the inputs' dtypes."""
+    m, d = h.shape
+    v = w.shape[0]
+    dev = h.device
+    dh = torch.empty((m, d), dtype=hidden_dtype, device=dev)
+    dw = torch.empty((v, d), dtype=weight_dtype, device=dev)
+    if m == 0:
+        return dh, dw.zero_()
+    g = grad_output.to(torch.float32).contiguous()
+    vc = vocab_chunk_for(chunk_size, m, v)
+    L = _lib.lib()
+    code = _lib.dtype_code(h.dtype)
+    ws_bytes = L.nf_ce_bwd_workspace(m, d, v, vc, code)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+    with device_of(h):
+        _lib.check(
+            L.nf_ce_bwd(h.data_ptr(), w.data_ptr(), m, d, v, vc, code, state.data_ptr(),
+                        state.numel(), g.data_ptr(), dh.data_ptr(), _lib.dtype_code(dh),
+                        dw.data_ptr(), _lib.dtype_code(dw), ws.data_ptr(), ws_bytes,
+                        _lib.stream_of(h)),
+            "nf_ce_bwd",
+        )
+    return dh, dw
 
 
 class _ChunkedCrossEntropy(torch.autograd.Function):
@@ -139,35 +168,30 @@ class _ChunkedCrossEntropy(torch.autograd.Function):
                              f"{tuple(hidden.shape)} and {tuple(lm_weight.shape)}")
         if targets.shape != (hidden.shape[0],):
             raise ValueError(f"targets must be [M={hidden.shape[0]}], got {tuple(targets.shape)}")
-        if force_reference:
-            loss, d_hidden, d_weight = _forward_eager(hidden, lm_weight, targets, chunk_size,
-                                                      ignore_index)
-        else:
-            loss, d_hidden, d_weight = _forward_hip(hidden, lm_weight, targets, chunk_size,
-                                                    ignore_index)
-        ctx.save_for_backward(d_hidden, d_weight)
         ctx.hidden_dtype = hidden.dtype
         ctx.weight_dtype = lm_weight.dtype
         ctx.eager = force_reference
+        if force_reference:
+            loss, d_hidden, d_weight = _forward_eager(hidden, lm_weight, targets, chunk_size,
+                                                      ignore_index)
+            ctx.save_for_backward(d_hidden, d_weight)
+            return loss
+        vocab_chunk_for(chunk_size, hidden.shape[0], lm_weight.shape[0])  # validates chunk_size
+        loss, h, w, state = _forward_hip(hidden, lm_weight, targets, ignore_index)
+        ctx.save_for_backward(h, w, state)
+        ctx.chunk_size = chunk_size
         return loss
 
     @staticmethod
     def backward(ctx, grad_output):
-        d_hidden, d_weight = ctx.saved_tensors
-        if ctx.eager or not d_hidden.is_cuda:
+        if ctx.eager:
+            d_hidden, d_weight = ctx.saved_tensors
             g = grad_output
             return ((d_hidden * g).to(ctx.hidden_dtype), (d_weight * g).to(ctx.weight_dtype),
                     None, None, None, None)
-        g = grad_output.to(torch.float32).contiguous()
-        dh = torch.empty(d_hidden.shape, dtype=ctx.hidden_dtype, device=d_hidden.device)
-        dw = torch.empty(d_weight.shape, dtype=ctx.weight_dtype, device=d_weight.device)
-        L = _lib.lib()
-        with device_of(d_hidden):
-            s = _lib.stream_of(d_hidden)
-            _lib.check(L.nf_scale_cast(d_hidden.data_ptr(), g.data_ptr(), dh.data_ptr(),
-                                       d_hidden.numel(), _lib.dtype_code(dh), s), "nf_scale_cast")
-            _lib.check(L.nf_scale_cast(d_weight.data_ptr(), g.data_ptr(), dw.data_ptr(),
-                                       d_weight.numel(), _lib.dtype_code(dw), s), "nf_scale_cast")
+        h, w, state = ctx.saved_tensors
+        dh, dw = _backward_hip(h, w, state, ctx.chunk_size, grad_output, ctx.hidden_dtype,
+                               ctx.weight_dtype)
         return dh, dw, None, None, None, None
 
 

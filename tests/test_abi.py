@@ -124,7 +124,23 @@ def test_ce_argument_validation():
     assert L.nf_ce_fwd_bwd(*base, 16, 8, 50, -100, 0, 1, *out, ws, None) == NF_ERR_ARG
     assert L.nf_ce_fwd_bwd(*base, 16, 8, 50, -100, 64, 2, *out, ws, None) == NF_ERR_DTYPE
     assert L.nf_ce_fwd_bwd(*base, 16, 8, 50, -100, 64, 1, *out, 16, None) == NF_ERR_WORKSPACE
-    assert L.nf_scale_cast(FAKE, FAKE, FAKE, -5, 1, None) == NF_ERR_ARG
+    # the two-call form: state and scratch sizes, shapes, dtypes, buffers
+    sb = L.nf_ce_state_bytes(4096)
+    assert sb >= 4096 * 8 and L.nf_ce_state_bytes(0) == 0
+    fws = L.nf_ce_fwd_workspace(4096, 2048, 32000, 1)
+    bws = L.nf_ce_bwd_workspace(4096, 2048, 32000, 4096, 1)
+    assert bws > 2048 * 32000 * 2 and fws > 0 and ws == sb + max(fws, bws)
+    assert L.nf_ce_fwd_workspace(4096, 2048, 32000, 2) == 0
+    fwd = [FAKE, FAKE, FAKE, 16, 8, 50, -100, 1, FAKE, None, FAKE, sb, FAKE, fws, None]
+    assert L.nf_ce_fwd(*fwd[:3], 0, *fwd[4:]) == NF_ERR_ARG
+    assert L.nf_ce_fwd(*fwd[:7], 2, *fwd[8:]) == NF_ERR_DTYPE
+    assert L.nf_ce_fwd(*fwd[:11], 8, *fwd[12:]) == NF_ERR_WORKSPACE  # state too small
+    assert L.nf_ce_fwd(*fwd[:13], 8, None) == NF_ERR_WORKSPACE
+    bwd = [FAKE, FAKE, 16, 8, 50, 64, 1, FAKE, sb, None, FAKE, 1, FAKE, 0, FAKE, bws, None]
+    assert L.nf_ce_bwd(*bwd[:5], 0, *bwd[6:]) == NF_ERR_ARG  # vocab_chunk
+    assert L.nf_ce_bwd(*bwd[:10], None, *bwd[11:]) == NF_ERR_ARG  # dhidden
+    assert L.nf_ce_bwd(*bwd[:11], 7, *bwd[12:]) == NF_ERR_DTYPE  # gradient dtype
+    assert L.nf_ce_bwd(*bwd[:15], 8, None) == NF_ERR_WORKSPACE
     assert L.nf_gemm_nt(FAKE, 4, FAKE, 4, FAKE, 2, 2, 2, 8, 1, None) == NF_ERR_ARG  # lda < K
 
 
@@ -189,7 +205,7 @@ def test_force_reference_swiglu_and_ce():
     loss.backward()
     lo, dho, dwo = on.ce_forward_backward(hid.detach().double().numpy(),
                                           w.detach().double().numpy(), tgt.numpy())
-    assert float(loss) == pytest.approx(lo, rel=1e-5)
+    assert float(loss.detach()) == pytest.approx(lo, rel=1e-5)
     assert on.rel_err(hid.grad.numpy(), dho) < 1e-5
     assert on.rel_err(w.grad.numpy(), dwo) < 1e-5
     assert torch.all(hid.grad[::3] == 0)

@@ -154,7 +154,7 @@ def test_ce_cfg4_bf16_full_size_and_deterministic(cuda):
     H = hid.float().cpu().numpy()
     W = w.float().cpu().numpy()
     lo, dho, dwo = on.ce_forward_backward(H, W, tgt.cpu().numpy())
-    assert abs(float(loss) - lo) / lo < 2e-2
+    assert abs(float(loss.detach()) - lo) / lo < 2e-2
     assert on.rel_err(dh.float().cpu().numpy(), dho) < 2e-2
     assert on.rel_err(dw.float().cpu().numpy(), dwo) < 2e-2
     assert np.all(dh.float().cpu().numpy()[(tgt == -100).cpu().numpy()] == 0)
@@ -173,25 +173,40 @@ def _reasoning_head_inputs(dev, seed=8):
     return hid, lm_head, tgt.to(dev)
 
 
-def test_ce_reasoning_head_model_shape_under_autocast(cuda):
+@pytest.mark.parametrize("chunk", [1024, 128])
+def test_ce_reasoning_head_model_shape_under_autocast(cuda, chunk):
     """bf16 hidden with an fp32 lm_head under bf16 autocast computes in bf16
     (as the reference's autocast-ed F.linear does) and returns each gradient
     in its input's dtype; parity against the fp64 oracle on the bf16-rounded
-    operands at the bf16 tolerance."""
-    note("ce reasoning head M512 D384 V32000 bf16/fp32 autocast")
+    operands at the bf16 tolerance.  chunk_size 1024 is one vocabulary chunk;
+    128 gives four, whose dH products are split over K and accumulate in
+    fp32 before the last one is written in bf16."""
+    note(f"ce reasoning head M512 D384 V32000 bf16/fp32 autocast chunk={chunk}")
     hid, lm_head, tgt = _reasoning_head_inputs(cuda)
     with torch.autocast("cuda", dtype=torch.bfloat16):
-        loss = chunked_cross_entropy(hid, lm_head, tgt, chunk_size=1024)
-    loss.backward()
+        loss = chunked_cross_entropy(hid, lm_head, tgt, chunk_size=chunk)
+    (loss * 0.5).backward()
     torch.cuda.synchronize()
     assert loss.dtype == torch.float32
     assert hid.grad.dtype == torch.bfloat16 and lm_head.grad.dtype == torch.float32
     lo, dho, dwo = on.ce_forward_backward(np64(hid), np64(lm_head.detach().to(torch.bfloat16)),
                                           tgt.cpu().numpy())
-    assert abs(float(loss) - lo) / lo < 2e-2
-    assert on.rel_err(np64(hid.grad), dho) < 2e-2
-    assert on.rel_err(np64(lm_head.grad), dwo) < 2e-2
+    assert abs(float(loss.detach()) - lo) / lo < 2e-2
+    assert on.rel_err(np64(hid.grad), 0.5 * dho) < 2e-2
+    assert on.rel_err(np64(lm_head.grad), 0.5 * dwo) < 2e-2
     assert not hid.grad[::7].any()
+
+
+def test_ce_fp16_inputs_give_fp16_gradients(cuda):
+    """fp16 hidden and weight are widened to fp32 for the products and the
+    gradients come back in fp16, scaled by grad_output (the half-precision
+    output path of the gradient epilogues), over several vocabulary chunks."""
+    note("ce fp16 inputs m=200 d=72 v=700 chunk=64")
+    hid, w, tgt = _ce_inputs(200, 72, 700, torch.float16, cuda, seed=9, w_std=0.2,
+                             ignore=slice(None, None, 5))
+    loss, dh, dw = _run_ce(hid, w, tgt, 64, scale=2.0)
+    assert dh.dtype == torch.float16 and dw.dtype == torch.float16
+    _check_ce(hid, w, tgt, loss, dh, dw, 2e-3, "fp16", scale=2.0)
 
 
 def test_ce_reasoning_head_step_replays_in_a_graph(cuda):
