@@ -130,5 +130,9 @@ def ptr(t: torch.Tensor | None) -> int | None:
 
 
 def stream_of(t: torch.Tensor) -> int:
-    """Raw hipStream_t of torch's current stream on t's device."""
-    return torch.cuda.current_stream(t.device).cuda_stream
+    """Raw hipStream_t of torch's current stream on t's device.
+
+    torch's own accessor for the handle (what ``current_stream().cuda_stream``
+    reads, without building a Stream object per launch: at the model's small
+    shapes the fused ops are host-bound and this is on every call)."""
+    return torch._C._cuda_getCurrentRawStream(t.get_device())

@@ -37,14 +37,18 @@ def require_device(t: torch.Tensor, op: str) -> None:
 
 
 class device_of:
-    """Make t's device current for the launch (no-op when it already is)."""
+    """Make t's device current for the launch (no-op when it already is).
+
+    Reads the current device with torch's raw accessor: the public
+    ``torch.cuda.current_device()`` re-checks lazy initialisation on every
+    call, and a device tensor implies an initialised runtime."""
 
     def __init__(self, t: torch.Tensor):
-        self.idx = t.device.index if t.device.index is not None else torch.cuda.current_device()
+        self.idx = t.get_device()
         self.prev = None
 
     def __enter__(self):
-        cur = torch.cuda.current_device()
+        cur = torch._C._cuda_getDevice()
         if cur != self.idx:
             self.prev = cur
             torch.cuda.set_device(self.idx)
