@@ -123,6 +123,49 @@ def test_ce_ragged_shapes(cuda, dtype, m, d, v, chunk):
     _check_ce(hid, w, tgt, loss, dh, dw, TOL[dtype], f"ragged {m},{d},{v}")
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_ce_one_call_entry_point(cuda, dtype):
+    """nf_ce_fwd_bwd (the reference's structure: loss and unscaled fp32
+    gradients in one call) through the C ABI: parity with the oracle, and
+    bit-identical to the two-call path asked for fp32 gradients with
+    grad_output 1 (the same kernels in the same order)."""
+    note(f"ce one-call entry point dtype={dtype}")
+    m, d, v, vc = 300, 72, 1030, 256
+    hid, w, tgt = _ce_inputs(m, d, v, dtype, cuda, seed=11, w_std=0.2,
+                             ignore=slice(None, None, 6))
+    L = _lib.lib()
+    code, s = _lib.dtype_code(dtype), _lib.stream_of(hid)
+    loss = torch.empty((), device=cuda)
+    dh = torch.empty(m, d, device=cuda)
+    dw = torch.empty(v, d, device=cuda)
+    bad = torch.empty(1, dtype=torch.int32, device=cuda)
+    nb = L.nf_ce_workspace(m, d, v, vc, code)
+    ws = torch.empty(nb, dtype=torch.uint8, device=cuda)
+    _lib.check(L.nf_ce_fwd_bwd(hid.data_ptr(), w.data_ptr(), tgt.data_ptr(), m, d, v, -100, vc,
+                               code, loss.data_ptr(), dh.data_ptr(), dw.data_ptr(), bad.data_ptr(),
+                               ws.data_ptr(), nb, s), "nf_ce_fwd_bwd")
+    torch.cuda.synchronize()
+    assert int(bad.item()) == 0
+    _check_ce(hid, w, tgt, loss, dh, dw, TOL[dtype], f"one call {dtype}")
+    # the same through nf_ce_fwd + nf_ce_bwd
+    sb = L.nf_ce_state_bytes(m)
+    state = torch.empty(sb, dtype=torch.uint8, device=cuda)
+    fw, bw = L.nf_ce_fwd_workspace(m, d, v, code), L.nf_ce_bwd_workspace(m, d, v, vc, code)
+    ws1 = torch.empty(fw, dtype=torch.uint8, device=cuda)
+    ws2 = torch.empty(bw, dtype=torch.uint8, device=cuda)
+    loss2, dh2, dw2 = torch.empty_like(loss), torch.empty_like(dh), torch.empty_like(dw)
+    one = torch.ones((), device=cuda)
+    _lib.check(L.nf_ce_fwd(hid.data_ptr(), w.data_ptr(), tgt.data_ptr(), m, d, v, -100, code,
+                           loss2.data_ptr(), None, state.data_ptr(), sb, ws1.data_ptr(), fw, s),
+               "nf_ce_fwd")
+    f32 = _lib.dtype_code(torch.float32)
+    _lib.check(L.nf_ce_bwd(hid.data_ptr(), w.data_ptr(), m, d, v, vc, code, state.data_ptr(), sb,
+                           one.data_ptr(), dh2.data_ptr(), f32, dw2.data_ptr(), f32,
+                           ws2.data_ptr(), bw, s), "nf_ce_bwd")
+    torch.cuda.synchronize()
+    assert torch.equal(loss, loss2) and torch.equal(dh, dh2) and torch.equal(dw, dw2)
+
+
 def test_ce_grad_output_scaling(cuda):
     note("ce grad scaling")
     hid, w, tgt = _ce_inputs(128, 64, 500, torch.float32, cuda, seed=5)
