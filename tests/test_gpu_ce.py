@@ -56,6 +56,27 @@ def test_gemm_nt_leading_dimensions(cuda):
     assert not c[:, 70:].any()
 
 
+def test_gemm_nt_output_over_2gib(cuda):
+    """An fp32 C of 2.15 GB is past the 32-bit offsets of a buffer resource:
+    the store epilogue takes its plain-store path (ragged last column tile);
+    checked against torch's fp32 product on the device."""
+    note("gemm_nt C > 2 GiB m=16384 n=32800 k=64")
+    m, n, k = 16384, 32800, 64
+    g = gen(5)
+    a = randn((m, k), g, torch.bfloat16, cuda)
+    b = randn((n, k), g, torch.bfloat16, cuda)
+    c = torch.full((m, n), float("nan"), device=cuda)
+    assert c.numel() * 4 >= 2 ** 31
+    L = _lib.lib()
+    _lib.check(L.nf_gemm_nt(a.data_ptr(), k, b.data_ptr(), k, c.data_ptr(), n, m, n, k,
+                            _lib.dtype_code(torch.bfloat16), _lib.stream_of(a)), "nf_gemm_nt")
+    want = a.float() @ b.float().T
+    torch.cuda.synchronize()
+    err = float((c - want).abs().max() / want.abs().max())
+    del want, c
+    assert err < 1e-5, err
+
+
 def _ce_inputs(m, d, v, dtype, dev, seed=0, w_std=0.02, ignore=None):
     g = gen(seed)
     hid = randn((m, d), g, dtype, dev)
