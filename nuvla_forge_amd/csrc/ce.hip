@@ -346,11 +346,14 @@ __global__ NF_GEMM_BOUNDS(C) void ce_stats_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// lse per token: a block takes 64 tokens; its 4 wavefronts each combine every
-// 4th vocabulary tile of the 64 tokens (consecutive tokens per lane, so the
-// loads are contiguous), then wavefront 0 combines the 4 parts in order.
+// lse per token: a block takes 16 tokens and 16 parts; part q combines
+// vocabulary tiles q, q + 16, q + 32, ... of its token in that order (the
+// loads of four tiles issued before their combines, so a part waits for one
+// load latency per four tiles, not per tile), then the first part combines
+// the 16 partial results in order.  A row of 16 tokens is 128 contiguous
+// bytes of the [ntiles][M] stats.
 // ---------------------------------------------------------------------------
-constexpr int kLseRows = 64, kLseParts = 4;
+constexpr int kLseRows = 16, kLseParts = 16;
 
 __global__ __launch_bounds__(kLseRows * kLseParts) void ce_lse_kernel(
     const float2 *__restrict__ stats, int ntiles, const float *tgt_logit,
@@ -360,8 +363,19 @@ __global__ __launch_bounds__(kLseRows * kLseParts) void ce_lse_kernel(
   const int rl = threadIdx.x % kLseRows, q = threadIdx.x / kLseRows;
   const int64_t row = (int64_t)blockIdx.x * kLseRows + rl;
   float2 a = make_float2(-INFINITY, 0.f);
-  if (row < M)
-    for (int t = q; t < ntiles; t += kLseParts) a = combine_stats(a, stats[(int64_t)t * M + row]);
+  if (row < M) {
+    constexpr int kBatch = 4;
+    for (int t0 = q; t0 < ntiles; t0 += kLseParts * kBatch) {
+      float2 v[kBatch];
+#pragma unroll
+      for (int u = 0; u < kBatch; ++u) {
+        const int t = t0 + u * kLseParts;
+        v[u] = t < ntiles ? stats[(int64_t)t * M + row] : make_float2(-INFINITY, 0.f);
+      }
+#pragma unroll
+      for (int u = 0; u < kBatch; ++u) a = combine_stats(a, v[u]);
+    }
+  }
   part[q][rl] = a;
   __syncthreads();
   if (q != 0 || row >= M) return;
@@ -920,7 +934,9 @@ int ce_bwd_run(const TI *H, const TI *W, int64_t M, int64_t D, int64_t V, int64_
         jp->tiles *= q.S;
       }
     }
-    if ((e = launch_gemm_store<C>(jw, jh, s))) return e;
+    // a split job's slices are the longest blocks: dispatch them first
+    if ((e = sp.h.S > 1 ? launch_gemm_store<C>(jh, jw, s) : launch_gemm_store<C>(jw, jh, s)))
+      return e;
   }
   return NF_OK;
 }
