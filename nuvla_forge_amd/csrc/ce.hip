@@ -239,8 +239,17 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float *__restr
   const float g = scale ? *scale : 1.f;
   for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total;
        i += (int64_t)gridDim.x * 256) {
+    // slices added in order 0 .. S-1; 8 loads in flight per batch
+    constexpr int kBatch = 8;
     float a = 0.f;
-    for (int k = 0; k < S; ++k) a += part[k * total + i];
+    for (int k0 = 0; k0 < S; k0 += kBatch) {
+      float v[kBatch];
+#pragma unroll
+      for (int u = 0; u < kBatch; ++u) v[u] = k0 + u < S ? part[(k0 + u) * total + i] : 0.f;
+#pragma unroll
+      for (int u = 0; u < kBatch; ++u)
+        if (k0 + u < S) a += v[u];
+    }
     const int64_t o = (i / N) * ldc + i % N;
     if (Cin) a = Cin[o] + a;
     store_dyn(C, cdt, o, a * g);
