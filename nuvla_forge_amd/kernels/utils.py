@@ -25,6 +25,24 @@ def next_power_of_2(n: int) -> int:
     return 1 << (n - 1).bit_length()
 
 
+def warps_for_block(block_n: int) -> int:
+    """Wavefronts per row for a row of ``block_n`` elements (reference
+    utils.py:30-44, where it picks Triton warps for single-row reductions).
+
+    On MI355X the row kernels place a row on 64-lane wavefronts: the adaLN
+    forward gives each lane one or two 16-byte chunks (8 elements each) and
+    splits rows of N >= 1024 over at least two wavefronts, so the count is the
+    smallest power of two with 64 * w * 16 >= N, at least 2 from N = 1024 on.
+    The C++ launch plan (``make_plan`` in csrc/adaln_impl.h) applies the same
+    rule; this function only reports it."""
+    w = 1
+    while 64 * w * 8 * 2 < block_n:
+        w *= 2
+    if block_n >= 1024 and w < 2:
+        w = 2
+    return w
+
+
 def require_device(t: torch.Tensor, op: str) -> None:
     """The fused ops run only on ROCm device tensors; say so instead of falling back."""
     if not t.is_cuda:

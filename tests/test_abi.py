@@ -156,6 +156,20 @@ def test_vocab_chunk_budget():
 # ---------------------------------------------------------------------------
 # Python drop-in on the CPU
 # ---------------------------------------------------------------------------
+def test_launch_heuristics_of_the_utils_module():
+    """kernels.utils keeps the reference's helpers (utils.py:23-44): the next
+    power of two, and the per-row wavefront count of the adaLN forward plan
+    (64-lane wavefronts, up to two 8-element chunks per lane, >= 2 from 1024)."""
+    from nuvla_forge_amd.kernels import utils
+
+    assert [utils.next_power_of_2(n) for n in (0, 1, 2, 3, 1000, 1024, 1025)] == \
+        [1, 1, 2, 4, 1024, 1024, 2048]
+    want = {1: 1, 256: 1, 1000: 1, 1023: 1, 1024: 2, 2048: 2, 2049: 4, 4096: 4, 8192: 8,
+            16384: 16}
+    assert {n: utils.warps_for_block(n) for n in want} == want
+    assert utils.HAS_TRITON is utils.HAS_HIP
+
+
 def test_fused_ops_refuse_cpu_tensors():
     x = torch.randn(8, 16)
     g = torch.zeros(2, 16)
