@@ -401,16 +401,24 @@ __global__ __launch_bounds__(kLseRows * kLseParts) void ce_lse_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// loss, n_valid, inv_count: one block, fixed-order tree
+// loss, n_valid, inv_count: one block; each thread sums a strided share of
+// the rows, each wavefront reduces its lanes (fixed butterfly), and thread 0
+// adds the 16 wavefront sums in order.
 // ---------------------------------------------------------------------------
 constexpr int kLossThreads = 1024;
+
+__device__ __forceinline__ int wave_sum_int(int v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+  return v;
+}
 
 __global__ __launch_bounds__(kLossThreads) void ce_loss_kernel(
     const float *loss_row, const int *flags, int64_t M, float *loss,
     float *inv_out, int *bad_out) {
-  __shared__ float sl[kLossThreads];
-  __shared__ int sn[kLossThreads];
-  __shared__ int sb[kLossThreads];
+  constexpr int kWaves = kLossThreads / 64;
+  __shared__ float sl[kWaves];
+  __shared__ int sn[kWaves], sb[kWaves];
   float a = 0.f;
   int n = 0, bad = 0;
   for (int64_t i = threadIdx.x; i < M; i += kLossThreads) {
@@ -418,23 +426,28 @@ __global__ __launch_bounds__(kLossThreads) void ce_loss_kernel(
     n += flags[i] & 1;
     bad += (flags[i] >> 1) & 1;
   }
-  sl[threadIdx.x] = a;
-  sn[threadIdx.x] = n;
-  sb[threadIdx.x] = bad;
-  __syncthreads();
-  for (int s = kLossThreads / 2; s > 0; s >>= 1) {
-    if ((int)threadIdx.x < s) {
-      sl[threadIdx.x] += sl[threadIdx.x + s];
-      sn[threadIdx.x] += sn[threadIdx.x + s];
-      sb[threadIdx.x] += sb[threadIdx.x + s];
-    }
-    __syncthreads();
+  a = wave_sum(a);
+  n = wave_sum_int(n);
+  bad = wave_sum_int(bad);
+  const int w = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) {
+    sl[w] = a;
+    sn[w] = n;
+    sb[w] = bad;
   }
+  __syncthreads();
   if (threadIdx.x == 0) {
-    const float inv = 1.f / (float)(sn[0] > 1 ? sn[0] : 1);
-    *loss = sl[0] * inv;
+    float tl = 0.f;
+    int tn = 0, tb = 0;
+    for (int k = 0; k < kWaves; ++k) {
+      tl += sl[k];
+      tn += sn[k];
+      tb += sb[k];
+    }
+    const float inv = 1.f / (float)(tn > 1 ? tn : 1);
+    *loss = tl * inv;
     *inv_out = inv;
-    if (bad_out) *bad_out = sb[0];
+    if (bad_out) *bad_out = tb;
   }
 }
 
