@@ -82,6 +82,26 @@ int nf_gemm_swiglu(const void *x, int64_t ldx, const void *w_gate,
                    int64_t ldo, int64_t M, int64_t D, int64_t H, int dtype,
                    void *stream);
 
+/* Bytes of workspace nf_gemm_swiglu_wgrad needs for this shape (the
+ * token-contiguous copies of da, db and x plus the fp32 split-K slices). */
+size_t nf_gemm_swiglu_wgrad_workspace(int64_t M, int64_t D, int64_t H);
+
+/* Weight gradients of the gate/up projection, both in one launch:
+ *   dw_gate = da^T x,   dw_up = db^T x          (fp32 accumulate, bf16 out)
+ * No kernel of the reference computes this: it replaces the weight-gradient
+ * GEMMs of the two Linears in SwiGLUMLP (nuvla_forge/model/dit.py:104-110)
+ * that autograd runs in the backward.  da / db [M, H] (row stride ld_ab) are
+ * the gradients at the gate and up outputs, x [M, D] (row stride ldx) the
+ * projection input, dw_gate / dw_up [H, D] (row stride ldw) are overwritten.
+ * The sum over the M tokens is split into slices added in a fixed order, so
+ * the result is bit-identical run to run.  M == 0 zeroes the gradients.
+ * bf16 only; every operand under 2 GiB; the workspace is 16-byte aligned. */
+int nf_gemm_swiglu_wgrad(const void *da, const void *db, int64_t ld_ab,
+                         const void *x, int64_t ldx, void *dw_gate,
+                         void *dw_up, int64_t ldw, int64_t M, int64_t D,
+                         int64_t H, int dtype, void *workspace,
+                         size_t workspace_bytes, void *stream);
+
 /* ------------------------------------------------------------------------
  * adaLN-Zero seam: gated residual add, RMSNorm, modulation.  Row m of the
  * [M, N] activations belongs to sample m / T (M = B * T).

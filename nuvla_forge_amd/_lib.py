@@ -67,6 +67,11 @@ SIGNATURES = {
     "nf_gemm_swiglu": (
         _I32, [_P, _I64, _P, _P, _I64, _P, _P, _P, _I64, _I64, _I64, _I64, _I32, _P],
     ),
+    "nf_gemm_swiglu_wgrad_workspace": (_SZ, [_I64, _I64, _I64]),
+    "nf_gemm_swiglu_wgrad": (
+        _I32,
+        [_P, _P, _I64, _P, _I64, _P, _P, _I64, _I64, _I64, _I64, _I32, _P, _SZ, _P],
+    ),
 }
 
 _lib: ctypes.CDLL | None = None

@@ -1,0 +1,357 @@
+// GEMM with a store epilogue on the MFMA core of gemm_core.h, shared by the
+// kernels that need a plain product C = scale * (Cin + A B^T): one or two
+// independent jobs per launch, optional split-K with a fixed-order reduce,
+// output in fp32 / bf16 / fp16.  Plus the 2-D transposes that make operands
+// K-contiguous, and the launch helpers.
+#pragma once
+
+#include "gemm_core.h"
+
+namespace nf {
+namespace gemm {
+
+// Can an operand of `rows` x K (row stride ld) use the buffer-load path?
+template <typename TI>
+inline bool buf_ok(const void *p, int64_t ld, int64_t rows, int64_t K) {
+  constexpr int VE = 16 / sizeof(TI);
+  return K % VE == 0 && ld % VE == 0 && aligned16(p) &&
+         rows * ld * (int64_t)sizeof(TI) < ((int64_t)1 << 31) - 64;
+}
+
+
+// ---------------------------------------------------------------------------
+// Branch-free epilogue stores.  With SB, a store goes through a buffer
+// resource over the destination (which must be under 2 GiB); a masked
+// element gets an out-of-range offset and the buffer unit drops it, so no
+// lane diverges.  Without SB, plain stores under a per-element condition.
+// ---------------------------------------------------------------------------
+constexpr uint32_t kOobOffset = 0x80000000u;
+
+template <bool SB>
+struct OutBuf {
+  char *base;
+  __amdgpu_buffer_rsrc_t rsrc;
+  __device__ __forceinline__ void init(void *p, int64_t bytes) {
+    base = static_cast<char *>(p);
+    if constexpr (SB)
+      rsrc = __builtin_amdgcn_make_buffer_rsrc(p, (short)0, (int)bytes, 0x00020000);
+  }
+  __device__ __forceinline__ void st32(int64_t off, bool ok, float v) const {
+    if constexpr (SB)
+      __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), rsrc,
+                                            ok ? (uint32_t)off : kOobOffset, 0, 0);
+    else if (ok)
+      *reinterpret_cast<float *>(base + off) = v;
+  }
+  __device__ __forceinline__ float ld32(int64_t off, bool ok) const {
+    if constexpr (SB)
+      return __uint_as_float(
+          __builtin_amdgcn_raw_buffer_load_b32(rsrc, ok ? (uint32_t)off : kOobOffset, 0, 0));
+    else
+      return ok ? *reinterpret_cast<const float *>(base + off) : 0.f;
+  }
+  __device__ __forceinline__ void st16(int64_t off, bool ok, uint16_t v) const {
+    if constexpr (SB)
+      __builtin_amdgcn_raw_buffer_store_b16(v, rsrc, ok ? (uint32_t)off : kOobOffset, 0, 0);
+    else if (ok)
+      *reinterpret_cast<uint16_t *>(base + off) = v;
+  }
+  __device__ __forceinline__ void st64(int64_t off, bool ok, u32x2 v) const {
+    if constexpr (SB)
+      __builtin_amdgcn_raw_buffer_store_b64(v, rsrc, ok ? (uint32_t)off : kOobOffset, 0, 0);
+    else if (ok)
+      *reinterpret_cast<u32x2 *>(base + off) = v;
+  }
+  __device__ __forceinline__ void st128(int64_t off, bool ok, u32x4 v) const {
+    if constexpr (SB)
+      __builtin_amdgcn_raw_buffer_store_b128(v, rsrc, ok ? (uint32_t)off : kOobOffset, 0, 0);
+    else if (ok)
+      *reinterpret_cast<u32x4 *>(base + off) = v;
+  }
+};
+
+inline bool sb_ok(int64_t bytes) { return bytes < ((int64_t)1 << 31) - 64; }
+
+// ---------------------------------------------------------------------------
+// plain store epilogue, C[m, n] = scale * (Cin[m, n] + A B^T), for one or two
+// independent GEMMs in one launch (the dW and dH products of a vocabulary
+// chunk: each alone is too few 256x256 tiles to fill the chip, together they
+// do).  A job with Cin loads that fp32 tile into the accumulators before the
+// K loop, so the load latency overlaps the first operand copies and the
+// epilogue only stores.  C has element type cdt (fp32, bf16 or fp16: the
+// last product of a gradient goes straight to the caller's type) and
+// scale, when given, is a device fp32 scalar (the loss's grad_output).
+// ---------------------------------------------------------------------------
+// A job with ksplit > 1 divides K into slices of kslice (a multiple of the
+// stage width): block (tile, s) writes the partial product over slice s to
+// part[s] ([M, N], dense, fp32) and splitk_reduce_kernel adds the slices in
+// order, then Cin, scales and converts.
+template <typename TI>
+struct GemmJob {
+  const TI *A;
+  const TI *B;
+  const float *Cin;    // fp32 [M, ldc] added to the product, or null
+  void *C;             // [M, ldc] of cdt
+  const float *scale;  // device scalar multiplying the result, or null
+  int64_t lda, ldb, ldc, M, N, K;
+  int cdt;       // NF_DTYPE_F32 / BF16 / F16
+  int tiles_m;   // tiles along M
+  int tiles;     // blocks of this job: tiles_m * tiles_n * ksplit
+  int ksplit;    // K slices (1: no split)
+  int64_t kslice;
+  float *part;   // [ksplit, M, N] partial products when ksplit > 1
+};
+
+__host__ __device__ inline int dtype_bytes(int dt) { return dt == NF_DTYPE_F32 ? 4 : 2; }
+
+__device__ __forceinline__ uint16_t to_half_bits(float v, int dt) {
+  uint16_t bits;
+  if (dt == NF_DTYPE_BF16) {
+    const bf16 h = static_cast<bf16>(v);
+    __builtin_memcpy(&bits, &h, 2);
+  } else {
+    const f16 h = static_cast<f16>(v);
+    __builtin_memcpy(&bits, &h, 2);
+  }
+  return bits;
+}
+
+template <class C, bool BUF, bool SB>
+__global__ NF_GEMM_BOUNDS(C) void gemm_store_kernel(GemmJob<typename C::TI> j0,
+                                                    GemmJob<typename C::TI> j1) {
+  __shared__ __attribute__((aligned(16))) char smem[C::LDS_BYTES];
+  int t = gemm::xcd_order(blockIdx.x, j0.tiles + j1.tiles);
+  const bool second = t >= j0.tiles;
+  const GemmJob<typename C::TI> &j = second ? j1 : j0;
+  if (second) t -= j0.tiles;
+  const int per_split = j.tiles / j.ksplit;
+  const int ks = t / per_split;  // K slice of this block
+  int tm, tn;
+  gemm::group_tile(t % per_split, j.tiles_m, per_split / j.tiles_m, gemm::kTileGroup, tm, tn);
+  const int64_t m0 = (int64_t)tm * C::BM;
+  const int64_t n0 = (int64_t)tn * C::BN;
+  const int64_t M = j.M, N = j.N;
+  const bool split = j.ksplit > 1;
+  const int64_t k0 = ks * j.kslice;
+  const int64_t klen = j.K - k0 < j.kslice ? j.K - k0 : j.kslice;
+  // a split block writes its fp32 partial densely; the reduce does the rest
+  const int64_t ldc = split ? N : j.ldc;
+  const int cdt = split ? NF_DTYPE_F32 : j.cdt;
+  const bool preload = !split && j.Cin != nullptr;
+  OutBuf<SB> out, cin;
+  out.init(split ? static_cast<void *>(j.part + ks * M * N) : j.C,
+           M * ldc * (int64_t)dtype_bytes(cdt));
+  cin.init(const_cast<float *>(j.Cin), M * ldc * (int64_t)sizeof(float));
+  const int w = threadIdx.x >> 6, wm = w / C::WN, wn = w % C::WN;
+  // element (i, jj, r) of this lane sits at byte offset base + i * 32 rows
+  // + 8 * (r / 4) + (r % 4) rows + jj * 32 columns
+  const int64_t row0 = m0 + gemm::acc_row<C>(wm, 0, 0);
+  const int64_t col0 = n0 + gemm::acc_col<C>(wn, 0);
+  floatx16 acc[C::TM][C::TN];
+#pragma unroll
+  for (int i = 0; i < C::TM; ++i)
+#pragma unroll
+    for (int jj = 0; jj < C::TN; ++jj)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int dr = i * 32 + 8 * (r >> 2) + (r & 3);
+        const bool ok = row0 + dr < M && col0 + jj * 32 < N;
+        acc[i][jj][r] = preload ? cin.ld32(((row0 + dr) * ldc + col0 + jj * 32) * 4, ok) : 0.f;
+      }
+  gemm::mainloop<C, BUF, false>(j.A + k0, j.lda, j.B + k0, j.ldb, M, N, klen, m0, n0, smem, acc);
+  const float g = (!split && j.scale) ? *j.scale : 1.f;
+  if (cdt == NF_DTYPE_F32) {
+#pragma unroll
+    for (int i = 0; i < C::TM; ++i)
+#pragma unroll
+      for (int jj = 0; jj < C::TN; ++jj)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int dr = i * 32 + 8 * (r >> 2) + (r & 3);
+          const bool ok = row0 + dr < M && col0 + jj * 32 < N;
+          out.st32(((row0 + dr) * ldc + col0 + jj * 32) * 4, ok, acc[i][jj][r] * g);
+        }
+  } else {
+#pragma unroll
+    for (int i = 0; i < C::TM; ++i)
+#pragma unroll
+      for (int jj = 0; jj < C::TN; ++jj)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int dr = i * 32 + 8 * (r >> 2) + (r & 3);
+          const bool ok = row0 + dr < M && col0 + jj * 32 < N;
+          out.st16(((row0 + dr) * ldc + col0 + jj * 32) * 2, ok,
+                   to_half_bits(acc[i][jj][r] * g, cdt));
+        }
+  }
+}
+
+// C[m, n] = scale * (Cin[m, n] + sum over s = 0 .. S-1 of part[s, m, n]),
+// the slices added in order; C of element type cdt.
+static __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float *__restrict__ part,
+                                                            int S, int64_t M, int64_t N,
+                                                            const float *Cin, void *C,
+                                                            int64_t ldc, int cdt,
+                                                            const float *scale) {
+  const int64_t total = M * N;
+  const float g = scale ? *scale : 1.f;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total;
+       i += (int64_t)gridDim.x * 256) {
+    // slices added in order 0 .. S-1; 8 loads in flight per batch
+    constexpr int kBatch = 8;
+    float a = 0.f;
+    for (int k0 = 0; k0 < S; k0 += kBatch) {
+      float v[kBatch];
+#pragma unroll
+      for (int u = 0; u < kBatch; ++u) v[u] = k0 + u < S ? part[(k0 + u) * total + i] : 0.f;
+#pragma unroll
+      for (int u = 0; u < kBatch; ++u)
+        if (k0 + u < S) a += v[u];
+    }
+    const int64_t o = (i / N) * ldc + i % N;
+    if (Cin) a = Cin[o] + a;
+    store_dyn(C, cdt, o, a * g);
+  }
+}
+
+
+// ---------------------------------------------------------------------------
+// transpose with zero padding: out[c, r] = in[r, c] (r < R), 0 for R <= r < ldo
+// ---------------------------------------------------------------------------
+template <typename T>
+__global__ __launch_bounds__(256) void transpose_pad_kernel(
+    const T *__restrict__ in, int64_t R, int64_t Cn, int64_t ldi,
+    T *__restrict__ out, int64_t ldo) {
+  __shared__ T tile[64][65];
+  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+  const int64_t r0 = (int64_t)blockIdx.x * 64, c0 = (int64_t)blockIdx.y * 64;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int64_t r = r0 + ty + 4 * i, c = c0 + tx;
+    tile[ty + 4 * i][tx] = (r < R && c < Cn) ? in[r * ldi + c] : static_cast<T>(0.f);
+  }
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int64_t c = c0 + ty + 4 * i, r = r0 + tx;
+    if (c < Cn && r < ldo) out[c * ldo + r] = tile[tx][ty + 4 * i];
+  }
+}
+
+// 16-bit elements, 16-byte accesses: a 64 x 64 tile is read as 8-element row
+// vectors and written as 8-element column vectors through LDS.  Requires
+// Cn, ldi, ldo multiples of 8 and 16-byte aligned bases (a vector is then
+// wholly inside or outside the matrix).
+constexpr int kTpPitch = 66;  // LDS row pitch in elements (spreads column reads over banks)
+
+static __global__ __launch_bounds__(256) void transpose16_kernel(
+    const uint16_t *__restrict__ in, int64_t R, int64_t Cn, int64_t ldi,
+    uint16_t *__restrict__ out, int64_t ldo) {
+  __shared__ uint16_t tile[64 * kTpPitch];
+  const int t = threadIdx.x;
+  const int64_t r0 = (int64_t)blockIdx.x * 64, c0 = (int64_t)blockIdx.y * 64;
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int row = t / 8 + 32 * i, vec = t % 8;
+    const int64_t r = r0 + row, c = c0 + 8 * vec;
+    u32x4 v = {0u, 0u, 0u, 0u};
+    if (r < R && c < Cn) v = *reinterpret_cast<const u32x4 *>(in + r * ldi + c);
+    uint16_t e[8];
+    __builtin_memcpy(e, &v, 16);
+#pragma unroll
+    for (int q = 0; q < 8; ++q) tile[row * kTpPitch + 8 * vec + q] = e[q];
+  }
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int oc = t / 8 + 32 * i, seg = t % 8;
+    const int64_t c = c0 + oc, r = r0 + 8 * seg;
+    uint16_t e[8];
+#pragma unroll
+    for (int q = 0; q < 8; ++q) e[q] = tile[(8 * seg + q) * kTpPitch + oc];
+    u32x4 v;
+    __builtin_memcpy(&v, e, 16);
+    if (c < Cn && r < ldo) *reinterpret_cast<u32x4 *>(out + c * ldo + r) = v;
+  }
+}
+
+
+inline int64_t round_up(int64_t x, int64_t m) { return (x + m - 1) / m * m; }
+inline size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+template <class C>
+GemmJob<typename C::TI> make_job(const typename C::TI *A, int64_t lda, const typename C::TI *B,
+                                 int64_t ldb, const float *Cin, void *Cout, int cdt,
+                                 const float *scale, int64_t ldc, int64_t M, int64_t N,
+                                 int64_t K) {
+  GemmJob<typename C::TI> j;
+  j.A = A; j.B = B; j.Cin = Cin; j.C = Cout; j.scale = scale;
+  j.lda = lda; j.ldb = ldb; j.ldc = ldc; j.M = M; j.N = N; j.K = K;
+  j.cdt = cdt;
+  j.tiles_m = (int)((M + C::BM - 1) / C::BM);
+  j.tiles = j.tiles_m * (int)((N + C::BN - 1) / C::BN);
+  j.ksplit = 1;
+  j.kslice = K;
+  j.part = nullptr;
+  return j;
+}
+
+template <typename TI>
+bool job_buf_ok(const GemmJob<TI> &j) {
+  return j.tiles == 0 || (buf_ok<TI>(j.A, j.lda, j.M, j.K) && buf_ok<TI>(j.B, j.ldb, j.N, j.K));
+}
+// every buffer the epilogue addresses through a 32-bit offset is under 2 GiB
+template <typename TI>
+bool job_sb_ok(const GemmJob<TI> &j) {
+  if (j.tiles == 0) return true;
+  if (j.ksplit > 1) return sb_ok(j.M * j.N * (int64_t)sizeof(float));
+  return sb_ok(j.M * j.ldc * (int64_t)dtype_bytes(j.cdt)) &&
+         (!j.Cin || sb_ok(j.M * j.ldc * (int64_t)sizeof(float)));
+}
+
+// Both jobs in one grid (j1 may be empty: tiles == 0), then the split-K
+// reductions of a split job.
+template <class C>
+int launch_gemm_store(const GemmJob<typename C::TI> &j0, const GemmJob<typename C::TI> &j1,
+                      hipStream_t s) {
+  const int64_t total = (int64_t)j0.tiles + j1.tiles;
+  if (total == 0) return NF_OK;
+  if (total > 0x7fffffffLL) return set_error(NF_ERR_ARG, "gemm: too many tiles");
+  const dim3 grid((unsigned)total);
+  const bool sb = job_sb_ok(j0) && job_sb_ok(j1);
+  const bool buf = job_buf_ok(j0) && job_buf_ok(j1);
+  if (buf && sb)
+    gemm_store_kernel<C, true, true><<<grid, C::NT, 0, s>>>(j0, j1);
+  else if (buf)
+    gemm_store_kernel<C, true, false><<<grid, C::NT, 0, s>>>(j0, j1);
+  else
+    gemm_store_kernel<C, false, false><<<grid, C::NT, 0, s>>>(j0, j1);
+  if (int e = check_launch("gemm_store")) return e;
+  for (const auto *jp : {&j0, &j1}) {
+    if (jp->tiles == 0 || jp->ksplit <= 1) continue;
+    int64_t blocks = (jp->M * jp->N + 255) / 256;
+    if (blocks > 2048) blocks = 2048;
+    splitk_reduce_kernel<<<(unsigned)blocks, 256, 0, s>>>(jp->part, jp->ksplit, jp->M, jp->N,
+                                                         jp->Cin, jp->C, jp->ldc, jp->cdt,
+                                                         jp->scale);
+    if (int e = check_launch("splitk_reduce")) return e;
+  }
+  return NF_OK;
+}
+
+template <typename T>
+int launch_transpose(const void *in, int64_t R, int64_t Cn, int64_t ldi, void *out,
+                     int64_t ldo, hipStream_t s) {
+  dim3 grid((unsigned)((ldo + 63) / 64), (unsigned)((Cn + 63) / 64));
+  if (sizeof(T) == 2 && Cn % 8 == 0 && ldi % 8 == 0 && ldo % 8 == 0 && aligned16(in) &&
+      aligned16(out))
+    transpose16_kernel<<<grid, 256, 0, s>>>((const uint16_t *)in, R, Cn, ldi, (uint16_t *)out,
+                                            ldo);
+  else
+    transpose_pad_kernel<T><<<grid, 256, 0, s>>>((const T *)in, R, Cn, ldi, (T *)out, ldo);
+  return check_launch("transpose");
+}
+
+
+}  // namespace gemm
+}  // namespace nf

@@ -14,7 +14,7 @@
 // a and b of the same (token, unit) pairs, and the epilogue is element-wise
 // in registers: fp32 silu(a) * b rounded once, plus a and b rounded to the
 // input type (what the backward needs; the caller may skip them).
-#include "gemm_core.h"
+#include "gemm_store.h"
 
 namespace nf {
 namespace swiglu_gemm {
@@ -100,6 +100,46 @@ __global__ NF_GEMM_BOUNDS(C) void gate_up_swiglu_kernel(Args p) {
     }
 }
 
+// ---------------------------------------------------------------------------
+// Weight gradients of the gate/up projection: dW_gate = da^T x and
+// dW_up = db^T x (the Linears' weight gradients in the reference's
+// SwiGLUMLP backward, model/dit.py:104-110).  Long in K (the tokens) and small
+// in output (H x D), these are the shape a library GEMM handles worst; here
+// da, db and x are transposed to K-contiguous [H, M] and [D, M] copies, both
+// products run in one launch split along K so that it fills the chip, and the
+// fixed-order split-K reduce writes the bf16 gradients.
+// ---------------------------------------------------------------------------
+namespace wgrad {
+struct Layout {
+  int64_t ldt;     // row stride of the transposed copies (tokens, padded to 8)
+  int S;           // K slices per product
+  int64_t kslice;  // tokens per slice (a multiple of the stage width)
+  size_t off_dat, off_dbt, off_xt, off_part, total;
+};
+inline Layout layout(int64_t M, int64_t D, int64_t H) {
+  using C = gemm::DCfg<256, 256, 2, 4, 2, 64>;
+  Layout L{};
+  L.ldt = gemm::round_up(M, 8);
+  const int64_t tiles = ((H + C::BM - 1) / C::BM) * ((D + C::BN - 1) / C::BN);
+  // fill one wave of 256 blocks with both products, slices of >= 256 tokens
+  int64_t S = 256 / (2 * tiles);
+  const int64_t smax = (L.ldt + 255) / 256;
+  if (S > smax) S = smax;
+  if (S > 64) S = 64;
+  if (S < 1) S = 1;
+  L.kslice = gemm::round_up((L.ldt + S - 1) / S, C::BK);
+  L.S = (int)((L.ldt + L.kslice - 1) / L.kslice);
+  size_t o = 0;
+  auto take = [&](size_t bytes) { const size_t at = o; o = gemm::align256(o + bytes); return at; };
+  L.off_dat = take((size_t)H * L.ldt * 2);
+  L.off_dbt = take((size_t)H * L.ldt * 2);
+  L.off_xt = take((size_t)D * L.ldt * 2);
+  L.off_part = take(L.S > 1 ? (size_t)2 * L.S * H * D * sizeof(float) : 0);
+  L.total = o;
+  return L;
+}
+}  // namespace wgrad
+
 }  // namespace swiglu_gemm
 }  // namespace nf
 
@@ -138,4 +178,66 @@ extern "C" int nf_gemm_swiglu(const void *x, int64_t ldx, const void *w_gate, co
   else
     gate_up_swiglu_kernel<false><<<grid, C::NT, 0, s>>>(args);
   return check_launch("nf_gemm_swiglu");
+}
+
+extern "C" size_t nf_gemm_swiglu_wgrad_workspace(int64_t M, int64_t D, int64_t H) {
+  if (M <= 0 || D <= 0 || H <= 0) return 0;
+  return nf::swiglu_gemm::wgrad::layout(M, D, H).total;
+}
+
+extern "C" int nf_gemm_swiglu_wgrad(const void *da, const void *db, int64_t ld_ab, const void *x,
+                                    int64_t ldx, void *dw_gate, void *dw_up, int64_t ldw,
+                                    int64_t M, int64_t D, int64_t H, int dtype, void *workspace,
+                                    size_t workspace_bytes, void *stream) {
+  using namespace nf::gemm;
+  using C = DCfg<256, 256, 2, 4, 2, 64>;
+  if (M < 0 || D <= 0 || H <= 0)
+    return set_error(NF_ERR_ARG, "nf_gemm_swiglu_wgrad: bad shape M=%lld D=%lld H=%lld",
+                     (long long)M, (long long)D, (long long)H);
+  if (dtype != NF_DTYPE_BF16)
+    return set_error(NF_ERR_DTYPE, "nf_gemm_swiglu_wgrad: dtype %d unsupported (bf16 only)",
+                     dtype);
+  if (!dw_gate || !dw_up || (M > 0 && (!da || !db || !x)))
+    return set_error(NF_ERR_ARG, "nf_gemm_swiglu_wgrad: null pointer");
+  if (ld_ab < H || ldx < D || ldw < D)
+    return set_error(NF_ERR_ARG, "nf_gemm_swiglu_wgrad: bad leading dimension");
+  const int64_t lim = ((int64_t)1 << 31) - 64;
+  if (M * ld_ab * 2 >= lim || M * ldx * 2 >= lim || H * ldw * 2 >= lim)
+    return set_error(NF_ERR_ARG, "nf_gemm_swiglu_wgrad: an operand exceeds 2 GiB");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (M == 0) {  // no tokens: zero gradients
+    for (void *w : {dw_gate, dw_up})
+      if (hipMemset2DAsync(w, (size_t)ldw * 2, 0, (size_t)D * 2, (size_t)H, s) != hipSuccess)
+        return set_error(NF_ERR_LAUNCH, "nf_gemm_swiglu_wgrad: clearing the gradients failed");
+    return NF_OK;
+  }
+  const nf::swiglu_gemm::wgrad::Layout L = nf::swiglu_gemm::wgrad::layout(M, D, H);
+  if (!workspace || workspace_bytes < L.total || !aligned16(workspace))
+    return set_error(NF_ERR_WORKSPACE, "nf_gemm_swiglu_wgrad: workspace %zu bytes < required %zu",
+                     workspace_bytes, L.total);
+  if ((int64_t)H * L.ldt * 2 >= lim || (int64_t)D * L.ldt * 2 >= lim ||
+      (L.S > 1 && H * D * (int64_t)sizeof(float) >= lim))
+    return set_error(NF_ERR_ARG, "nf_gemm_swiglu_wgrad: a transposed operand exceeds 2 GiB");
+  char *ws = static_cast<char *>(workspace);
+  bf16 *dat = reinterpret_cast<bf16 *>(ws + L.off_dat);
+  bf16 *dbt = reinterpret_cast<bf16 *>(ws + L.off_dbt);
+  bf16 *xt = reinterpret_cast<bf16 *>(ws + L.off_xt);
+  float *part = reinterpret_cast<float *>(ws + L.off_part);
+  int e;
+  if ((e = launch_transpose<uint16_t>(da, M, H, ld_ab, dat, L.ldt, s))) return e;
+  if ((e = launch_transpose<uint16_t>(db, M, H, ld_ab, dbt, L.ldt, s))) return e;
+  if ((e = launch_transpose<uint16_t>(x, M, D, ldx, xt, L.ldt, s))) return e;
+  auto jg = make_job<C>(dat, L.ldt, xt, L.ldt, nullptr, dw_gate, NF_DTYPE_BF16, nullptr, ldw, H,
+                        D, L.ldt);
+  auto ju = make_job<C>(dbt, L.ldt, xt, L.ldt, nullptr, dw_up, NF_DTYPE_BF16, nullptr, ldw, H,
+                        D, L.ldt);
+  if (L.S > 1) {
+    jg.ksplit = ju.ksplit = L.S;
+    jg.kslice = ju.kslice = L.kslice;
+    jg.tiles *= L.S;
+    ju.tiles *= L.S;
+    jg.part = part;
+    ju.part = part + (size_t)L.S * H * D;
+  }
+  return launch_gemm_store<C>(jg, ju, s);
 }

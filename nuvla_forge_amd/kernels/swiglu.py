@@ -72,8 +72,9 @@ class _FusedGateUpSwiGLU(torch.autograd.Function):
 
     forward: one ``nf_gemm_swiglu`` launch writes act and the bf16 a, b the
     backward needs.  backward: ``nf_swiglu_bwd`` forms da, db from a, b and
-    dact (sigmoid recomputed), then the plain products dx = da W_gate +
-    db W_up, dW_gate = da^T x, dW_up = db^T x run as library GEMMs.
+    dact (sigmoid recomputed); ``nf_gemm_swiglu_wgrad`` computes dW_gate =
+    da^T x and dW_up = db^T x in one split-K launch (a token sum added in a
+    fixed order); dx = da W_gate + db W_up runs as library GEMMs.
     """
 
     @staticmethod
@@ -109,9 +110,24 @@ class _FusedGateUpSwiGLU(torch.autograd.Function):
             )
         need = ctx.needs_input_grad
         dx = torch.addmm(torch.mm(da, w_gate), db, w_up) if need[0] else None
-        dwg = torch.mm(da.t(), x) if need[1] else None
-        dwu = torch.mm(db.t(), x) if need[2] else None
-        return dx, dwg, dwu
+        dwg = dwu = None
+        if need[1] or need[2]:
+            m, d = x.shape
+            h = a.shape[1]
+            dwg = torch.empty((h, d), dtype=torch.bfloat16, device=x.device)
+            dwu = torch.empty_like(dwg)
+            with device_of(x):
+                nbytes = L.nf_gemm_swiglu_wgrad_workspace(m, d, h)
+                ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=x.device)
+                _lib.check(
+                    L.nf_gemm_swiglu_wgrad(da.data_ptr(), db.data_ptr(), da.stride(0),
+                                           x.data_ptr(), x.stride(0), dwg.data_ptr(),
+                                           dwu.data_ptr(), dwg.stride(0), m, d, h,
+                                           _lib.dtype_code(torch.bfloat16), ws.data_ptr(),
+                                           nbytes, _lib.stream_of(x)),
+                    "nf_gemm_swiglu_wgrad",
+                )
+        return dx, dwg if need[1] else None, dwu if need[2] else None
 
 
 def _gate_up_eager(x, w_gate, w_up):

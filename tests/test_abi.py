@@ -86,6 +86,45 @@ def test_gemm_swiglu_argument_validation():
     assert L.nf_gemm_swiglu(*empty) == NF_OK
 
 
+def _round_up(v: int, m: int) -> int:
+    return (v + m - 1) // m * m
+
+
+def test_gemm_swiglu_wgrad_workspace_and_validation():
+    L = _lib.lib()
+    assert L.nf_gemm_swiglu_wgrad_workspace(0, 384, 1536) == 0
+    # Headline DiT MLP (M = 8 x 1176 tokens, D 384, H 1536): 6 x 2 output tiles of
+    # 256 x 256 per product, so the token sum is cut into 256 // 24 = 10 slices of
+    # 960 tokens; the workspace is the token-contiguous copies of da, db, x and
+    # the fp32 slices of both products.
+    m, d, h = 9408, 384, 1536
+    slices = 256 // (2 * 6 * 2)
+    want = 2 * _round_up(h * m * 2, 256) + _round_up(d * m * 2, 256) + 2 * slices * h * d * 4
+    assert L.nf_gemm_swiglu_wgrad_workspace(m, d, h) == want
+    # one tile and 100 tokens (padded to 104): no split, no fp32 slices
+    assert L.nf_gemm_swiglu_wgrad_workspace(100, 64, 64) == 3 * _round_up(64 * 104 * 2, 256)
+    # da, db, ld_ab, x, ldx, dw_gate, dw_up, ldw, M, D, H, dtype, workspace, bytes, stream
+    ok = [FAKE, FAKE, h, FAKE, d, FAKE, FAKE, d, m, d, h, 1, FAKE, want, None]
+    bad_dtype = list(ok)
+    bad_dtype[11] = 0
+    assert L.nf_gemm_swiglu_wgrad(*bad_dtype) == NF_ERR_DTYPE and "bf16 only" in _err()
+    short_ld = list(ok)
+    short_ld[2] = h - 1
+    assert L.nf_gemm_swiglu_wgrad(*short_ld) == NF_ERR_ARG and "leading dimension" in _err()
+    no_x = list(ok)
+    no_x[3] = None
+    assert L.nf_gemm_swiglu_wgrad(*no_x) == NF_ERR_ARG and "null" in _err()
+    small_ws = list(ok)
+    small_ws[13] = want - 1
+    assert L.nf_gemm_swiglu_wgrad(*small_ws) == NF_ERR_WORKSPACE and str(want) in _err()
+    bad_shape = list(ok)
+    bad_shape[9] = 0
+    assert L.nf_gemm_swiglu_wgrad(*bad_shape) == NF_ERR_ARG and "bad shape" in _err()
+    huge = list(ok)
+    huge[8] = 1 << 20  # 1M tokens x 1536 bf16 = 3 GiB per operand
+    assert L.nf_gemm_swiglu_wgrad(*huge) == NF_ERR_ARG and "2 GiB" in _err()
+
+
 def test_adaln_argument_validation():
     L = _lib.lib()
     args = [FAKE, 1024, FAKE, 1024, FAKE, 1024, FAKE, FAKE, 1024, FAKE, 1024, FAKE, FAKE, FAKE]

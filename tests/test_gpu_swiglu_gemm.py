@@ -110,3 +110,60 @@ def test_gate_up_swiglu_forward_is_deterministic_and_3d(cuda):
     assert a1.shape == (4, 96, 640) and torch.equal(a1, a2)
     ref = F.silu(x.float() @ wg.float().T) * (x.float() @ wu.float().T)
     assert on.rel_err(np64(a1.reshape(-1, 640)), np64(ref)) < 2e-2
+
+
+def _wgrad(da, db, x, ldw=None):
+    """Call nf_gemm_swiglu_wgrad on [M, H] views da, db and [M, D] view x."""
+    from nuvla_forge_amd import _lib
+
+    m, h = da.shape
+    d = x.shape[1]
+    ldw = ldw or d
+    dwg_buf = torch.full((h, ldw), 7.0, dtype=torch.bfloat16, device=x.device)
+    dwu_buf = torch.full_like(dwg_buf, 7.0)
+    L = _lib.lib()
+    nbytes = L.nf_gemm_swiglu_wgrad_workspace(m, d, h)
+    ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=x.device)
+    _lib.check(L.nf_gemm_swiglu_wgrad(da.data_ptr(), db.data_ptr(), da.stride(0), x.data_ptr(),
+                                      x.stride(0), dwg_buf.data_ptr(), dwu_buf.data_ptr(), ldw,
+                                      m, d, h, 1, ws.data_ptr(), nbytes, _lib.stream_of(x)),
+               "nf_gemm_swiglu_wgrad")
+    torch.cuda.synchronize()
+    return dwg_buf, dwu_buf
+
+
+# (M, D, H, row pad of da/db, row pad of x, row pad of dW): the headline DiT MLP
+# (10 token slices), ragged H and D (the element-wise transpose), fewer tokens
+# than one 8-token pad, and strided views with untouched pad columns.
+@pytest.mark.parametrize("m,d,h,pab,px,pw", [
+    (9408, 384, 1536, 0, 0, 0), (1000, 200, 333, 0, 0, 0), (5, 64, 96, 0, 0, 0),
+    (777, 136, 264, 8, 16, 8), (3000, 1024, 2816, 0, 0, 0)])
+def test_gate_up_wgrad_entry_matches_fp64(cuda, m, d, h, pab, px, pw):
+    """dW_gate = da^T x, dW_up = db^T x from the same bf16 operands in fp64.
+    The only rounding is fp32 accumulation and the final bf16 store, so the
+    norm-wise error stays under 2^-8 (round-to-nearest bf16 is within 2^-9
+    of each element); the gradients are bit-identical on a second call and
+    the pad columns of dW keep their contents."""
+    note(f"gate/up wgrad entry m={m} d={d} h={h} pads={pab},{px},{pw}")
+    g = gen(11)
+    dab = randn((m, h + pab), g, torch.bfloat16, cuda)
+    dbb = randn((m, h + pab), g, torch.bfloat16, cuda)
+    xb = randn((m, d + px), g, torch.bfloat16, cuda)
+    da, db, x = dab[:, :h], dbb[:, :h], xb[:, :d]
+    dwg, dwu = _wgrad(da, db, x, d + pw)
+    ref_g, ref_u = np64(da).T @ np64(x), np64(db).T @ np64(x)
+    assert on.rel_err(np64(dwg[:, :d]), ref_g) < 2.0 ** -8
+    assert on.rel_err(np64(dwu[:, :d]), ref_u) < 2.0 ** -8
+    if pw:
+        assert bool((dwg[:, d:] == 7.0).all()) and bool((dwu[:, d:] == 7.0).all())
+    dwg2, dwu2 = _wgrad(da, db, x, d + pw)
+    assert torch.equal(dwg, dwg2) and torch.equal(dwu, dwu2)
+
+
+def test_gate_up_wgrad_entry_without_tokens_zeroes(cuda):
+    note("gate/up wgrad entry m=0")
+    e = torch.empty((0, 64), dtype=torch.bfloat16, device=cuda)
+    x = torch.empty((0, 32), dtype=torch.bfloat16, device=cuda)
+    dwg, dwu = _wgrad(e, e, x, 40)
+    assert bool((dwg[:, :32] == 0).all()) and bool((dwu[:, :32] == 0).all())
+    assert bool((dwg[:, 32:] == 7.0).all())
