@@ -3,8 +3,8 @@
 Covers BASELINE cfg1 (fp32 [2,64,256], all six gradients at 1e-5) and cfg2
 (bf16 [8,1024,1024], 10 bit-identical backward passes), the reference's test
 shapes (tests/test_kernels.py:85-115, incl. the N=1000 masked tail), odd N
-(element-wise kernel variant), wide N (multi-wavefront rows), mixed autocast
-dtypes, strided / broadcast conditioning views as the DiT block passes them
+(element-wise kernel variant), wide N (multi-wavefront rows) in fp32, bf16
+and fp16, mixed autocast dtypes (fp32 residual with a bf16 or fp16 branch), strided / broadcast conditioning views as the DiT block passes them
 (model/dit.py:146-166), missing upstream gradients, and the large seam stress
 shape [32,2048,2048]; many samples with one row each (several reduction
 rounds) and single-row inputs.
@@ -73,7 +73,7 @@ def test_cfg1_fp32_all_six_gradients(cuda):
     _check(inp, t, dh, dout, h, out, grads, 1e-5, "cfg1")
 
 
-@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("b,t,n", [(2, 16, 256), (4, 32, 1024), (3, 7, 768), (1, 64, 1536),
                                    (2, 8, 1000), (2, 3, 333), (1, 5, 8), (2, 4, 4096),
                                    (1, 2, 16384), (300, 1, 64), (1, 1, 1024), (5, 3, 2048),
@@ -113,6 +113,19 @@ def test_mixed_autocast_dtypes(cuda):
     assert h.dtype == torch.float32 and grads["y"].dtype == torch.bfloat16
     assert grads["gate"].dtype == torch.bfloat16 and grads["weight"].dtype == torch.float32
     _check(inp, t, dh, dout, h, out, grads, 2e-2, "mixed")
+
+
+def test_mixed_fp32_residual_fp16_branch(cuda):
+    """x fp32 residual with an fp16 branch output, fp16 conditioning and weight
+    (the fp16 autocast form of the seam)."""
+    note("adaln mixed fp32 / fp16")
+    b, t, n = 3, 40, 768
+    inp = _inputs(b, t, n, torch.float32, cuda, cond_dtype=torch.float16, y_dtype=torch.float16)
+    dh, dout = _upstream(b * t, n, torch.float32, cuda)
+    h, out, grads = _run(inp, t, dh, dout)
+    assert h.dtype == torch.float32 and grads["y"].dtype == torch.float16
+    assert grads["gate"].dtype == torch.float16 and grads["shift"].dtype == torch.float16
+    _check(inp, t, dh, dout, h, out, grads, 2e-2, "mixed fp16")
 
 
 def test_strided_and_broadcast_conditioning(cuda):
