@@ -208,7 +208,7 @@ static __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float *
       for (int u = 0; u < kBatch; ++u)
         if (k0 + u < S) a += v[u];
     }
-    const int64_t o = (i / N) * ldc + i % N;
+    const int64_t o = ldc == N ? i : (i / N) * ldc + i % N;  // dense C skips the division
     if (Cin) a = Cin[o] + a;
     store_dyn(C, cdt, o, a * g);
   }
@@ -275,6 +275,26 @@ static __global__ __launch_bounds__(256) void transpose16_kernel(
   }
 }
 
+
+// rows x cols 16-bit elements of a matrix with row stride ld set to zero (a
+// kernel rather than hipMemset2DAsync, so that a captured graph holds no
+// memset node)
+static __global__ __launch_bounds__(256) void zero16_kernel(uint16_t *__restrict__ p, int64_t ld,
+                                                            int64_t rows, int64_t cols) {
+  const int64_t total = rows * cols;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total;
+       i += (int64_t)gridDim.x * 256)
+    p[(i / cols) * ld + i % cols] = 0;
+}
+
+inline int launch_zero16(void *p, int64_t ld, int64_t rows, int64_t cols, hipStream_t s) {
+  const int64_t total = rows * cols;
+  if (total <= 0) return NF_OK;
+  int64_t blocks = (total + 255) / 256;
+  if (blocks > 1024) blocks = 1024;
+  zero16_kernel<<<(unsigned)blocks, 256, 0, s>>>(static_cast<uint16_t *>(p), ld, rows, cols);
+  return check_launch("zero16");
+}
 
 inline int64_t round_up(int64_t x, int64_t m) { return (x + m - 1) / m * m; }
 inline size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }

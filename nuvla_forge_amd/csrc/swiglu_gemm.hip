@@ -206,10 +206,8 @@ extern "C" int nf_gemm_swiglu_wgrad(const void *da, const void *db, int64_t ld_a
     return set_error(NF_ERR_ARG, "nf_gemm_swiglu_wgrad: an operand exceeds 2 GiB");
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (M == 0) {  // no tokens: zero gradients
-    for (void *w : {dw_gate, dw_up})
-      if (hipMemset2DAsync(w, (size_t)ldw * 2, 0, (size_t)D * 2, (size_t)H, s) != hipSuccess)
-        return set_error(NF_ERR_LAUNCH, "nf_gemm_swiglu_wgrad: clearing the gradients failed");
-    return NF_OK;
+    int e = launch_zero16(dw_gate, ldw, H, D, s);
+    return e ? e : launch_zero16(dw_up, ldw, H, D, s);
   }
   const nf::swiglu_gemm::wgrad::Layout L = nf::swiglu_gemm::wgrad::layout(M, D, H);
   if (!workspace || workspace_bytes < L.total || !aligned16(workspace))
