@@ -6,7 +6,8 @@ Then the op through the autograd Function: the reference's test cases
 (tests/test_kernels.py:182-237: M512 H64 V1000 at chunk 128/4096, every 3rd
 row ignored, all rows ignored), ragged shapes (non-multiple-of-8 D and V),
 bad targets, grad_output scaling, and BASELINE cfg4 (bf16 M4096 D2048 V32000,
-10% ignored) against an fp32 host oracle, with a bit-identical rerun.
+10% ignored) against an fp32 host oracle, with a bit-identical rerun; and the
+reference's peak-memory test (fused below the eager reference).
 """
 
 from __future__ import annotations
@@ -311,3 +312,31 @@ def test_ce_reasoning_head_step_replays_in_a_graph(cuda):
         assert all(torch.equal(a, b) for a, b in zip(outs, eager)), f"replay {i}"
         make()()  # eager work between replays
         torch.cuda.synchronize()
+
+
+def test_ce_peak_memory_below_the_eager_reference(cuda):
+    """The reference's memory test (tests/test_kernels.py:240-262): bf16 hidden
+    [4096, 512] and W [32000, 512]; loss + backward through the fused op peaks
+    below the eager reference (fp32 logits materialised)."""
+    note("ce peak memory bf16 [4096,512] x [32000,512]")
+    from nuvla_forge_amd.kernels.reference import chunked_cross_entropy_ref
+
+    m, h, v = 4096, 512, 32000
+    g = gen(23)
+    hid = randn((m, h), g, torch.bfloat16, cuda).requires_grad_(True)
+    w = randn((v, h), g, torch.bfloat16, cuda).requires_grad_(True)
+    tgt = torch.randint(0, v, (m,), generator=g).to(cuda)
+
+    def peak(fn):
+        hid.grad = w.grad = None
+        torch.cuda.synchronize()
+        torch.cuda.empty_cache()
+        torch.cuda.reset_peak_memory_stats()
+        fn().backward()
+        torch.cuda.synchronize()
+        return torch.cuda.max_memory_allocated()
+
+    naive = peak(lambda: chunked_cross_entropy_ref(hid, w, tgt))
+    fused = peak(lambda: chunked_cross_entropy(hid, w, tgt, chunk_size=1024))
+    note(f"peak MiB: eager {naive / 2**20:.1f}, fused {fused / 2**20:.1f}")
+    assert fused < naive
