@@ -229,3 +229,33 @@ def test_stress_shape(cuda):
         errs["d" + k] = on.rel_err(f32(grads[k]), gw[k])
     bad = {k: v for k, v in errs.items() if not v <= 2e-2}
     assert not bad, bad
+
+
+@pytest.mark.parametrize("b,t,n,dt", [(8, 1024, 1024, torch.bfloat16), (8, 6, 384, None)])
+def test_fwd_bwd_replays_in_a_graph(cuda, b, t, n, dt):
+    """Forward + backward captured in a HIP graph (as bench.py times it):
+    every replay matches the eager step bit for bit.  dt None: the DiT
+    block's autocast mix (fp32 x, bf16 y and conditioning, fp32 weight)."""
+    from tests.helpers import assert_graph_replays_match
+
+    note(f"adaln graph replay b={b} t={t} n={n} dt={dt}")
+    if dt is None:
+        inp = _inputs(b, t, n, torch.float32, cuda, cond_dtype=torch.bfloat16,
+                      y_dtype=torch.bfloat16)
+        inp["weight"] = inp["weight"].float()
+        dh, dout = _upstream(b * t, n, torch.float32, cuda)
+    else:
+        inp = _inputs(b, t, n, dt, cuda)
+        dh, dout = _upstream(b * t, n, dt, cuda)
+
+    def make():
+        leaves = {k: v.detach().requires_grad_(True) for k, v in inp.items()}
+
+        def step():
+            h, out = fused_adaln_residual_rmsnorm(**leaves, tokens_per_sample=t)
+            grads = torch.autograd.grad([h, out], list(leaves.values()), [dh, dout])
+            return (h, out, *grads)
+
+        return step
+
+    assert_graph_replays_match(make)

@@ -91,3 +91,24 @@ def test_swiglu_rejects_mismatched_inputs(cuda):
         fused_swiglu(a, torch.zeros(4, 5, device=cuda))
     with pytest.raises(TypeError):
         fused_swiglu(a, torch.zeros(4, 4, device=cuda, dtype=torch.bfloat16))
+
+
+def test_swiglu_replays_in_a_graph(cuda):
+    """cfg3 forward + backward captured in a HIP graph (as bench.py times it):
+    every replay matches the eager step bit for bit."""
+    from tests.helpers import assert_graph_replays_match
+
+    note("swiglu graph replay [8192, 4096]")
+    g = gen(6)
+    a, b, dout = (randn((8192, 4096), g, torch.bfloat16, cuda) for _ in range(3))
+
+    def make():
+        la, lb = a.detach().requires_grad_(True), b.detach().requires_grad_(True)
+
+        def step():
+            out = fused_swiglu(la, lb)
+            return (out, *torch.autograd.grad(out, [la, lb], dout))
+
+        return step
+
+    assert_graph_replays_match(make)
