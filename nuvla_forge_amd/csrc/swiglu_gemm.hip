@@ -109,6 +109,15 @@ __global__ NF_GEMM_BOUNDS(C) void gate_up_swiglu_kernel(Args p) {
 // products run in one launch split along K so that it fills the chip, and the
 // fixed-order split-K reduce writes the bf16 gradients.
 // ---------------------------------------------------------------------------
+// rows x ld elements of `es` bytes stay under 2 GiB (32-bit buffer offsets);
+// divides instead of multiplying, so absurd sizes cannot overflow the test
+inline bool under_2gib(int64_t rows, int64_t ld, int64_t es) {
+  const int64_t lim = ((int64_t)1 << 31) - 64;
+  if (rows < 0 || ld <= 0) return false;
+  if (ld > lim / es) return rows == 0;
+  return rows <= (lim - 1) / (ld * es);
+}
+
 namespace wgrad {
 struct Layout {
   int64_t ldt;     // row stride of the transposed copies (tokens, padded to 8)
@@ -160,8 +169,7 @@ extern "C" int nf_gemm_swiglu(const void *x, int64_t ldx, const void *w_gate, co
   if (ldx < D || ldw < D || ldo < H)
     return set_error(NF_ERR_ARG, "nf_gemm_swiglu: bad leading dimension");
   // 32-bit buffer offsets: every operand and output under 2 GiB
-  const int64_t lim = ((int64_t)1 << 31) - 64;
-  if (M * ldx * 2 >= lim || H * ldw * 2 >= lim || M * ldo * 2 >= lim)
+  if (!under_2gib(M, ldx, 2) || !under_2gib(H, ldw, 2) || !under_2gib(M, ldo, 2))
     return set_error(NF_ERR_ARG, "nf_gemm_swiglu: an operand exceeds 2 GiB");
   const int64_t tiles_m = (M + C::BM - 1) / C::BM, tiles_n = (H + C::BN / 2 - 1) / (C::BN / 2);
   if (tiles_m * tiles_n > 0x7fffffffLL)
@@ -181,7 +189,8 @@ extern "C" int nf_gemm_swiglu(const void *x, int64_t ldx, const void *w_gate, co
 }
 
 extern "C" size_t nf_gemm_swiglu_wgrad_workspace(int64_t M, int64_t D, int64_t H) {
-  if (M <= 0 || D <= 0 || H <= 0) return 0;
+  const int64_t big = (int64_t)1 << 31;  // beyond what the entry point accepts
+  if (M <= 0 || D <= 0 || H <= 0 || M > big || D > big || H > big) return 0;
   return nf::swiglu_gemm::wgrad::layout(M, D, H).total;
 }
 
@@ -201,8 +210,8 @@ extern "C" int nf_gemm_swiglu_wgrad(const void *da, const void *db, int64_t ld_a
     return set_error(NF_ERR_ARG, "nf_gemm_swiglu_wgrad: null pointer");
   if (ld_ab < H || ldx < D || ldw < D)
     return set_error(NF_ERR_ARG, "nf_gemm_swiglu_wgrad: bad leading dimension");
-  const int64_t lim = ((int64_t)1 << 31) - 64;
-  if (M * ld_ab * 2 >= lim || M * ldx * 2 >= lim || H * ldw * 2 >= lim)
+  using nf::swiglu_gemm::under_2gib;
+  if (!under_2gib(M, ld_ab, 2) || !under_2gib(M, ldx, 2) || !under_2gib(H, ldw, 2))
     return set_error(NF_ERR_ARG, "nf_gemm_swiglu_wgrad: an operand exceeds 2 GiB");
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (M == 0) {  // no tokens: zero gradients
@@ -213,8 +222,8 @@ extern "C" int nf_gemm_swiglu_wgrad(const void *da, const void *db, int64_t ld_a
   if (!workspace || workspace_bytes < L.total || !aligned16(workspace))
     return set_error(NF_ERR_WORKSPACE, "nf_gemm_swiglu_wgrad: workspace %zu bytes < required %zu",
                      workspace_bytes, L.total);
-  if ((int64_t)H * L.ldt * 2 >= lim || (int64_t)D * L.ldt * 2 >= lim ||
-      (L.S > 1 && H * D * (int64_t)sizeof(float) >= lim))
+  if (!under_2gib(H, L.ldt, 2) || !under_2gib(D, L.ldt, 2) ||
+      (L.S > 1 && !under_2gib(H, D, sizeof(float))))
     return set_error(NF_ERR_ARG, "nf_gemm_swiglu_wgrad: a transposed operand exceeds 2 GiB");
   char *ws = static_cast<char *>(workspace);
   bf16 *dat = reinterpret_cast<bf16 *>(ws + L.off_dat);

@@ -123,6 +123,10 @@ def test_gemm_swiglu_wgrad_workspace_and_validation():
     huge = list(ok)
     huge[8] = 1 << 20  # 1M tokens x 1536 bf16 = 3 GiB per operand
     assert L.nf_gemm_swiglu_wgrad(*huge) == NF_ERR_ARG and "2 GiB" in _err()
+    absurd = list(ok)
+    absurd[8] = 1 << 62  # the size test divides, so this cannot wrap around
+    assert L.nf_gemm_swiglu_wgrad(*absurd) == NF_ERR_ARG and "2 GiB" in _err()
+    assert L.nf_gemm_swiglu_wgrad_workspace(1 << 62, d, h) == 0
 
 
 def test_adaln_argument_validation():
