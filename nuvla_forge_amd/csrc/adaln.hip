@@ -170,7 +170,8 @@ extern "C" int nf_adaln_fwd(const void *x, int64_t ld_x, const void *y,
 }
 
 extern "C" size_t nf_adaln_bwd_workspace(int64_t M, int64_t N, int64_t T) {
-  if (M <= 0 || N <= 0 || T <= 0 || M % T != 0) return 0;
+  if (M <= 0 || N <= 0 || T <= 0 || M % T != 0 || N > kMaxN || M > ((int64_t)1 << 40) / N)
+    return 0;
   return workspace_bytes(make_plan(M, N, T), N);
 }
 

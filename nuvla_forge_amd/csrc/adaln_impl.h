@@ -767,6 +767,8 @@ inline int check_shape(const char *who, int64_t M, int64_t N, int64_t T) {
                      (long long)M, (long long)T);
   if (N > kMaxN)
     return set_error(NF_ERR_ARG, "%s: N=%lld exceeds %d", who, (long long)N, kMaxN);
+  if (M > ((int64_t)1 << 40) / N)  // keeps grids and byte counts far from overflow
+    return set_error(NF_ERR_ARG, "%s: M x N exceeds 2^40 elements", who);
   return NF_OK;
 }
 

@@ -631,12 +631,20 @@ using namespace nf;
 using namespace nf::ce;
 
 namespace {
+// Sizes whose buffers could exist: M, V, D within int32 and each operand
+// under 2^40 elements, so every byte count below fits int64 / size_t.
+bool ce_sizes_ok(int64_t M, int64_t D, int64_t V) {
+  const int64_t i32 = 0x7fffffffLL, cap = (int64_t)1 << 40;
+  return M > 0 && D > 0 && V > 0 && M <= i32 && V <= i32 && D <= i32 && M * D <= cap &&
+         V * D <= cap;
+}
 int ce_check_shape(const char *fn, int64_t M, int64_t D, int64_t V) {
   if (M <= 0 || D <= 0 || V <= 0)
     return set_error(NF_ERR_ARG, "%s: bad shape M=%lld D=%lld V=%lld", fn, (long long)M,
                      (long long)D, (long long)V);
-  if (V > 0x7fffffffLL || M > 0x7fffffffLL)
-    return set_error(NF_ERR_ARG, "%s: M or V exceeds int32", fn);
+  if (!ce_sizes_ok(M, D, V))
+    return set_error(NF_ERR_ARG, "%s: M, V or D exceeds int32, or an operand 2^40 elements",
+                     fn);
   return NF_OK;
 }
 int ce_check_dtype(const char *fn, int dtype) {
@@ -648,18 +656,18 @@ size_t es_of(int dtype) { return dtype == NF_DTYPE_BF16 ? 2 : 4; }
 }  // namespace
 
 extern "C" size_t nf_ce_state_bytes(int64_t M) {
-  return M > 0 ? state_layout(M).total : 0;
+  return M > 0 && M <= 0x7fffffffLL ? state_layout(M).total : 0;
 }
 
 extern "C" size_t nf_ce_fwd_workspace(int64_t M, int64_t D, int64_t V, int dtype) {
-  if (M <= 0 || D <= 0 || V <= 0) return 0;
+  if (!ce_sizes_ok(M, D, V)) return 0;
   if (dtype != NF_DTYPE_BF16 && dtype != NF_DTYPE_F32) return 0;
   return fwd_layout(M, V, (int)es_of(dtype)).total;
 }
 
 extern "C" size_t nf_ce_bwd_workspace(int64_t M, int64_t D, int64_t V, int64_t vocab_chunk,
                                       int dtype) {
-  if (M <= 0 || D <= 0 || V <= 0 || vocab_chunk <= 0) return 0;
+  if (!ce_sizes_ok(M, D, V) || vocab_chunk <= 0) return 0;
   if (dtype != NF_DTYPE_BF16 && dtype != NF_DTYPE_F32) return 0;
   return bwd_layout(M, D, V, vocab_chunk, (int)es_of(dtype)).total;
 }
@@ -754,6 +762,8 @@ extern "C" int nf_gemm_nt(const void *A, int64_t lda, const void *B, int64_t ldb
                           int64_t ldc, int64_t M, int64_t N, int64_t K, int dtype,
                           void *stream) {
   if (M < 0 || N < 0 || K < 0) return set_error(NF_ERR_ARG, "nf_gemm_nt: negative size");
+  if (M > 0x7fffffffLL || N > 0x7fffffffLL || K > 0x7fffffffLL)
+    return set_error(NF_ERR_ARG, "nf_gemm_nt: a size exceeds int32");
   if (M == 0 || N == 0) return NF_OK;
   if (!A || !B || !C) return set_error(NF_ERR_ARG, "nf_gemm_nt: null pointer");
   if (lda < K || ldb < K || ldc < N) return set_error(NF_ERR_ARG, "nf_gemm_nt: bad leading dim");

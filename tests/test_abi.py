@@ -143,6 +143,8 @@ def test_adaln_argument_validation():
     assert L.nf_adaln_fwd(*bad_ld, 64, 1024, 8, *tail) == NF_ERR_ARG
     assert L.nf_adaln_bwd_workspace(8192, 1024, 1024) > 8 * 1024 * 4
     assert L.nf_adaln_bwd_workspace(10, 1024, 3) == 0
+    assert L.nf_adaln_bwd_workspace(1 << 40, 1024, 1) == 0  # beyond any buffer
+    assert L.nf_adaln_fwd(*args, 1 << 40, 1024, 8, *tail) == NF_ERR_ARG and "2^40" in _err()
     small = L.nf_adaln_bwd_workspace(64, 1024, 8)
     bwd = [FAKE, FAKE, FAKE, 1024, FAKE, 1024, FAKE, 1024, FAKE, FAKE, 1024, FAKE, FAKE, FAKE,
            FAKE, small - 1, 64, 1024, 8, 1, 1, 1, 1, 1, None]
@@ -159,6 +161,12 @@ def test_adaln_argument_validation():
 
 def test_ce_argument_validation():
     L = _lib.lib()
+    # sizes no buffer could have are refused before any byte count is formed
+    assert L.nf_ce_workspace(4096, 1 << 40, 32000, 4096, 1) == 0
+    assert L.nf_ce_fwd(FAKE, FAKE, FAKE, 16, 1 << 40, 50, -100, 1, FAKE, None, FAKE, 1 << 20,
+                       FAKE, 1 << 20, None) == NF_ERR_ARG and "2^40" in _err()
+    assert L.nf_gemm_nt(FAKE, 1 << 40, FAKE, 1 << 40, FAKE, 16, 16, 16, 1 << 40, 1,
+                        None) == NF_ERR_ARG and "int32" in _err()
     ws = L.nf_ce_workspace(4096, 2048, 32000, 4096, 1)
     assert ws > 2048 * 32000 * 2  # holds W^T
     assert L.nf_ce_workspace(4096, 2048, 32000, 4096, 2) == 0  # fp16 unsupported
