@@ -4,7 +4,8 @@ Usage: ``python -m nuvla_forge_amd.build [-v]``.  Every ``csrc/*.hip`` file is
 compiled to an object in ``_build/`` (in parallel), then linked into
 ``nuvla_forge_amd/libnf_hip.so``.  The library links ``libamdhip64.so.7`` by
 soname, so inside a process that imported torch first it binds to the HIP
-runtime torch already loaded.
+runtime torch already loaded.  Last, ``tests/c/abi_smoke`` (a C program using
+the library through its C ABI alone) is compiled with gcc.
 """
 
 from __future__ import annotations
@@ -83,7 +84,27 @@ def build(verbose: bool = False, jobs: int | None = None) -> Path:
     if res.returncode != 0:
         raise RuntimeError(f"link failed:\n{res.stdout}{res.stderr}")
     os.replace(tmp, LIB)
+    build_c_smoke(verbose)
     return LIB
+
+
+def build_c_smoke(verbose: bool = False) -> Path:
+    """Compile tests/c/abi_smoke.c, a C program that drives libnf_hip.so
+    through the C ABI alone (run by tests/test_gpu_c_abi.py), with gcc; it
+    finds the library next to the package through its rpath."""
+    src = PKG.parent / "tests" / "c" / "abi_smoke.c"
+    exe = src.with_suffix("")
+    rocm = Path(os.environ.get("ROCM_PATH", "/opt/rocm"))
+    cmd = [os.environ.get("CC", "gcc"), "-std=c99", "-O2", "-Wall", "-Wextra",
+           "-D__HIP_PLATFORM_AMD__", f"-I{INCLUDE}", f"-I{rocm / 'include'}", str(src),
+           "-o", str(exe), f"-L{LIB.parent}", "-lnf_hip", f"-L{rocm / 'lib'}", "-lamdhip64",
+           "-lm", "-Wl,-rpath,$ORIGIN/../../nuvla_forge_amd", f"-Wl,-rpath,{rocm / 'lib'}"]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"C ABI smoke program failed to build:\n{res.stdout}{res.stderr}")
+    return exe
 
 
 if __name__ == "__main__":

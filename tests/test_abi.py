@@ -50,6 +50,27 @@ def test_library_exports_every_declared_symbol():
     assert declared == set(_lib.SIGNATURES), "ctypes signature table out of sync with the header"
 
 
+def test_header_is_c_and_the_c_program_links_the_library():
+    """include/nuvla_forge_hip.h compiles as C99; tests/c/abi_smoke (built with
+    the library) resolves libnf_hip.so through its rpath."""
+    import shutil
+    import subprocess
+
+    gcc = shutil.which("gcc")
+    if gcc is None:
+        pytest.skip("no gcc")
+    src = '#include "nuvla_forge_hip.h"\nint main(void) { return nf_abi_version() != NF_ABI_VERSION; }\n'
+    res = subprocess.run([gcc, "-std=c99", "-Wall", "-Wextra", "-Werror", "-fsyntax-only",
+                          f"-I{ROOT / 'include'}", "-x", "c", "-"], input=src,
+                         capture_output=True, text=True)
+    assert res.returncode == 0, res.stderr
+    exe = ROOT / "tests" / "c" / "abi_smoke"
+    assert exe.exists(), "tests/c/abi_smoke is built by nuvla_forge_amd.build"
+    ldd = subprocess.run(["ldd", str(exe)], capture_output=True, text=True).stdout
+    line = [ln for ln in ldd.splitlines() if "libnf_hip.so" in ln]
+    assert line and "not found" not in line[0], ldd
+
+
 def test_abi_version():
     assert _lib.lib().nf_abi_version() == _lib.ABI_VERSION == 1
     assert K.HAS_HIP and K.HAS_TRITON
