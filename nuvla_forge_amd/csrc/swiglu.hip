@@ -3,16 +3,22 @@
 // Each thread owns UNROLL 8-element chunks spaced one block-width apart, so a
 // wavefront's loads for one unroll step are 64 consecutive 16-byte vectors
 // (bf16/f16) or 32-byte pairs (f32): fully coalesced 128-bit accesses.  All
-// loads of a thread are issued before any math so that UNROLL x (2 or 3)
-// vector loads are in flight per lane.  Math is fp32 with one rounding at
-// the store; the backward recomputes the sigmoid from `a`.
+// loads of a thread are issued before any math.  Math is fp32 with one
+// rounding at the store; the backward recomputes the sigmoid from `a`.
+//
+// Launch shape: one-wavefront blocks with one chunk per thread, the most
+// blocks and the fewest registers per wave, so the dispatcher keeps every CU
+// full of short-lived waves.  Swept over blocks of 64-1024 threads and 1-8
+// chunks per thread, fwd+bwd: bf16 [8192, 4096] 78.7 us (85% of 8 TB/s)
+// against 90.8 us for 256 threads x 4 chunks; the [65536, 5632] stress chain
+// 1.466 ms against 1.553 ms.
 #include "nf_device.h"
 
 namespace nf {
 namespace {
 
-constexpr int kBlock = 256;
-constexpr int kUnroll = 4;
+constexpr int kBlock = 64;
+constexpr int kUnroll = 1;
 
 template <typename T, bool VEC>
 __global__ __launch_bounds__(kBlock) void swiglu_fwd_kernel(
