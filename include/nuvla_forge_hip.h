@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define NF_ABI_VERSION 1
+#define NF_ABI_VERSION 2
 
 /* element type codes */
 #define NF_DTYPE_F32 0
@@ -71,16 +71,16 @@ int nf_swiglu_bwd(const void *dout, const void *a, const void *b, void *da,
  * No kernel of the reference computes this: it replaces the two Linear calls
  * and the fused_swiglu call of SwiGLUMLP.forward
  * (nuvla_forge/model/dit.py:104-110), whose a and b round-trip HBM.
- * x [M, D] (row stride ldx), w_gate / w_up [H, D] (row stride ldw, the
- * nn.Linear weight layout, used in place), a / b / act [M, H] (row stride
- * ldo).  a and b are written (rounded to bf16, for the backward) only when
- * both are non-null.  bf16 only (NF_ERR_DTYPE otherwise); every operand and
- * output under 2 GiB.
+ * x [M, D] (row stride ldx), w_gate / w_up [H, D] (row strides ld_gate /
+ * ld_up, the nn.Linear weight layout, used in place), a / b / act [M, H]
+ * (row stride ldo).  a and b are written (rounded to bf16, for the
+ * backward) only when both are non-null.  bf16 only (NF_ERR_DTYPE
+ * otherwise); every operand and output under 2 GiB.
  * ---------------------------------------------------------------------- */
 int nf_gemm_swiglu(const void *x, int64_t ldx, const void *w_gate,
-                   const void *w_up, int64_t ldw, void *a, void *b, void *act,
-                   int64_t ldo, int64_t M, int64_t D, int64_t H, int dtype,
-                   void *stream);
+                   int64_t ld_gate, const void *w_up, int64_t ld_up, void *a,
+                   void *b, void *act, int64_t ldo, int64_t M, int64_t D,
+                   int64_t H, int dtype, void *stream);
 
 /* Bytes of workspace nf_gemm_swiglu_wgrad needs for this shape (the
  * token-contiguous copies of da, db and x plus the fp32 split-K slices). */

@@ -14,7 +14,7 @@ from pathlib import Path
 import torch
 
 LIB_PATH = Path(__file__).resolve().with_name("libnf_hip.so")
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 DTYPE_CODE = {torch.float32: 0, torch.bfloat16: 1, torch.float16: 2}
 
@@ -65,7 +65,7 @@ SIGNATURES = {
     ),
     "nf_gemm_nt": (_I32, [_P, _I64, _P, _I64, _P, _I64, _I64, _I64, _I64, _I32, _P]),
     "nf_gemm_swiglu": (
-        _I32, [_P, _I64, _P, _P, _I64, _P, _P, _P, _I64, _I64, _I64, _I64, _I32, _P],
+        _I32, [_P, _I64, _P, _I64, _P, _I64, _P, _P, _P, _I64, _I64, _I64, _I64, _I32, _P],
     ),
     "nf_gemm_swiglu_wgrad_workspace": (_SZ, [_I64, _I64, _I64]),
     "nf_gemm_swiglu_wgrad": (

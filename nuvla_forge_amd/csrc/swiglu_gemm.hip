@@ -34,7 +34,7 @@ struct Args {
   bf16 *a;    // [M, ldo] or null
   bf16 *b;    // [M, ldo] or null
   bf16 *act;  // [M, ldo]
-  int64_t ldx, ldw, ldo, M, D, H;
+  int64_t ldx, ldg, ldu, ldo, M, D, H;  // ldg / ldu: row strides of W_gate / W_up
   int tiles_m, tiles_n;
 };
 
@@ -70,7 +70,8 @@ __global__ NF_GEMM_BOUNDS(C) void gate_up_swiglu_kernel(Args p) {
   // wavefront w copies tile rows 32 w .. 32 w + 31: units u0 + 32 (w / 2) + 0..31
   // of W_up (w odd) or W_gate (w even); r0 makes tile row 32 w that matrix row
   const int64_t unit0 = u0 + 32 * (wave >> 1);
-  opb.init((wave & 1) ? p.wu : p.wg, p.ldw, p.H, p.D, unit0 - 32 * wave, wave);
+  opb.init((wave & 1) ? p.wu : p.wg, (wave & 1) ? p.ldu : p.ldg, p.H, p.D, unit0 - 32 * wave,
+           wave);
   gemm::mainloop_dtl_ops<C, BUF>(opa, opb, p.D, smem, acc);
 
   const int l = threadIdx.x & 63;
@@ -154,9 +155,10 @@ inline Layout layout(int64_t M, int64_t D, int64_t H) {
 
 using namespace nf;
 
-extern "C" int nf_gemm_swiglu(const void *x, int64_t ldx, const void *w_gate, const void *w_up,
-                              int64_t ldw, void *a, void *b, void *act, int64_t ldo, int64_t M,
-                              int64_t D, int64_t H, int dtype, void *stream) {
+extern "C" int nf_gemm_swiglu(const void *x, int64_t ldx, const void *w_gate, int64_t ld_gate,
+                              const void *w_up, int64_t ld_up, void *a, void *b, void *act,
+                              int64_t ldo, int64_t M, int64_t D, int64_t H, int dtype,
+                              void *stream) {
   using namespace nf::swiglu_gemm;
   if (M < 0 || D <= 0 || H <= 0)
     return set_error(NF_ERR_ARG, "nf_gemm_swiglu: bad shape M=%lld D=%lld H=%lld",
@@ -166,19 +168,21 @@ extern "C" int nf_gemm_swiglu(const void *x, int64_t ldx, const void *w_gate, co
     return set_error(NF_ERR_DTYPE, "nf_gemm_swiglu: dtype %d unsupported (bf16 only)", dtype);
   if (!x || !w_gate || !w_up || !act || (!a) != (!b))
     return set_error(NF_ERR_ARG, "nf_gemm_swiglu: null pointer (a and b: both or neither)");
-  if (ldx < D || ldw < D || ldo < H)
+  if (ldx < D || ld_gate < D || ld_up < D || ldo < H)
     return set_error(NF_ERR_ARG, "nf_gemm_swiglu: bad leading dimension");
   // 32-bit buffer offsets: every operand and output under 2 GiB
-  if (!under_2gib(M, ldx, 2) || !under_2gib(H, ldw, 2) || !under_2gib(M, ldo, 2))
+  if (!under_2gib(M, ldx, 2) || !under_2gib(H, ld_gate, 2) || !under_2gib(H, ld_up, 2) ||
+      !under_2gib(M, ldo, 2))
     return set_error(NF_ERR_ARG, "nf_gemm_swiglu: an operand exceeds 2 GiB");
   const int64_t tiles_m = (M + C::BM - 1) / C::BM, tiles_n = (H + C::BN / 2 - 1) / (C::BN / 2);
   if (tiles_m * tiles_n > 0x7fffffffLL)
     return set_error(NF_ERR_ARG, "nf_gemm_swiglu: grid too large");
   Args args{static_cast<const bf16 *>(x), static_cast<const bf16 *>(w_gate),
             static_cast<const bf16 *>(w_up), static_cast<bf16 *>(a), static_cast<bf16 *>(b),
-            static_cast<bf16 *>(act), ldx, ldw, ldo, M, D, H, (int)tiles_m, (int)tiles_n};
-  const bool buf = D % 8 == 0 && ldx % 8 == 0 && ldw % 8 == 0 && aligned16(x) &&
-                   aligned16(w_gate) && aligned16(w_up);
+            static_cast<bf16 *>(act), ldx, ld_gate, ld_up, ldo, M, D, H, (int)tiles_m,
+            (int)tiles_n};
+  const bool buf = D % 8 == 0 && ldx % 8 == 0 && ld_gate % 8 == 0 && ld_up % 8 == 0 &&
+                   aligned16(x) && aligned16(w_gate) && aligned16(w_up);
   hipStream_t s = static_cast<hipStream_t>(stream);
   const unsigned grid = (unsigned)(tiles_m * tiles_n);
   if (buf)

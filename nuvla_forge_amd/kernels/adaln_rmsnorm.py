@@ -10,6 +10,10 @@ tokens_per_sample, eps=1e-6, force_reference=False)`` (adaln_rmsnorm.py:239-270)
     h   = x + gate * y                                (residual stream, x.dtype)
     out = rmsnorm(h) * weight * (1 + scale) + shift   (next branch input, x.dtype)
 
+Dispatch as in the reference (adaln_rmsnorm.py:258-267): host tensors, rows
+wider than ``MAX_N`` and ``force_reference=True`` run the eager formulation
+(``reference.adaln_residual_rmsnorm_ref``); device tensors run the HIP kernels.
+
 Differences from the reference's launch code, none visible in results beyond
 fp32 rounding:
   * the conditioning tensors are read through their row stride, so the
@@ -27,10 +31,9 @@ import torch
 
 from .. import _lib
 from .reference import adaln_residual_rmsnorm_ref
-from .utils import device_of, require_device
+from .utils import device_of, use_fused
 
-MAX_N = 16384
-
+MAX_N = 16384  # widest row the kernels take (the reference's own limit, :262)
 
 
 def _rows(t: torch.Tensor) -> torch.Tensor:
@@ -151,11 +154,14 @@ def fused_adaln_residual_rmsnorm(
 ):
     """Fused gated residual + RMSNorm + adaLN-Zero modulation.
 
+    Falls back to the eager PyTorch formulation for host tensors, for rows
+    wider than 16384 and under ``force_reference=True``, as the reference does.
+
     Returns:
         (h, out) — the updated residual stream and the modulated branch input,
         both [M, N] in x.dtype.
     """
-    if force_reference:
+    if x.shape[-1] > MAX_N or not use_fused(x, "fused_adaln_residual_rmsnorm",
+                                             force_reference):
         return adaln_residual_rmsnorm_ref(x, y, gate, weight, scale, shift, tokens_per_sample, eps)
-    require_device(x, "fused_adaln_residual_rmsnorm")
     return _FusedAdaLNResidualRMSNorm.apply(x, y, gate, weight, scale, shift, tokens_per_sample, eps)

@@ -16,18 +16,25 @@ already multiplied by ``grad_output`` in each input's dtype.  The reference
 forms fp32 gradients in the forward pass, keeps them (dW alone is [V, D]
 fp32) until the backward and then scales and casts them; here nothing
 between the two passes is larger than the state, and the results are the
-same.  The valid-token count stays on the device, so the reference's
-``.item()`` host sync is gone.
+same.  The valid-token count stays on the device, so a device call makes no
+host synchronisation at all (the reference's ``.item()`` at chunked_ce.py:126
+is gone): targets outside ``[0, V)`` that are not ``ignore_index`` are
+counted on the device and treated as ignored.  Setting ``VALIDATE_TARGETS =
+True`` opts into raising ``ValueError`` for them instead, at the price of one
+device-to-host read per call (skipped while a graph is being captured).
+
+Host tensors (and ``force_reference=True``) run the reference's own row-chunk
+loop in ATen (chunked_ce.py:133-167 with ``_ce_chunk_torch``, :101-117).
 
 ``chunk_size`` keeps its meaning as the memory budget: the reference holds a
 [chunk_size, V] fp32 logits tile; this path holds an [M, vc] probability tile
 with vc = chunk_size * V / M rounded up to the 128-column MFMA tile (at most
 V).  Results do not depend on it beyond fp rounding.
 
-Element types: bf16 inputs run bf16 MFMA with fp32 accumulation; fp32 inputs
-run fp32 MFMA.  Mixed bf16/fp32 inputs compute in bf16 when autocast is on
-for the device (as the reference's autocast-ed ``F.linear`` does) and in fp32
-otherwise; fp16 inputs are widened to fp32.
+Element types: under bf16 autocast for the device the products run in bf16
+(MFMA, fp32 accumulation) whatever the input types, as the reference's
+autocast-ed ``F.linear`` and ``@`` do; otherwise bf16 inputs run bf16 MFMA,
+fp32 inputs fp32 MFMA, and mixed or fp16 inputs are widened to fp32.
 """
 
 from __future__ import annotations
@@ -35,12 +42,13 @@ from __future__ import annotations
 import torch
 
 from .. import _lib
-from .utils import device_of, require_device
+from .utils import device_of, use_fused
 
-# Out-of-range targets (not ignore_index, outside [0, V)) raise ValueError.
-# The check reads one device int back to the host; it is skipped while a
-# stream is being captured into a graph (such rows count as ignored there).
-VALIDATE_TARGETS = True
+# Opt-in: raise ValueError for targets outside [0, V) that are not
+# ignore_index.  The check reads one device int back to the host (a
+# synchronisation), so it is off by default, when such rows count as ignored;
+# it is skipped while a stream is being captured into a graph.
+VALIDATE_TARGETS = False
 
 
 def vocab_chunk_for(chunk_size: int, m: int, v: int) -> int:
@@ -53,12 +61,15 @@ def vocab_chunk_for(chunk_size: int, m: int, v: int) -> int:
 
 
 def _compute_dtype(hidden: torch.Tensor, lm_weight: torch.Tensor) -> torch.dtype:
+    """bf16 under bf16 autocast for the device (what F.linear would compute in,
+    even for the fp32 residual stream and fp32 lm_head of the reasoning head),
+    else the inputs' shared bf16 / fp32 type, else fp32."""
+    dev = hidden.device.type
+    if torch.is_autocast_enabled(dev) and torch.get_autocast_dtype(dev) == torch.bfloat16:
+        return torch.bfloat16
     hd, wd = hidden.dtype, lm_weight.dtype
     if hd == wd and hd in (torch.bfloat16, torch.float32):
         return hd
-    if torch.bfloat16 in (hd, wd) and torch.is_autocast_enabled(hidden.device.type) and \
-            torch.get_autocast_dtype(hidden.device.type) == torch.bfloat16:
-        return torch.bfloat16
     return torch.float32
 
 
@@ -112,7 +123,8 @@ def _forward_hip(hidden, lm_weight, targets, ignore_index):
     if m == 0:
         return loss.zero_(), h, w, None
     tg = targets.to(torch.int64).contiguous()
-    bad = torch.empty(1, dtype=torch.int32, device=dev)
+    validate = VALIDATE_TARGETS and not torch.cuda.is_current_stream_capturing()
+    bad = torch.empty(1, dtype=torch.int32, device=dev) if validate else None
     L = _lib.lib()
     code = _lib.dtype_code(cdt)
     st_bytes = L.nf_ce_state_bytes(m)
@@ -122,12 +134,12 @@ def _forward_hip(hidden, lm_weight, targets, ignore_index):
     with device_of(hidden):
         _lib.check(
             L.nf_ce_fwd(h.data_ptr(), w.data_ptr(), tg.data_ptr(), m, d, v, int(ignore_index),
-                        code, loss.data_ptr(), bad.data_ptr(), state.data_ptr(), st_bytes,
+                        code, loss.data_ptr(), _lib.ptr(bad), state.data_ptr(), st_bytes,
                         ws.data_ptr(), ws_bytes, _lib.stream_of(hidden)),
             "nf_ce_fwd",
         )
-    if VALIDATE_TARGETS and not torch.cuda.is_current_stream_capturing():
-        nbad = int(bad.item())
+    if validate:
+        nbad = int(bad.item())  # the opt-in check's one host synchronisation
         if nbad:
             raise ValueError(f"chunked_cross_entropy: {nbad} target(s) outside [0, {v}) "
                              f"and not ignore_index={ignore_index}")
@@ -170,8 +182,10 @@ class _ChunkedCrossEntropy(torch.autograd.Function):
             raise ValueError(f"targets must be [M={hidden.shape[0]}], got {tuple(targets.shape)}")
         ctx.hidden_dtype = hidden.dtype
         ctx.weight_dtype = lm_weight.dtype
-        ctx.eager = force_reference
-        if force_reference:
+        # the reference's rule (chunked_ce.py:133): the eager chunk loop for
+        # force_reference and for host tensors, the device kernels otherwise
+        ctx.eager = not use_fused(hidden, "chunked_cross_entropy", force_reference)
+        if ctx.eager:
             loss, d_hidden, d_weight = _forward_eager(hidden, lm_weight, targets, chunk_size,
                                                       ignore_index)
             ctx.save_for_backward(d_hidden, d_weight)
@@ -215,8 +229,8 @@ def chunked_cross_entropy(
 
     Returns:
         Scalar fp32 loss, mean-reduced over non-ignored tokens (0 if none).
+
+    Host tensors run the reference's eager row-chunk loop, as in the reference.
     """
-    if not force_reference:
-        require_device(hidden, "chunked_cross_entropy")
     return _ChunkedCrossEntropy.apply(hidden, lm_weight, targets, chunk_size, ignore_index,
                                       force_reference)

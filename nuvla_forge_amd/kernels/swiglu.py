@@ -19,7 +19,7 @@ import torch.nn.functional as F
 
 from .. import _lib
 from .reference import swiglu_ref
-from .utils import device_of, require_device
+from .utils import device_of, use_fused
 
 
 def _check(a: torch.Tensor, b: torch.Tensor) -> None:
@@ -87,9 +87,9 @@ class _FusedGateUpSwiGLU(torch.autograd.Function):
         L = _lib.lib()
         with device_of(x):
             _lib.check(
-                L.nf_gemm_swiglu(x.data_ptr(), x.stride(0), w_gate.data_ptr(), w_up.data_ptr(),
-                                 w_gate.stride(0), a.data_ptr(), b.data_ptr(), act.data_ptr(),
-                                 h, m, d, h, _lib.dtype_code(torch.bfloat16),
+                L.nf_gemm_swiglu(x.data_ptr(), x.stride(0), w_gate.data_ptr(), w_gate.stride(0),
+                                 w_up.data_ptr(), w_up.stride(0), a.data_ptr(), b.data_ptr(),
+                                 act.data_ptr(), h, m, d, h, _lib.dtype_code(torch.bfloat16),
                                  _lib.stream_of(x)),
                 "nf_gemm_swiglu",
             )
@@ -141,18 +141,18 @@ def fused_gate_up_swiglu(x: torch.Tensor, w_gate: torch.Tensor, w_up: torch.Tens
     into the projection GEMM's epilogue.
 
     Args:
-        x: [..., D] activations on a ROCm device.
-        w_gate, w_up: [H, D] projection weights (``nn.Linear.weight``).
+        x: [..., D] activations.
+        w_gate, w_up: [H, D] projection weights (``nn.Linear.weight``); each
+            may have its own row stride.
         force_reference: run the eager formulation (two Linears + silu * mul).
 
     The fused kernel computes in bf16 with fp32 accumulation: it runs when
     the inputs are bf16, or under bf16 autocast (as the Linears would); other
-    dtypes take the two Linears and the fused SwiGLU kernel.  Gradients come
-    back in each input's dtype.
+    dtypes take the two Linears and the fused SwiGLU kernel.  Host tensors
+    take the eager formulation.  Gradients come back in each input's dtype.
     """
-    if force_reference:
+    if not use_fused(x, "fused_gate_up_swiglu", force_reference):
         return _gate_up_eager(x, w_gate, w_up)
-    require_device(x, "fused_gate_up_swiglu")
     if w_gate.shape != w_up.shape or w_gate.dim() != 2 or x.shape[-1] != w_gate.shape[1]:
         raise ValueError(f"fused_gate_up_swiglu: x [..., D] and weights [H, D] expected, got "
                          f"{tuple(x.shape)}, {tuple(w_gate.shape)}, {tuple(w_up.shape)}")
@@ -179,11 +179,12 @@ def fused_swiglu(a: torch.Tensor, b: torch.Tensor, force_reference: bool = False
     """SwiGLU: ``silu(a) * b``, fused into a single pass.
 
     Args:
-        a: gate projection, any shape, on a ROCm device.
+        a: gate projection, any shape.
         b: up projection, same shape and dtype as ``a``.
         force_reference: run the eager PyTorch formulation instead.
+
+    Host tensors take the eager formulation, as in the reference (swiglu.py:104).
     """
-    if force_reference:
+    if not use_fused(a, "fused_swiglu", force_reference):
         return swiglu_ref(a, b)
-    require_device(a, "fused_swiglu")
     return _FusedSwiGLU.apply(a, b)

@@ -3,9 +3,14 @@
 Mirrors ``nuvla_forge/kernels/utils.py``: the reference exports ``HAS_TRITON``
 (is the fused backend importable).  Here the fused backend is the HIP library,
 so ``HAS_HIP`` is the probe and ``HAS_TRITON`` is kept as the same flag under
-the reference's name, so callers that test it keep working.  There is no
-Triton and no escape hatch that silently swaps backends: the eager formulation
-runs only when a caller passes ``force_reference=True``.
+the reference's name, so callers that test it keep working.
+
+Dispatch follows the reference's rule (adaln_rmsnorm.py:258-267,
+swiglu.py:104, chunked_ce.py:133): host tensors and ``force_reference=True``
+take the eager PyTorch formulation.  Device tensors always take the HIP
+kernels; a missing or stale library raises there instead of silently running
+the eager path on the GPU, and there is no environment switch that swaps
+backends.
 """
 
 from __future__ import annotations
@@ -43,15 +48,17 @@ def warps_for_block(block_n: int) -> int:
     return w
 
 
-def require_device(t: torch.Tensor, op: str) -> None:
-    """The fused ops run only on ROCm device tensors; say so instead of falling back."""
-    if not t.is_cuda:
-        raise RuntimeError(
-            f"{op}: the fused HIP path needs a ROCm device tensor (got {t.device}); "
-            "pass force_reference=True for the eager PyTorch formulation"
-        )
+def use_fused(t: torch.Tensor, op: str, force_reference: bool = False) -> bool:
+    """True when ``op`` runs the HIP kernels on ``t``: a device tensor and no
+    ``force_reference``.  Host tensors take the eager formulation, as the
+    reference's dispatch does for tensors that are not on the GPU.  On a
+    device tensor the HIP library must load (RuntimeError otherwise)."""
+    if force_reference or not t.is_cuda:
+        return False
     if torch.version.hip is None:
         raise RuntimeError(f"{op}: this build targets ROCm (gfx950); torch has no HIP")
+    _lib.lib()  # raises RuntimeError naming the problem if the library cannot load
+    return True
 
 
 class device_of:

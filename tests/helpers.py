@@ -32,6 +32,27 @@ def np64(t: torch.Tensor) -> np.ndarray:
     return t.detach().to("cpu", torch.float64).numpy()
 
 
+def swiglu_rel_errs(a, b, dout, out, da, db, rows: int = 4096) -> dict:
+    """Norm-wise relative errors of a SwiGLU forward/backward against the
+    oracle evaluated in fp32 on the host, a block of rows at a time (the
+    BASELINE stress shape has 369 M elements per tensor)."""
+    from oracle import numerics as on
+
+    num = {"out": 0.0, "da": 0.0, "db": 0.0}
+    den = dict(num)
+    m = a.shape[0]
+    for r0 in range(0, m, rows):
+        sl = slice(r0, min(r0 + rows, m))
+        A, B, G = (t[sl].to("cpu", torch.float32).numpy() for t in (a, b, dout))
+        want = {"out": on.swiglu_forward(A, B)}
+        want["da"], want["db"] = on.swiglu_backward(A, B, G)
+        for k, got in (("out", out), ("da", da), ("db", db)):
+            g = got[sl].to("cpu", torch.float32).numpy()
+            num[k] = max(num[k], float(np.abs(g - want[k]).max()))
+            den[k] = max(den[k], float(np.abs(want[k]).max()))
+    return {k: num[k] / den[k] if den[k] else num[k] for k in num}
+
+
 def assert_graph_replays_match(make, replays: int = 3) -> None:
     """Capture ``make()()`` (a step returning tensors) into a HIP graph and
     check that every replay, with eager work and synchronisations between

@@ -2,9 +2,8 @@
 
 Checks that libnf_hip.so loads, exports every function include/*.h declares,
 reports its ABI version, and rejects bad arguments with a status and a
-message before touching the GPU; and that the Python drop-in refuses CPU
-tensors on the fused path (no silent fallback) while ``force_reference=True``
-runs the eager formulation.
+message before touching the GPU; and that ``force_reference=True`` runs the
+eager formulation (host tensors take it too: tests/test_cpu_dispatch.py).
 """
 
 from __future__ import annotations
@@ -72,7 +71,7 @@ def test_header_is_c_and_the_c_program_links_the_library():
 
 
 def test_abi_version():
-    assert _lib.lib().nf_abi_version() == _lib.ABI_VERSION == 1
+    assert _lib.lib().nf_abi_version() == _lib.ABI_VERSION == 2
     assert K.HAS_HIP and K.HAS_TRITON
 
 
@@ -88,22 +87,26 @@ def test_swiglu_argument_validation():
 
 def test_gemm_swiglu_argument_validation():
     L = _lib.lib()
-    # x, ldx, w_gate, w_up, ldw, a, b, act, ldo, M, D, H, dtype, stream
-    ok = [FAKE, 64, FAKE, FAKE, 64, FAKE, FAKE, FAKE, 128, 16, 64, 128, 1, None]
+    # x, ldx, w_gate, ld_gate, w_up, ld_up, a, b, act, ldo, M, D, H, dtype, stream
+    ok = [FAKE, 64, FAKE, 64, FAKE, 128, FAKE, FAKE, FAKE, 128, 16, 64, 128, 1, None]
     bad_dtype = list(ok)
-    bad_dtype[12] = 0
+    bad_dtype[13] = 0
     assert L.nf_gemm_swiglu(*bad_dtype) == NF_ERR_DTYPE and "bf16 only" in _err()
     one_saved = list(ok)
-    one_saved[6] = None  # a without b
+    one_saved[7] = None  # a without b
     assert L.nf_gemm_swiglu(*one_saved) == NF_ERR_ARG and "both or neither" in _err()
     short_ldo = list(ok)
-    short_ldo[8] = 100  # ldo < H
+    short_ldo[9] = 100  # ldo < H
     assert L.nf_gemm_swiglu(*short_ldo) == NF_ERR_ARG and "leading dimension" in _err()
+    for i in (3, 5):  # each weight's own row stride is checked against D
+        short_ldw = list(ok)
+        short_ldw[i] = 63
+        assert L.nf_gemm_swiglu(*short_ldw) == NF_ERR_ARG and "leading dimension" in _err()
     neg = list(ok)
-    neg[11] = 0  # H = 0
+    neg[12] = 0  # H = 0
     assert L.nf_gemm_swiglu(*neg) == NF_ERR_ARG and "bad shape" in _err()
     empty = list(ok)
-    empty[9] = 0  # M = 0: nothing to do, no launch
+    empty[10] = 0  # M = 0: nothing to do, no launch
     assert L.nf_gemm_swiglu(*empty) == NF_OK
 
 
@@ -240,17 +243,6 @@ def test_launch_heuristics_of_the_utils_module():
             16384: 16}
     assert {n: utils.warps_for_block(n) for n in want} == want
     assert utils.HAS_TRITON is utils.HAS_HIP
-
-
-def test_fused_ops_refuse_cpu_tensors():
-    x = torch.randn(8, 16)
-    g = torch.zeros(2, 16)
-    with pytest.raises(RuntimeError, match="force_reference"):
-        K.fused_swiglu(x, x)
-    with pytest.raises(RuntimeError, match="force_reference"):
-        K.fused_adaln_residual_rmsnorm(x, x, g, torch.ones(16), g, g, 4)
-    with pytest.raises(RuntimeError, match="force_reference"):
-        K.chunked_cross_entropy(x, torch.randn(5, 16), torch.zeros(8, dtype=torch.long))
 
 
 def test_force_reference_adaln_matches_oracle():

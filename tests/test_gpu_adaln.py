@@ -204,10 +204,49 @@ def test_rejects_bad_shapes(cuda):
     c3 = torch.zeros(3, 64, device=cuda)
     with pytest.raises(ValueError):  # T = 5 gives B = 2, not 3
         fused_adaln_residual_rmsnorm(x, x, c3, torch.ones(64, device=cuda), c3, c3, 5)
-    big = torch.zeros(2, 16385, device=cuda)
-    cb = torch.zeros(1, 16385, device=cuda)
-    with pytest.raises(ValueError):
-        fused_adaln_residual_rmsnorm(big, big, cb, torch.ones(16385, device=cuda), cb, cb, 2)
+
+
+def test_rows_wider_than_the_kernels_take_the_eager_path(cuda):
+    """N = 16385: the reference's eager fallback on the device (adaln_rmsnorm.py:262),
+    checked against the oracle (the eager path normalises in fp32)."""
+    note("adaln N=16385 eager fallback")
+    b, t, n = 1, 2, 16385
+    inp = _inputs(b, t, n, torch.float32, cuda, seed=9)
+    dh, dout = _upstream(b * t, n, torch.float32, cuda, seed=10)
+    h, out, grads = _run(inp, t, dh, dout)
+    _check(inp, t, dh, dout, h, out, grads, 1e-5, "N=16385")
+
+
+def test_eps_placement_rows_near_eps(cuda):
+    """Rows whose mean square is comparable to eps (x, y ~ N(0, 1e-3), eps =
+    1e-6), where eps inside the square root (reference.py:62,
+    adaln_rmsnorm.py:85-86) and any other placement differ by percents: fp32
+    at 1e-5 against the oracle, for the forward and all six gradients."""
+    note("adaln eps placement fp32 rows ~1e-3")
+    b, t, n = 2, 64, 1024
+    g = gen(11)
+    inp = {
+        "x": randn((b * t, n), g, torch.float32, cuda, std=1e-3),
+        "y": randn((b * t, n), g, torch.float32, cuda, std=1e-3),
+        "gate": randn((b, n), g, torch.float32, cuda, std=0.1),
+        "weight": randn((n,), g, torch.float32, cuda, std=0.02, mean=1.0),
+        "scale": randn((b, n), g, torch.float32, cuda, std=0.1),
+        "shift": randn((b, n), g, torch.float32, cuda, std=0.1),
+    }
+    dh, dout = _upstream(b * t, n, torch.float32, cuda, seed=12)
+    h, out, grads = _run(inp, t, dh, dout)
+    _check(inp, t, dh, dout, h, out, grads, 1e-5, "eps rows")
+    # the rows really sit where eps matters: moving eps outside the root
+    # changes the oracle's output by far more than the tolerance
+    a = {k: np64(v) for k, v in inp.items()}
+    hh = a["x"] + np.repeat(a["gate"], t, axis=0) * a["y"]
+    ms = np.mean(hh * hh, axis=1)
+    assert 0.3 < float(np.median(ms)) / 1e-6 < 3.0
+    _, ow, _ = on.adaln_forward(**a, t=t)
+    wrong = 1.0 / (np.sqrt(ms) + 1e-6)
+    out_wrong = (hh * wrong[:, None]) * a["weight"] * (1 + np.repeat(a["scale"], t, 0)) + \
+        np.repeat(a["shift"], t, 0)
+    assert on.rel_err(out_wrong, ow) > 1e-2
 
 
 def test_stress_shape(cuda):

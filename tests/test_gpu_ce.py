@@ -195,12 +195,76 @@ def test_ce_grad_output_scaling(cuda):
     _check_ce(hid, w, tgt, loss, dh, dw, 1e-5, "scaled", scale=3.0)
 
 
-def test_ce_rejects_out_of_range_targets(cuda):
+def test_ce_out_of_range_targets_count_as_ignored_or_raise_on_request(cuda, monkeypatch):
+    """By default a target outside [0, V) that is not ignore_index is treated
+    as ignored (counted on the device, no host synchronisation); with
+    VALIDATE_TARGETS it raises ValueError."""
+    from nuvla_forge_amd.kernels import chunked_ce
+
     note("ce bad target")
     hid, w, tgt = _ce_inputs(32, 16, 40, torch.float32, cuda)
     tgt[5] = 40
+    tgt[9] = -7
+    loss, dh, dw = _run_ce(hid, w, tgt, 8)
+    as_ignored = tgt.clone()
+    as_ignored[[5, 9]] = -100
+    _check_ce(hid, w, as_ignored, loss, dh, dw, 1e-5, "bad targets as ignored")
+    monkeypatch.setattr(chunked_ce, "VALIDATE_TARGETS", True)
     with pytest.raises(ValueError, match="outside"):
         chunked_cross_entropy(hid, w, tgt)
+
+
+def test_ce_reasoning_head_step_makes_no_host_sync(cuda):
+    """Eager forward + backward of the fused CE at the reasoning-head shape
+    under torch.cuda.set_sync_debug_mode("error"): any synchronising call
+    (the reference's n_valid .item(), chunked_ce.py:126, or a target check)
+    would raise."""
+    note("ce reasoning head: no host synchronisation")
+    hid, lm_head, tgt = _reasoning_head_inputs(cuda, seed=12)
+    torch.cuda.synchronize()
+    torch.cuda.set_sync_debug_mode("error")
+    try:
+        for _ in range(2):
+            with torch.autocast("cuda", dtype=torch.bfloat16):
+                loss = chunked_cross_entropy(hid, lm_head, tgt, chunk_size=1024)
+            loss.backward()
+    finally:
+        torch.cuda.set_sync_debug_mode("default")
+    torch.cuda.synchronize()
+    lo, _, _ = on.ce_forward_backward(np64(hid), np64(lm_head.detach().to(torch.bfloat16)),
+                                      tgt.cpu().numpy())
+    assert abs(float(loss.detach()) - lo) / lo < 2e-2
+
+
+def test_ce_fp32_hidden_and_lm_head_under_autocast_compute_in_bf16(cuda):
+    """The reasoning head as the reference model feeds it: the fp32 residual
+    stream out of the text blocks and the fp32 lm_head, under bf16 autocast
+    (train.py:174-179).  The reference's autocast-ed F.linear computes those
+    logits in bf16; so does this path: parity against the fp64 oracle on the
+    bf16-rounded operands, gradients in fp32."""
+    note("ce fp32 hidden + fp32 lm_head under bf16 autocast")
+    g = gen(13)
+    hid = randn((512, 384), g, torch.float32, cuda).requires_grad_(True)
+    lm_head = torch.nn.Parameter(randn((32000, 384), g, torch.float32, cuda, std=0.02))
+    tgt = torch.randint(0, 32000, (512,), generator=g)
+    tgt[::5] = -100
+    tgt = tgt.to(cuda)
+    with torch.autocast("cuda", dtype=torch.bfloat16):
+        loss = chunked_cross_entropy(hid, lm_head, tgt, chunk_size=1024)
+    loss.backward()
+    torch.cuda.synchronize()
+    assert hid.grad.dtype == torch.float32 and lm_head.grad.dtype == torch.float32
+    Hb = np64(hid.detach().to(torch.bfloat16))
+    Wb = np64(lm_head.detach().to(torch.bfloat16))
+    lo, dho, dwo = on.ce_forward_backward(Hb, Wb, tgt.cpu().numpy())
+    assert abs(float(loss.detach()) - lo) / lo < 2e-2
+    assert on.rel_err(np64(hid.grad), dho) < 2e-2
+    assert on.rel_err(np64(lm_head.grad), dwo) < 2e-2
+    # bf16 products, not fp32: with fp32 accumulation the loss sits on the
+    # bf16-rounded operands' value (to ~1e-7), while the unrounded operands'
+    # value differs from that by the rounding of 410 target logits (~1e-5)
+    lo32, _, _ = on.ce_forward_backward(np64(hid), np64(lm_head), tgt.cpu().numpy())
+    assert abs(float(loss.detach()) - lo) < abs(float(loss.detach()) - lo32)
 
 
 def test_ce_cfg4_bf16_full_size_and_deterministic(cuda):

@@ -1,0 +1,86 @@
+"""BASELINE cfg5, the large seam stress step, as one chained step (GPU).
+
+adaLN-RMSNorm forward + backward in bf16 at [32, 2048, 2048] followed by
+SwiGLU forward + backward in bf16 at [65536, 5632] -- the step bench.py times
+as the sustained-bandwidth workload.  Every output of the chained step is
+checked against the oracle (evaluated in fp32 on the host) at the bf16
+tolerance, and the step captured in a HIP graph reproduces the eager step bit
+for bit on every replay.
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from nuvla_forge_amd.kernels import fused_adaln_residual_rmsnorm, fused_swiglu
+from oracle import numerics as on
+from tests.helpers import assert_graph_replays_match, gen, note, randn, swiglu_rel_errs
+
+pytestmark = pytest.mark.gpu
+
+B, T, N = 32, 2048, 2048
+SM, SH = 65536, 5632
+NAMES = ("x", "y", "gate", "weight", "scale", "shift")
+
+
+def _inputs(dev):
+    g = gen(30)
+    inp = {
+        "x": randn((B * T, N), g, torch.bfloat16, dev),
+        "y": randn((B * T, N), g, torch.bfloat16, dev),
+        "gate": randn((B, N), g, torch.bfloat16, dev, std=0.1),
+        "weight": randn((N,), g, torch.bfloat16, dev, std=0.02, mean=1.0),
+        "scale": randn((B, N), g, torch.bfloat16, dev, std=0.1),
+        "shift": randn((B, N), g, torch.bfloat16, dev, std=0.1),
+    }
+    g1 = gen(31)
+    dh, dout = (randn((B * T, N), g1, torch.bfloat16, dev) for _ in range(2))
+    g2 = gen(32)
+    a, b, gout = (randn((SM, SH), g2, torch.bfloat16, dev) for _ in range(3))
+    return inp, dh, dout, a, b, gout
+
+
+def _make(inp, dh, dout, a, b, gout):
+    def make():
+        leaves = [v.detach().requires_grad_(True) for v in inp.values()]
+        la, lb = a.detach().requires_grad_(True), b.detach().requires_grad_(True)
+
+        def step():
+            h, out = fused_adaln_residual_rmsnorm(*leaves, tokens_per_sample=T)
+            ad = torch.autograd.grad([h, out], leaves, [dh, dout])
+            act = fused_swiglu(la, lb)
+            sw = torch.autograd.grad(act, [la, lb], gout)
+            return (h, out, *ad, act, *sw)
+
+        return step
+
+    return make
+
+
+def test_cfg5_chained_step_matches_oracle_and_its_graph(cuda):
+    note("cfg5 chained step: adaLN bf16 [32,2048,2048] + SwiGLU bf16 [65536,5632]")
+    inp, dh, dout, a, b, gout = _inputs(cuda)
+    make = _make(inp, dh, dout, a, b, gout)
+    outs = make()()
+    torch.cuda.synchronize()
+    h, out, *rest = outs
+    grads, (act, da, db) = dict(zip(NAMES, rest[:6])), rest[6:]
+
+    def f32(v):
+        return v.to("cpu", torch.float32).numpy()
+
+    arr = {k: f32(v) for k, v in inp.items()}
+    hw, ow, _ = on.adaln_forward(**arr, t=T)
+    gw = on.adaln_backward(**arr, t=T, dh_up=f32(dh), dout=f32(dout))
+    errs = {"h": on.rel_err(f32(h), hw), "out": on.rel_err(f32(out), ow)}
+    del hw, ow, arr
+    for k in NAMES:
+        errs["d" + k] = on.rel_err(f32(grads[k]), gw[k])
+    del gw
+    errs.update({"swiglu_" + k: v for k, v in swiglu_rel_errs(a, b, gout, act, da, db).items()})
+    bad = {k: v for k, v in errs.items() if not v <= 2e-2}
+    assert not bad, bad
+    del outs, h, out, rest, grads, act, da, db
+    note("cfg5 chained step: graph replays")
+    assert_graph_replays_match(make)

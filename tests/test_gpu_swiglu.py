@@ -61,6 +61,20 @@ def test_swiglu_misaligned_views(cuda, dtype):
     _check(a, b, dout, out, da, db, dtype, "misaligned")
 
 
+def test_swiglu_stress_shape(cuda):
+    """BASELINE cfg5's SwiGLU leg: bf16 [65536, 5632] (369 M elements, ~721 k
+    blocks), the oracle evaluated in fp32 on the host."""
+    from tests.helpers import swiglu_rel_errs
+
+    note("swiglu stress bf16 [65536, 5632]")
+    g = gen(31)
+    a, b, dout = (randn((65536, 5632), g, torch.bfloat16, cuda) for _ in range(3))
+    out, da, db = _run(a, b, dout)
+    errs = swiglu_rel_errs(a, b, dout, out, da, db)
+    bad = {k: v for k, v in errs.items() if not v <= TOL[torch.bfloat16]}
+    assert not bad, bad
+
+
 def test_swiglu_saturation_and_zero(cuda):
     note("swiglu saturation")
     a = torch.tensor([0.0, 80.0, -80.0, 1e-30, -1e-30, 20.0, -20.0], device=cuda)

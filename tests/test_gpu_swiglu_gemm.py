@@ -64,6 +64,26 @@ def test_gate_up_swiglu_matches_oracle(cuda, m, d, h):
     assert all(e <= 2e-2 for e in errs.values()), errs
 
 
+def test_gate_up_swiglu_weights_with_different_row_strides(cuda):
+    """w_gate a column-slice view of a wider [H, 2D + 8] tensor (row stride
+    2D + 8), w_up contiguous (row stride D): each weight is read through its
+    own row stride."""
+    note("gemm swiglu w_gate strided view, w_up contiguous")
+    m, d, h = 300, 128, 384
+    g = gen(7)
+    x = randn((m, d), g, torch.bfloat16, cuda)
+    wide = randn((h, 2 * d + 8), g, torch.bfloat16, cuda, std=d ** -0.5)
+    wg = wide[:, 8:8 + d]
+    wu = randn((h, d), g, torch.bfloat16, cuda, std=d ** -0.5)
+    dact = randn((m, h), g, torch.bfloat16, cuda)
+    assert wg.stride(0) == 2 * d + 8 and wu.stride(0) == d
+    act, (dx, dwg, dwu) = _run(x, wg, wu, dact)
+    ref = _oracle(np64(x), np64(wg), np64(wu), np64(dact))
+    errs = {k: on.rel_err(np64(v), r)
+            for k, v, r in zip(("act", "dx", "dwg", "dwu"), (act, dx, dwg, dwu), ref)}
+    assert all(e <= 2e-2 for e in errs.values()), errs
+
+
 def test_gate_up_swiglu_agrees_with_eager_composition(cuda):
     note("gemm swiglu vs eager composition")
     x, wg, wu, dact = _inputs(1024, 512, 1024, torch.bfloat16, cuda, seed=1)

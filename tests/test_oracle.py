@@ -89,6 +89,30 @@ def test_adaln_known_answer_hand_computed():
     assert out[0, 1] == pytest.approx(3.0 * r * 1.0 * 2.0 - 1.0, rel=1e-15)
 
 
+def test_adaln_eps_known_answer_where_eps_matters():
+    """mean(h^2) = 3e-6 next to eps = 1e-6: rstd = 1/sqrt(3e-6 + 1e-6) = 500
+    exactly, so out = h * 500.  eps outside the root (1/(sqrt(3e-6) + 1e-6) =
+    576.99...), eps dropped (577.35...), or a sum instead of the mean over N
+    (1/sqrt(9e-6 + 1e-6) = 316.2...) all miss by more than 10%."""
+    x = np.array([[1e-3, 2e-3, 2e-3]])
+    zero = np.zeros((1, 3))
+    h, out, rstd = on.adaln_forward(x, zero, zero, np.ones(3), zero, zero, 1, eps=1e-6)
+    assert rstd[0] == pytest.approx(500.0, rel=1e-12)
+    np.testing.assert_allclose(out, [[0.5, 1.0, 1.0]], rtol=1e-12)
+    # the same through a second sample with gate and modulation in play:
+    # h = 0.5 * y, w = 2, scale = 0.5, shift = 0.25
+    y = np.array([[2e-3, 4e-3, 4e-3]])
+    h2, out2, rstd2 = on.adaln_forward(zero, y, np.full((1, 3), 0.5), np.full(3, 2.0),
+                                       np.full((1, 3), 0.5), np.full((1, 3), 0.25), 1, eps=1e-6)
+    np.testing.assert_allclose(h2, x, rtol=1e-15)
+    assert rstd2[0] == pytest.approx(500.0, rel=1e-12)
+    np.testing.assert_allclose(out2, [[0.5 * 3 + 0.25, 1.0 * 3 + 0.25, 1.0 * 3 + 0.25]],
+                               rtol=1e-12)
+    for wrong in (1.0 / (math.sqrt(3e-6) + 1e-6), 1.0 / math.sqrt(3e-6),
+                  1.0 / math.sqrt(9e-6 + 1e-6)):
+        assert abs(wrong - rstd[0]) / rstd[0] > 0.1
+
+
 def test_adaln_zero_gate_is_identity_on_residual():
     """adaLN-Zero init: gate = 0 gives h == x exactly (reference test_kernel_math.py:111-121)."""
     rng = np.random.default_rng(2)
