@@ -161,6 +161,31 @@ int nf_adaln_bwd_reduce(void *workspace, size_t workspace_bytes,
                         int dt_weight, int dt_scale, int dt_shift,
                         void *stream);
 
+/* Size of the static device buffer nf_adaln_bwd_noalloc keeps its partial
+ * rows in (one per GPU, held until the process ends). */
+#define NF_ADALN_SCRATCH_BYTES ((size_t)16 << 20)
+
+/* The adaLN seam backward (nf_adaln_bwd, then nf_adaln_bwd_reduce, same
+ * arguments and results) without a caller workspace and without allocating:
+ * the partial rows live in a static device buffer of NF_ADALN_SCRATCH_BYTES
+ * owned by the library, one per GPU.  No counterpart in the reference: it is
+ * for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc).  Shapes
+ * whose partial rows exceed the buffer (nf_adaln_bwd_workspace(M, N, T) >
+ * NF_ADALN_SCRATCH_BYTES) return NF_ERR_WORKSPACE.  All calls on one GPU
+ * share its buffer: calls that overlap in time on one GPU (other streams,
+ * other threads) race and must be serialised by the caller.  Outputs may
+ * each be NULL as in nf_adaln_bwd_reduce. */
+int nf_adaln_bwd_noalloc(const void *dh_up, const void *dout, const void *x,
+                         int64_t ld_x, const void *y, int64_t ld_y,
+                         const void *gate, int64_t ld_gate, const void *weight,
+                         const void *scale, int64_t ld_scale, const float *rstd,
+                         void *dx, void *dy, void *dgate, void *dweight,
+                         void *dscale, void *dshift, int64_t M, int64_t N,
+                         int64_t T, int dt_x, int dt_y, int dt_gate,
+                         int dt_weight, int dt_scale, int dt_shift,
+                         void *stream);
+
 /* ------------------------------------------------------------------------
  * Chunked cross entropy.
  *   logits = hidden @ weight^T          ([M, V], never materialised)

@@ -46,6 +46,11 @@ SIGNATURES = {
         [_P, _SZ, _P, _P, _I64, _P, _P, _P, _P, _I64, _I64, _I64,
          _I32, _I32, _I32, _I32, _P],
     ),
+    "nf_adaln_bwd_noalloc": (
+        _I32,
+        [_P, _P, _P, _I64, _P, _I64, _P, _I64, _P, _P, _I64, _P, _P, _P,
+         _P, _P, _P, _P, _I64, _I64, _I64, _I32, _I32, _I32, _I32, _I32, _I32, _P],
+    ),
     "nf_ce_state_bytes": (_SZ, [_I64]),
     "nf_ce_fwd_workspace": (_SZ, [_I64, _I64, _I64, _I32]),
     "nf_ce_fwd": (

@@ -1,6 +1,9 @@
 // adaLN seam C entry points and the fixed-order partial reductions.  The
 // forward/backward row kernels live in adaln_impl.h and are instantiated per
 // (x, y) element-type pair in adaln_inst_*.hip.
+#include <atomic>
+#include <mutex>
+
 #include "adaln_impl.h"
 
 namespace nf {
@@ -244,4 +247,79 @@ extern "C" int nf_adaln_bwd_reduce(void *workspace,
   hipStream_t s = static_cast<hipStream_t>(stream);
   adaln_reduce_kernel<<<(unsigned)((N + kRcCols - 1) / kRcCols), kRcThreads, 0, s>>>(r);
   return check_launch("nf_adaln_bwd_reduce");
+}
+
+// ---------------------------------------------------------------------------
+// The backward with no caller workspace: the partial rows live in `scratch`,
+// a module-scope device array of NF_ADALN_SCRATCH_BYTES.  Every GPU the
+// library runs on holds its own copy (allocated when the code object is
+// loaded on that device, released at process exit).  In host code the name
+// `scratch` is only a stand-in for the symbol, not a device address: the
+// device address comes from hipGetSymbolAddress with that device current,
+// once per device, and only that address reaches the kernels.
+// ---------------------------------------------------------------------------
+namespace {
+constexpr size_t kScratchBytes = NF_ADALN_SCRATCH_BYTES;
+__device__ __align__(256) float scratch[kScratchBytes / sizeof(float)];
+
+constexpr int kMaxDevices = 64;
+std::atomic<void *> g_scratch_ptr[kMaxDevices];
+std::mutex g_scratch_mu;
+
+// This device's copy of `scratch` (the current device's).
+int scratch_of_current_device(void **out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess)
+    return set_error(NF_ERR_LAUNCH, "nf_adaln_bwd_noalloc: hipGetDevice failed: %s",
+                     hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxDevices)
+    return set_error(NF_ERR_ARG, "nf_adaln_bwd_noalloc: device %d beyond %d", dev, kMaxDevices);
+  void *p = g_scratch_ptr[dev].load(std::memory_order_acquire);
+  if (!p) {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    p = g_scratch_ptr[dev].load(std::memory_order_relaxed);
+    if (!p) {
+      e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+      if (e != hipSuccess || !p)
+        return set_error(NF_ERR_LAUNCH,
+                         "nf_adaln_bwd_noalloc: hipGetSymbolAddress(scratch) failed on device "
+                         "%d: %s", dev, hipGetErrorString(e));
+      g_scratch_ptr[dev].store(p, std::memory_order_release);
+    }
+  }
+  *out = p;
+  return NF_OK;
+}
+}  // namespace
+
+extern "C" int nf_adaln_bwd_noalloc(const void *dh_up, const void *dout, const void *x,
+                                    int64_t ld_x, const void *y, int64_t ld_y,
+                                    const void *gate, int64_t ld_gate, const void *weight,
+                                    const void *scale, int64_t ld_scale, const float *rstd,
+                                    void *dx, void *dy, void *dgate, void *dweight,
+                                    void *dscale, void *dshift, int64_t M, int64_t N,
+                                    int64_t T, int dt_x, int dt_y, int dt_gate, int dt_weight,
+                                    int dt_scale, int dt_shift, void *stream) {
+  if (int e = check_shape("nf_adaln_bwd_noalloc", M, N, T)) return e;
+  if (M == 0)  // no rows: the row part is empty, the reductions write dweight = 0
+    return nf_adaln_bwd_reduce(nullptr, 0, weight, scale, ld_scale, dgate, dweight, dscale,
+                               dshift, M, N, T, dt_gate, dt_weight, dt_scale, dt_shift, stream);
+  const size_t need = workspace_bytes(make_plan(M, N, T), N);
+  if (need > kScratchBytes)
+    return set_error(NF_ERR_WORKSPACE,
+                     "nf_adaln_bwd_noalloc: M=%lld N=%lld T=%lld needs %zu bytes of partial "
+                     "rows, more than the %zu-byte static buffer (use nf_adaln_bwd with a "
+                     "workspace)", (long long)M, (long long)N, (long long)T, need,
+                     kScratchBytes);
+  void *ws = nullptr;
+  if (int e = scratch_of_current_device(&ws)) return e;
+  // every partial row the reduction reads is written by the row kernel first
+  // (one full [3, N] row per block), so nothing in the buffer needs clearing
+  if (int e = nf_adaln_bwd(dh_up, dout, x, ld_x, y, ld_y, gate, ld_gate, weight, scale,
+                           ld_scale, rstd, dx, dy, ws, kScratchBytes, M, N, T, dt_x, dt_y,
+                           dt_gate, dt_weight, dt_scale, stream))
+    return e;
+  return nf_adaln_bwd_reduce(ws, kScratchBytes, weight, scale, ld_scale, dgate, dweight, dscale,
+                             dshift, M, N, T, dt_gate, dt_weight, dt_scale, dt_shift, stream);
 }
