@@ -43,11 +43,11 @@ def swiglu_rel_errs(a, b, dout, out, da, db, rows: int = 4096) -> dict:
     m = a.shape[0]
     for r0 in range(0, m, rows):
         sl = slice(r0, min(r0 + rows, m))
-        A, B, G = (t[sl].to("cpu", torch.float32).numpy() for t in (a, b, dout))
+        A, B, G = (t[sl].detach().to("cpu", torch.float32).numpy() for t in (a, b, dout))
         want = {"out": on.swiglu_forward(A, B)}
         want["da"], want["db"] = on.swiglu_backward(A, B, G)
         for k, got in (("out", out), ("da", da), ("db", db)):
-            g = got[sl].to("cpu", torch.float32).numpy()
+            g = got[sl].detach().to("cpu", torch.float32).numpy()
             num[k] = max(num[k], float(np.abs(g - want[k]).max()))
             den[k] = max(den[k], float(np.abs(want[k]).max()))
     return {k: num[k] / den[k] if den[k] else num[k] for k in num}

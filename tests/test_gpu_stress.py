@@ -68,7 +68,7 @@ def test_cfg5_chained_step_matches_oracle_and_its_graph(cuda):
     grads, (act, da, db) = dict(zip(NAMES, rest[:6])), rest[6:]
 
     def f32(v):
-        return v.to("cpu", torch.float32).numpy()
+        return v.detach().to("cpu", torch.float32).numpy()
 
     arr = {k: f32(v) for k, v in inp.items()}
     hw, ow, _ = on.adaln_forward(**arr, t=T)
