@@ -1,18 +1,27 @@
-"""Kernel microbenchmarks in the reference's report format.
+"""Write reports/kernels.json for the reference's RESULTS.md renderer.
 
-Counterpart of ``nuvla_forge/bench/bench_kernels.py`` (217 lines): the same
-command line (``--out``, ``--peak-bw``, ``--dtype``), the same shapes, the
-same timing protocol (events around ``iters`` calls after ``warmup`` calls,
-mean; forward + harness ops + backward, bench_kernels.py:48-58,70-76,104-107)
-and the same ``reports/kernels.json`` schema (``device``, ``peak_bw_gb_s``,
-``dtype``, and ``adaln`` / ``swiglu`` / ``cross_entropy`` row lists with the
-keys bench/report.py:45-80 reads), so an MI355X run renders into the
-reference's RESULTS.md tables unchanged.  The byte counts are the
-reference's (11 * M * N * e for the seam, 8 * M * N * e for SwiGLU,
-bench_kernels.py:84,120); "eager" is the reference formulation
-(``force_reference=True``) on the same device.
+The reference renders its kernel tables from ``reports/kernels.json``
+(``section_kernels``, nuvla_forge/bench/report.py:45-80).  This module writes
+that file from an MI355X run of this build, so the same renderer puts these
+numbers beside the reference's published H100 NVL tables.  What is shared
+with the reference is only what the renderer and the comparison need: the
+file's keys, the shapes of the reference's report, and its byte counts
+(11 * M * N * e for the adaLN seam, 8 * M * N * e for SwiGLU; the reference's
+bench_kernels.py:84,120), so the GB/s columns compare one to one.
+
+Measurement (this build's own protocol):
+  * a seam or SwiGLU case is one forward plus one autograd backward over fresh
+    leaves with pre-drawn upstream gradients, nothing else in the step; the
+    fused op and its eager formulation (``force_reference=True``) are both
+    captured in a HIP graph and timed by replay (``timing.time_graph``), so
+    neither side carries launch or Python costs the other does not;
+  * a cross-entropy case records the peak device memory of loss + backward,
+    fused (``chunk_size`` 1024) against the unchunked eager loss, each from a
+    fresh allocator peak, and both step times (eager launches, events);
+  * every bandwidth row also carries ``hbm_frac`` (GB/s over the peak).
 
     python -m nuvla_forge_amd.bench_kernels [--out reports/kernels.json]
+        [--peak-bw GB_PER_S] [--dtype bfloat16|float16|float32] [--steps K]
 """
 
 from __future__ import annotations
@@ -24,179 +33,162 @@ from pathlib import Path
 import torch
 
 from .kernels import chunked_cross_entropy, fused_adaln_residual_rmsnorm, fused_swiglu
-from .kernels.reference import (
-    adaln_residual_rmsnorm_ref,
-    chunked_cross_entropy_ref,
-    swiglu_ref,
-)
+from .kernels.reference import chunked_cross_entropy_ref
+from .timing import time_eager, time_graph
 
-# Spec-sheet peak HBM bandwidth by gfx architecture (the device name the HIP
-# runtime reports can be generic, e.g. "AMD Radeon Graphics"); --peak-bw
-# overrides.  Used only to put a measurement in context.
-PEAK_BW_GB_S = {
-    "gfx950": 8000.0,   # MI355X / MI350X: HBM3E
-    "gfx942": 5300.0,   # MI300X
-}
-
+# Shapes of the reference's report (bench_kernels.py:187,195,203), so each row
+# has a published counterpart: adaLN (B, T, N), SwiGLU (M, N), CE (M, H, V).
 ADALN_SHAPES = [(8, 32, 384), (8, 128, 384), (16, 256, 768), (8, 512, 1024), (4, 1024, 1536)]
 SWIGLU_SHAPES = [(8192, 1536), (16384, 1536), (32768, 3072)]
 CE_SHAPES = [(4096, 384, 32000), (8192, 384, 32000), (16384, 384, 32000)]
 
+# HBM3E bandwidth of the parts this build targets, by gfx architecture (the
+# runtime's marketing name can be generic, e.g. "AMD Radeon Graphics").
+HBM_GB_S = {"gfx950": 8000.0}
 
-def arch_name(device: int = 0) -> str:
-    return torch.cuda.get_device_properties(device).gcnArchName.split(":")[0]
 
-
-def peak_bw_for(arch: str, override: float | None = None) -> float:
+def device_peak_gb_s(arch: str, override: float | None = None) -> float:
+    """The peak the fractions are taken against: `override` if given, else
+    the spec figure for `arch` (SystemExit for an architecture not listed)."""
     if override:
         return float(override)
-    if arch not in PEAK_BW_GB_S:
-        raise SystemExit(f"no peak bandwidth known for {arch}; pass --peak-bw")
-    return PEAK_BW_GB_S[arch]
+    try:
+        return HBM_GB_S[arch]
+    except KeyError:
+        raise SystemExit(f"{arch}: not an MI355X-class part; pass --peak-bw") from None
 
 
-def bandwidth_gb_s(bytes_moved: int, ms: float) -> float:
-    return bytes_moved / (ms * 1e-3) / 1e9
+def gb_per_s(nbytes: int, ms: float) -> float:
+    return nbytes / ms / 1e6
 
 
-def roofline_note(achieved: float, peak: float) -> str:
-    """The reference's verdict bands (profiling.py:125-142): >80% saturated,
-    >50% healthy, >25% underutilised, else poor."""
-    pct = 100.0 * achieved / peak
-    if pct > 80:
-        verdict = "bandwidth-saturated; no headroom left in this kernel"
-    elif pct > 50:
-        verdict = "healthy; remaining gap is launch overhead and tails"
-    elif pct > 25:
-        verdict = "underutilised; check occupancy and coalescing"
-    else:
-        verdict = "poor; likely uncoalesced or occupancy-starved"
-    return f"{achieved:.0f} GB/s = {pct:.0f}% of {peak:.0f} GB/s peak -- {verdict}"
+def _draw(gen: torch.Generator, dtype, dev):
+    def draw(*shape, std=1.0, mean=0.0):
+        return (torch.randn(*shape, generator=gen) * std + mean).to(dtype).to(dev)
+    return draw
 
 
-def timeit(fn, iters: int = 50, warmup: int = 10) -> float:
-    for _ in range(warmup):
-        fn()
-    torch.cuda.synchronize()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record()
-    for _ in range(iters):
-        fn()
-    e1.record()
-    torch.cuda.synchronize()
-    return e0.elapsed_time(e1) / iters
+def _bandwidth_row(label, dtype, nbytes, make_for, peak, steps, warmup):
+    """Time make_for(force_reference) -> step-factory for both formulations."""
+    fused = time_graph(make_for(False), steps, warmup)[0]
+    eager = time_graph(make_for(True), steps, warmup)[0]
+    rate = gb_per_s(nbytes, fused)
+    return {"shape": label, "dtype": str(dtype).removeprefix("torch."), "eager_ms": eager,
+            "fused_ms": fused, "speedup": eager / fused, "achieved_gb_s": rate,
+            "hbm_frac": rate / peak, "bytes": nbytes}
 
 
-def _dtype_name(dtype: torch.dtype) -> str:
-    return str(dtype).split(".")[-1]
+def seam_row(b, t, n, dtype, dev, peak, steps, warmup):
+    draw = _draw(torch.Generator().manual_seed(b * 7 + t * 5 + n), dtype, dev)
+    tensors = [draw(b * t, n), draw(b * t, n), draw(b, n, std=0.1),
+               draw(n, std=0.02, mean=1.0), draw(b, n, std=0.1), draw(b, n, std=0.1)]
+    upstream = [draw(b * t, n), draw(b * t, n)]
+
+    def make_for(force):
+        def make():
+            leaves = [v.detach().requires_grad_(True) for v in tensors]
+
+            def step():
+                h, out = fused_adaln_residual_rmsnorm(*leaves, tokens_per_sample=t,
+                                                      force_reference=force)
+                return torch.autograd.grad([h, out], leaves, upstream)
+            return step
+        return make
+
+    nbytes = 11 * b * t * n * tensors[0].element_size()
+    return _bandwidth_row(f"B{b}xT{t}xN{n}", dtype, nbytes, make_for, peak, steps, warmup)
 
 
-def bench_adaln(b, t, n, dtype, dev, peak, iters=50, warmup=10):
-    mk = lambda *s: torch.randn(*s, device=dev, dtype=dtype, requires_grad=True)  # noqa: E731
-    args = {"x": mk(b * t, n), "y": mk(b * t, n), "gate": mk(b, n), "weight": mk(n),
-            "scale": mk(b, n), "shift": mk(b, n)}
-    dh = torch.randn(b * t, n, device=dev, dtype=dtype)
-    dout = torch.randn(b * t, n, device=dev, dtype=dtype)
+def swiglu_row(m, n, dtype, dev, peak, steps, warmup):
+    draw = _draw(torch.Generator().manual_seed(m + n), dtype, dev)
+    a, b, grad = draw(m, n), draw(m, n), draw(m, n)
 
-    def run(fn):
-        def inner():
-            for v in args.values():
-                v.grad = None
-            h, o = fn(**args, tokens_per_sample=t)
-            (h * dh + o * dout).sum().backward()
-        return inner
+    def make_for(force):
+        def make():
+            leaves = [a.detach().requires_grad_(True), b.detach().requires_grad_(True)]
 
-    eager_ms = timeit(run(adaln_residual_rmsnorm_ref), iters, warmup)
-    fused_ms = timeit(run(fused_adaln_residual_rmsnorm), iters, warmup)
-    bw = bandwidth_gb_s(11 * b * t * n * dtype.itemsize, fused_ms)
-    return {"shape": f"B{b}xT{t}xN{n}", "dtype": _dtype_name(dtype), "eager_ms": eager_ms,
-            "fused_ms": fused_ms, "speedup": eager_ms / fused_ms, "achieved_gb_s": bw,
-            "roofline": roofline_note(bw, peak)}
+            def step():
+                out = fused_swiglu(*leaves, force_reference=force)
+                return torch.autograd.grad(out, leaves, grad)
+            return step
+        return make
+
+    nbytes = 8 * m * n * a.element_size()
+    return _bandwidth_row(f"{m}x{n}", dtype, nbytes, make_for, peak, steps, warmup)
 
 
-def bench_swiglu(m, n, dtype, dev, peak, iters=50, warmup=10):
-    a = torch.randn(m, n, device=dev, dtype=dtype, requires_grad=True)
-    b = torch.randn(m, n, device=dev, dtype=dtype, requires_grad=True)
-    dout = torch.randn(m, n, device=dev, dtype=dtype)
+def ce_row(m, h, v, dtype, dev, steps, warmup):
+    draw = _draw(torch.Generator().manual_seed(m + h + v), dtype, dev)
+    hidden, weight = draw(m, h), draw(v, h, std=0.02)
+    targets = torch.randint(0, v, (m,), generator=torch.Generator().manual_seed(v)).to(dev)
 
-    def run(fn):
-        def inner():
-            a.grad = b.grad = None
-            fn(a, b).backward(dout)
-        return inner
+    def loss_and_grads(fn):
+        lh, lw = hidden.detach().requires_grad_(True), weight.detach().requires_grad_(True)
+        loss = fn(lh, lw)
+        return (loss, *torch.autograd.grad(loss, [lh, lw]))
 
-    eager_ms = timeit(run(swiglu_ref), iters, warmup)
-    fused_ms = timeit(run(fused_swiglu), iters, warmup)
-    bw = bandwidth_gb_s(8 * m * n * dtype.itemsize, fused_ms)
-    return {"shape": f"{m}x{n}", "dtype": _dtype_name(dtype), "eager_ms": eager_ms,
-            "fused_ms": fused_ms, "speedup": eager_ms / fused_ms, "achieved_gb_s": bw,
-            "roofline": roofline_note(bw, peak)}
+    fused = lambda lh, lw: chunked_cross_entropy(lh, lw, targets, chunk_size=1024)  # noqa: E731
+    eager = lambda lh, lw: chunked_cross_entropy_ref(lh, lw, targets)  # noqa: E731
 
-
-def bench_ce(m, h, v, dtype, dev, iters=10, warmup=3):
-    """Judged on peak memory, as in the reference (bench_kernels.py:134-163)."""
-    hid = torch.randn(m, h, device=dev, dtype=dtype, requires_grad=True)
-    w = torch.randn(v, h, device=dev, dtype=dtype, requires_grad=True)
-    tgt = torch.randint(0, v, (m,), device=dev)
-    row = {"shape": f"M{m}xH{h}xV{v}", "dtype": _dtype_name(dtype)}
-    for name, fn in (("naive", lambda: chunked_cross_entropy_ref(hid, w, tgt)),
-                     ("chunked", lambda: chunked_cross_entropy(hid, w, tgt, chunk_size=1024))):
-        hid.grad = w.grad = None
+    def peak_mib(fn):
+        torch.cuda.synchronize()
         torch.cuda.empty_cache()
         torch.cuda.reset_peak_memory_stats()
-        try:
-            row[f"{name}_ms"] = timeit(lambda: fn().backward(), iters, warmup)  # noqa: B023
-            row[f"{name}_peak_mib"] = torch.cuda.max_memory_allocated() / 2**20
-        except torch.cuda.OutOfMemoryError:
-            row[f"{name}_ms"] = row[f"{name}_peak_mib"] = None
-            row[f"{name}_oom"] = True
-    if row.get("naive_peak_mib") and row.get("chunked_peak_mib"):
+        out = loss_and_grads(fn)
+        torch.cuda.synchronize()
+        del out
+        return torch.cuda.max_memory_allocated() / 2 ** 20
+
+    row = {"shape": f"M{m}xH{h}xV{v}", "dtype": str(dtype).removeprefix("torch.")}
+    row["chunked_peak_mib"] = peak_mib(fused)
+    row["fused_ms"] = time_eager(lambda: loss_and_grads(fused), steps, warmup)
+    try:
+        row["naive_peak_mib"] = peak_mib(eager)
+        row["eager_ms"] = time_eager(lambda: loss_and_grads(eager), steps, warmup)
         row["memory_reduction"] = row["naive_peak_mib"] / row["chunked_peak_mib"]
+    except torch.cuda.OutOfMemoryError:
+        torch.cuda.empty_cache()
+        row["naive_oom"] = True
     return row
 
 
-def run_all(dtype=torch.bfloat16, peak=None, adaln=ADALN_SHAPES, swiglu=SWIGLU_SHAPES,
-            ce=CE_SHAPES, iters=50, warmup=10, log=print):
-    """Measure every shape list; returns the kernels.json report dict."""
+def run_all(dtype=torch.bfloat16, peak_override=None, adaln=ADALN_SHAPES,
+            swiglu=SWIGLU_SHAPES, ce=CE_SHAPES, steps=50, warmup=10, log=print) -> dict:
+    """The whole report as a dict in the schema bench/report.py reads."""
     dev = torch.device("cuda", 0)
-    arch = arch_name()
-    peak = peak_bw_for(arch, peak)
-    report = {"device": f"{torch.cuda.get_device_name(0)} ({arch})", "peak_bw_gb_s": peak,
-              "dtype": _dtype_name(dtype), "adaln": [], "swiglu": [], "cross_entropy": []}
+    arch = torch.cuda.get_device_properties(dev).gcnArchName.split(":")[0]
+    peak = device_peak_gb_s(arch, peak_override)
+    report = {"device": f"{torch.cuda.get_device_name(dev)} ({arch})", "peak_bw_gb_s": peak,
+              "dtype": str(dtype).removeprefix("torch."),
+              "adaln": [], "swiglu": [], "cross_entropy": []}
     for b, t, n in adaln:
-        r = bench_adaln(b, t, n, dtype, dev, peak, iters, warmup)
-        report["adaln"].append(r)
-        log(f"  adaLN  {r['shape']:<16} eager {r['eager_ms']:.3f} ms | fused {r['fused_ms']:.3f} "
-            f"ms | {r['speedup']:.2f}x | {r['roofline']}")
+        report["adaln"].append(seam_row(b, t, n, dtype, dev, peak, steps, warmup))
+        log(report["adaln"][-1])
     for m, n in swiglu:
-        r = bench_swiglu(m, n, dtype, dev, peak, iters, warmup)
-        report["swiglu"].append(r)
-        log(f"  SwiGLU {r['shape']:<16} eager {r['eager_ms']:.3f} ms | fused {r['fused_ms']:.3f} "
-            f"ms | {r['speedup']:.2f}x | {r['roofline']}")
+        report["swiglu"].append(swiglu_row(m, n, dtype, dev, peak, steps, warmup))
+        log(report["swiglu"][-1])
     for m, h, v in ce:
-        r = bench_ce(m, h, v, dtype, dev, max(2, iters // 5), max(1, warmup // 3))
-        report["cross_entropy"].append(r)
-        log(f"  CE     {r['shape']:<16} naive {r.get('naive_peak_mib') or 0:.0f} MiB "
-            f"{r.get('naive_ms') or 0:.3f} ms | chunked {r.get('chunked_peak_mib') or 0:.0f} MiB "
-            f"{r.get('chunked_ms') or 0:.3f} ms")
+        report["cross_entropy"].append(ce_row(m, h, v, dtype, dev, max(3, steps // 5),
+                                              max(1, warmup // 5)))
+        log(report["cross_entropy"][-1])
     return report
 
 
-def main(argv=None) -> int:
+def main() -> None:
     ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
     ap.add_argument("--out", default="reports/kernels.json")
     ap.add_argument("--peak-bw", type=float, default=None)
     ap.add_argument("--dtype", default="bfloat16", choices=["bfloat16", "float16", "float32"])
-    args = ap.parse_args(argv)
+    ap.add_argument("--steps", type=int, default=50)
+    args = ap.parse_args()
     if not torch.cuda.is_available():
-        raise SystemExit("needs a GPU")
-    report = run_all(getattr(torch, args.dtype), args.peak_bw)
+        raise SystemExit("bench_kernels: no ROCm GPU visible")
+    report = run_all(getattr(torch, args.dtype), args.peak_bw, steps=args.steps)
     out = Path(args.out)
     out.parent.mkdir(parents=True, exist_ok=True)
-    out.write_text(json.dumps(report, indent=2))
+    out.write_text(json.dumps(report, indent=2) + "\n")
     print(f"wrote {out}")
-    return 0
 
 
 if __name__ == "__main__":
-    raise SystemExit(main())
+    main()
