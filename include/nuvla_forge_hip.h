@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define NF_ABI_VERSION 2
+#define NF_ABI_VERSION 3
 
 /* element type codes */
 #define NF_DTYPE_F32 0
@@ -202,47 +202,52 @@ int nf_adaln_bwd_noalloc(const void *dh_up, const void *dout, const void *x,
  * (NF_DTYPE_BF16 uses bf16 MFMA with fp32 accumulation, NF_DTYPE_F32 uses
  * fp32 MFMA).  targets is int64 [M].
  *
- * nf_ce_fwd computes the loss and fills `state` (nf_ce_state_bytes(M),
- * 16-byte aligned: per-row lse and target column, inv), which the caller
- * keeps for nf_ce_bwd; `workspace` (nf_ce_fwd_workspace) is scratch.
- * Replaces _ChunkedCrossEntropy.forward's loss and the lse / loss part of
- * the `_ce_fwd_bwd` kernel, nuvla_forge/kernels/chunked_ce.py:49-98 and
+ * Only valid rows do work: the forward compacts them on the device (the
+ * count never reaches the host) and forms each row's logits once, so the
+ * products execute 6 * n * V * D flops (logits, dhidden, dweight).
+ *
+ * nf_ce_fwd computes the loss and fills `state` (nf_ce_state_bytes, 16-byte
+ * aligned), which the caller keeps for nf_ce_bwd; `workspace`
+ * (nf_ce_fwd_workspace) is scratch for the call.  The valid rows are taken
+ * `chunk_rows` at a time (rounded up to 256): a chunk's logits become
+ * (softmax - onehot) * inv in place in the input type, so memory is
+ * O(chunk_rows * V), not O(M * V), as the reference's row chunks
+ * (chunk_size) are; results do not depend on chunk_rows beyond fp rounding.
+ * The forward also runs the gradient products of every chunk but the last
+ * (into fp32 accumulators in `state`).  Replaces _ChunkedCrossEntropy.forward
+ * and the `_ce_fwd_bwd` kernel, nuvla_forge/kernels/chunked_ce.py:49-98 and
  * :120-172.
  *
- * nf_ce_bwd forms the gradients from `state`: `vocab_chunk` columns of
- * (softmax - onehot) exist at a time (bf16 or fp32 like the inputs), so
- * memory is O(M * vocab_chunk), not O(M * V); the reference chunks rows of
- * M, and the result does not depend on either chunking beyond fp rounding.
- * grad_output is a device fp32 scalar (NULL: 1).  dhidden and dweight are
- * written in dt_hidden and dt_weight (fp32, bf16 or fp16: the callers'
- * types), already scaled.  Replaces the gradient half of `_ce_fwd_bwd` and
- * _ChunkedCrossEntropy.backward's scaling and casts, chunked_ce.py:174-182
- * (the reference forms the fp32 gradients in the forward pass and keeps
- * them until the backward).
+ * nf_ce_bwd runs the last chunk's products and writes the gradients already
+ * multiplied by grad_output (a device fp32 scalar, NULL: 1), in dt_hidden
+ * and dt_weight (fp32, bf16 or fp16: the callers' types).  Replaces
+ * _ChunkedCrossEntropy.backward's scaling and casts, chunked_ce.py:174-182.
+ * The same M, D, V, chunk_rows and dtype as the forward.
  * ---------------------------------------------------------------------- */
-size_t nf_ce_state_bytes(int64_t M);
-size_t nf_ce_fwd_workspace(int64_t M, int64_t D, int64_t V, int dtype);
+size_t nf_ce_state_bytes(int64_t M, int64_t D, int64_t V, int64_t chunk_rows,
+                         int dtype);
+size_t nf_ce_fwd_workspace(int64_t M, int64_t D, int64_t V,
+                           int64_t chunk_rows, int dtype);
 int nf_ce_fwd(const void *hidden, const void *weight, const int64_t *targets,
-              int64_t M, int64_t D, int64_t V, int64_t ignore_index, int dtype,
-              float *loss, int32_t *bad_targets, void *state,
-              size_t state_bytes, void *workspace, size_t workspace_bytes,
-              void *stream);
-size_t nf_ce_bwd_workspace(int64_t M, int64_t D, int64_t V,
-                           int64_t vocab_chunk, int dtype);
-int nf_ce_bwd(const void *hidden, const void *weight, int64_t M, int64_t D,
-              int64_t V, int64_t vocab_chunk, int dtype, const void *state,
-              size_t state_bytes, const float *grad_output, void *dhidden,
-              int dt_hidden, void *dweight, int dt_weight, void *workspace,
+              int64_t M, int64_t D, int64_t V, int64_t ignore_index,
+              int64_t chunk_rows, int dtype, float *loss, int32_t *bad_targets,
+              void *state, size_t state_bytes, void *workspace,
               size_t workspace_bytes, void *stream);
+size_t nf_ce_bwd_workspace(int64_t M, int64_t D, int64_t V,
+                           int64_t chunk_rows, int dtype);
+int nf_ce_bwd(int64_t M, int64_t D, int64_t V, int64_t chunk_rows, int dtype,
+              void *state, size_t state_bytes, const float *grad_output,
+              void *dhidden, int dt_hidden, void *dweight, int dt_weight,
+              void *workspace, size_t workspace_bytes, void *stream);
 
 /* Both in one call, the reference's structure (_ce_fwd_bwd,
  * chunked_ce.py:49-98): loss and the unscaled fp32 gradients.  `workspace`
  * (nf_ce_workspace) holds the state and the scratch of both halves. */
-size_t nf_ce_workspace(int64_t M, int64_t D, int64_t V, int64_t vocab_chunk,
+size_t nf_ce_workspace(int64_t M, int64_t D, int64_t V, int64_t chunk_rows,
                        int dtype);
 int nf_ce_fwd_bwd(const void *hidden, const void *weight,
                   const int64_t *targets, int64_t M, int64_t D, int64_t V,
-                  int64_t ignore_index, int64_t vocab_chunk, int dtype,
+                  int64_t ignore_index, int64_t chunk_rows, int dtype,
                   float *loss, float *dhidden, float *dweight,
                   int32_t *bad_targets, void *workspace,
                   size_t workspace_bytes, void *stream);

@@ -14,7 +14,7 @@ from pathlib import Path
 import torch
 
 LIB_PATH = Path(__file__).resolve().with_name("libnf_hip.so")
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 DTYPE_CODE = {torch.float32: 0, torch.bfloat16: 1, torch.float16: 2}
 
@@ -51,16 +51,16 @@ SIGNATURES = {
         [_P, _P, _P, _I64, _P, _I64, _P, _I64, _P, _P, _I64, _P, _P, _P,
          _P, _P, _P, _P, _I64, _I64, _I64, _I32, _I32, _I32, _I32, _I32, _I32, _P],
     ),
-    "nf_ce_state_bytes": (_SZ, [_I64]),
-    "nf_ce_fwd_workspace": (_SZ, [_I64, _I64, _I64, _I32]),
+    "nf_ce_state_bytes": (_SZ, [_I64, _I64, _I64, _I64, _I32]),
+    "nf_ce_fwd_workspace": (_SZ, [_I64, _I64, _I64, _I64, _I32]),
     "nf_ce_fwd": (
         _I32,
-        [_P, _P, _P, _I64, _I64, _I64, _I64, _I32, _P, _P, _P, _SZ, _P, _SZ, _P],
+        [_P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I32, _P, _P, _P, _SZ, _P, _SZ, _P],
     ),
     "nf_ce_bwd_workspace": (_SZ, [_I64, _I64, _I64, _I64, _I32]),
     "nf_ce_bwd": (
         _I32,
-        [_P, _P, _I64, _I64, _I64, _I64, _I32, _P, _SZ, _P, _P, _I32, _P, _I32, _P, _SZ, _P],
+        [_I64, _I64, _I64, _I64, _I32, _P, _SZ, _P, _P, _I32, _P, _I32, _P, _SZ, _P],
     ),
     "nf_ce_workspace": (_SZ, [_I64, _I64, _I64, _I64, _I32]),
     "nf_ce_fwd_bwd": (

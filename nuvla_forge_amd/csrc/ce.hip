@@ -1,28 +1,38 @@
-// Chunked cross entropy on the MFMA GEMM core of gemm_core.h, in two calls
-// (all on the caller's stream, fixed reduction orders throughout).
+// Chunked cross entropy on the MFMA GEMM core of gemm_core.h, in two calls,
+// all on the caller's stream with fixed reduction orders (no atomics).
+//
+// Only valid rows (target != ignore_index, inside [0, V)) do any work: the
+// forward compacts them on the device (no count reaches the host), and every
+// later kernel sizes itself by that device count.  The logits are formed once
+// per row (6 * n_valid * V * D flops in all: logits, dH, dW), never twice.
 //
 // Forward (nf_ce_fwd):
-//   1. ce_stats:  S^T = W H^T tile by tile; per (vocabulary tile, token) the
-//      max and sum of exp(S - max), plus S[m, t_m] for the target column.
-//      S itself is never stored.
-//   2. ce_lse:    lse[m] = combine of the tile partials (fixed order);
-//                 loss_row[m] = lse - S[m, t_m] for valid rows.
-//   3. ce_loss:   one block: n_valid, loss = sum(loss_row) / max(n, 1),
-//                 inv = 1 / max(n, 1).
-//   lse, the target columns and inv are the state the backward reads.
-// Backward (nf_ce_bwd, with the loss's grad_output g):
-//   4. transpose  W [V, D] -> Wt [D, ldwt],  H [M, D] -> Ht [D, ldht]
-//      (zero-padded columns), so every GEMM below is K-contiguous (NT).
-//   5. per vocabulary chunk c of `vocab_chunk` columns:
-//      ce_prob:  recompute S_c^T = W_c H^T; P_c = inv * (softmax - onehot)
-//                (0 for ignored rows) in the input type, written row-major
-//                [M, Vc] and transposed [Vc, M];
-//      dW_c  = g * P_c^T H    (gemm_store, K = M)   -> dweight rows of c, in
-//                                                     dweight's type
-//      dH   += P_c   W_c      (gemm_store, K = Vc)  -> an fp32 accumulator;
-//                                                     the last chunk writes
-//                                                     g * dH in dhidden's type
-// Memory is O(M * vocab_chunk) for P; the [M, V] logits never exist.
+//   1. ce_compact: the valid rows in order -> rows[], their target columns,
+//      pos[m] (compacted index or -1), n_valid, inv = 1 / max(n_valid, 1).
+//   2. gather + transposes: Hc = H[rows] ([M, D], zero past n_valid), its
+//      transpose Hct [D, M], and Wt = W^T [D, V] (zero-padded), so every GEMM
+//      below reads K-contiguous operands.
+//   3. per chunk of `crows` compacted rows:
+//      ce_logits: S = Hc_c W^T tile by tile (formed transposed, W Hc_c^T, so a
+//                 lane holds each token's logits along the vocabulary); per
+//                 (vocabulary tile of WTM rows, token) the max and the sum of
+//                 exp(S - max), the target logit, and E = exp(S - max) in the
+//                 input type, written row-major [crows, ldp];
+//      ce_lse:    lse per row from the tile statistics (fixed order), and the
+//                 row's loss lse - S[target];
+//      ce_fix:    P = inv * (E * exp(max - lse) - onehot) in place, and its
+//                 transpose PT [V, crows];
+//      gradient products of every chunk but the last (one launch):
+//                 dW_acc (+)= PT_c Hc_c      (fp32 [V, D], K = the chunk's rows)
+//                 dHc_c   = P_c Wt^T         (fp32, K = V, split along K)
+//   4. ce_loss:   the mean over the valid rows.
+// Backward (nf_ce_bwd, with the loss's grad_output g): the last chunk's
+// products, dW = g * (dW_acc + PT H_c) written in dweight's type, and the
+// scatter of dHc back to the hidden rows as g * dH (0 for ignored rows).
+//
+// Memory: the state kept between the calls holds one chunk's P and PT, W^T,
+// Hc^T and the fp32 dH rows, plus the fp32 dW accumulator when there is more
+// than one chunk; the [M, V] logits never exist (unless one chunk covers M).
 #include <type_traits>
 
 #include "gemm_store.h"
@@ -32,12 +42,10 @@ namespace ce {
 
 using namespace gemm;
 
-
 // bf16: 256x256 block tiles, 8 wavefronts of 128x64 (two per SIMD, so one
 // wavefront's LDS waits and epilogue overlap the other's MFMAs), operands
-// copied global -> LDS directly in 64-wide K-stages, two stage buffers (one
-// barrier per 64 k: measured ~12% faster than 32-wide stages with four
-// buffers); f32 (correctness path): 128x128 tiles staged through registers.
+// copied global -> LDS directly in 64-wide K-stages, two stage buffers; f32
+// (correctness path): 128x128 tiles staged through registers.
 template <typename TI>
 struct MainCfgT;
 template <>
@@ -52,50 +60,158 @@ __device__ __forceinline__ float log_f32(float x) {
   return __builtin_amdgcn_logf(x) * kLn2;       // log2 on the hardware
 }
 
-// ---------------------------------------------------------------------------
-// Logit statistics of one (vocabulary tile, token tile) block.  The product
-// is formed transposed, acc = W_tile H_tile^T (rows: vocabulary entries,
-// columns: tokens), so each lane holds 16 * TM logits of each of its TN
-// tokens and the per-token max / sum of exp are reductions in registers,
-// then one exchange between the two lane halves and a fixed-order combine
-// of the WM wavefronts that share the token (through LDS).  Writes
-// stats[vtile * M + token] = (max, sum exp(logit - max)) over the tile, and
-// tgt_logit[token] from the block holding the token's target column.
-// ---------------------------------------------------------------------------
 __device__ __forceinline__ float2 combine_stats(float2 a, float2 b) {
   const float m = fmaxf(a.x, b.x);
   if (m == -INFINITY) return make_float2(m, 0.f);
   return make_float2(m, a.y * exp_f32(a.x - m) + b.y * exp_f32(b.x - m));
 }
 
-template <class C, bool BUF>
-__global__ NF_GEMM_BOUNDS(C) void ce_stats_kernel(
-    const typename C::TI *W, const typename C::TI *H, int64_t V, int64_t M, int64_t D,
-    const int64_t *targets, float2 *stats, float *tgt_logit, int vtiles, int mtiles) {
+__device__ __forceinline__ int64_t chunk_count(const int *n_ptr, int64_t j0, int64_t crows) {
+  const int64_t c = (int64_t)__builtin_amdgcn_readfirstlane(*n_ptr) - j0;
+  return c < 0 ? 0 : (c > crows ? crows : c);
+}
+
+// ---------------------------------------------------------------------------
+// 1. compaction of the valid rows, in order.  One block; each round takes
+// 4 x 1024 targets, each wavefront ranks its lanes by a ballot, and the
+// per-wavefront counts are prefixed through LDS in wavefront order.
+// ---------------------------------------------------------------------------
+constexpr int kCompactThreads = 1024, kCompactSub = 4;
+
+__global__ __launch_bounds__(kCompactThreads) void ce_compact_kernel(
+    const int64_t *__restrict__ targets, int64_t M, int64_t V, int64_t ignore_index,
+    int *__restrict__ rows, int *__restrict__ tcol, int *__restrict__ pos, int *n_out,
+    float *inv_out, int *bad_out) {
+  constexpr int kWaves = kCompactThreads / 64;
+  __shared__ int wsum[kCompactSub][kWaves];
+  __shared__ int wbad[kCompactSub][kWaves];
+  const int l = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const uint64_t below = (1ull << l) - 1ull;
+  int carry = 0, bad_total = 0;  // the same in every thread
+  for (int64_t base = 0; base < M; base += kCompactThreads * kCompactSub) {
+    int64_t tg[kCompactSub];
+    bool valid[kCompactSub];
+    int before[kCompactSub];
+#pragma unroll
+    for (int u = 0; u < kCompactSub; ++u) {
+      const int64_t m = base + (int64_t)u * kCompactThreads + threadIdx.x;
+      tg[u] = m < M ? targets[m] : ignore_index;
+      const bool in_range = tg[u] >= 0 && tg[u] < V;
+      valid[u] = m < M && tg[u] != ignore_index && in_range;
+      const bool bad = m < M && tg[u] != ignore_index && !in_range;
+      const uint64_t vm = __ballot(valid[u]);
+      const uint64_t bm = __ballot(bad);
+      before[u] = __popcll(vm & below);
+      if (l == 0) {
+        wsum[u][w] = __popcll(vm);
+        wbad[u][w] = __popcll(bm);
+      }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int u = 0; u < kCompactSub; ++u) {
+      int off = carry, tot = 0, btot = 0;
+      for (int k = 0; k < kWaves; ++k) {
+        off += k < w ? wsum[u][k] : 0;
+        tot += wsum[u][k];
+        btot += wbad[u][k];
+      }
+      const int64_t m = base + (int64_t)u * kCompactThreads + threadIdx.x;
+      if (m < M) {
+        if (valid[u]) {
+          const int idx = off + before[u];
+          rows[idx] = (int)m;
+          tcol[idx] = (int)tg[u];
+          pos[m] = idx;
+        } else {
+          pos[m] = -1;
+        }
+      }
+      carry += tot;
+      bad_total += btot;
+    }
+    __syncthreads();  // wsum / wbad are rewritten by the next round
+  }
+  if (threadIdx.x == 0) {
+    *n_out = carry;
+    *inv_out = 1.f / (float)(carry > 1 ? carry : 1);
+    if (bad_out) *bad_out = bad_total;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// 2. Hc[r, :] = H[rows[r], :] for r < n_valid, 0 for n_valid <= r < R.
+// VEC: 16-byte vectors (D a multiple of the vector width, aligned rows).
+// ---------------------------------------------------------------------------
+template <typename T, bool VEC>
+__global__ __launch_bounds__(256) void ce_gather_kernel(const T *__restrict__ H, int64_t D,
+                                                        const int *__restrict__ rows,
+                                                        const int *n_ptr, int64_t R,
+                                                        T *__restrict__ Hc) {
+  const int64_t n = *n_ptr;
+  constexpr int VE = VEC ? 16 / (int)sizeof(T) : 1;
+  const int64_t dv = D / VE;
+  const int64_t total = R * dv;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total;
+       i += (int64_t)gridDim.x * 256) {
+    const int64_t r = i / dv, c = (i % dv) * VE;
+    if constexpr (VEC) {
+      u32x4 v = {0u, 0u, 0u, 0u};
+      if (r < n) v = *reinterpret_cast<const u32x4 *>(H + (int64_t)rows[r] * D + c);
+      *reinterpret_cast<u32x4 *>(Hc + r * D + c) = v;
+    } else {
+      Hc[r * D + c] = r < n ? H[(int64_t)rows[r] * D + c] : static_cast<T>(0.f);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// 3. logits of one chunk, their tile statistics and E = exp(S - tile max).
+// The product is formed transposed, acc = W_tile Hc_tile^T (rows: vocabulary
+// entries, columns: tokens), so each lane holds 16 * TM logits of each of its
+// TN tokens: a wavefront's max and sum of exp over its WTM vocabulary rows
+// are reductions in registers plus one exchange between the lane halves.
+// Statistics tile t covers vocabulary rows [t * WTM, (t + 1) * WTM):
+// stats[t * crows + token] = (max, sum exp(S - max)).  The target logit comes
+// from the one lane holding it.  E goes out row-major [token, ldp] (columns
+// V..ldp zero): with 16-bit 256 x 256 tiles through LDS (free once the K loop
+// ends) as 16-byte row vectors -- element (t, c) at byte t * 512 +
+// 2 * (c ^ e_swz(t)), the XOR moving whole 8-element vectors so rows still
+// read as vectors while the writes of a half-wave spread over the banks;
+// otherwise straight from the accumulators.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ int e_swz(int t) { return 8 * (((t >> 3) ^ (t & 7)) & 31); }
+
+template <class C, bool BUF, bool SB>
+__global__ NF_GEMM_BOUNDS(C) void ce_logits_kernel(
+    const typename C::TI *W, const typename C::TI *Hc, int64_t V, int64_t D, int64_t j0,
+    int64_t crows, const int *n_ptr, const int *tcol, float2 *stats, float *tgt,
+    typename C::TI *E, int64_t ldp, int vtiles, int ttiles) {
+  using TI = typename C::TI;
+  constexpr int ES = (int)sizeof(TI);
   // one LDS buffer only: a second __shared__ object makes the compiler wait
   // for every direct-to-LDS copy in flight before each operand read of the
-  // K loop (it cannot tell the copies do not write that object); the
-  // per-wavefront partials reuse the operand stages after the K loop
+  // K loop; the E staging reuses the operand stages after the K loop
   __shared__ __attribute__((aligned(16))) char smem[C::LDS_BYTES];
-  static_assert(sizeof(float2) * C::WM * C::BN <= C::LDS_BYTES, "partials do not fit");
-  float2(*red)[C::BN] = reinterpret_cast<float2(*)[C::BN]>(smem);
-  int vt, mt;
-  gemm::group_tile(gemm::xcd_order(blockIdx.x, vtiles * mtiles), vtiles, mtiles,
-                   gemm::kTileGroup, vt, mt);
+  int vt, tt;
+  gemm::group_tile(gemm::xcd_order(blockIdx.x, vtiles * ttiles), vtiles, ttiles,
+                   gemm::kTileGroup, vt, tt);
+  const int64_t cnt = chunk_count(n_ptr, j0, crows);
   const int64_t v0 = (int64_t)vt * C::BM;
-  const int64_t m0 = (int64_t)mt * C::BN;
+  const int64_t t0 = (int64_t)tt * C::BN;  // first token of the tile, chunk-local
+  if (t0 >= cnt) return;
   floatx16 acc[C::TM][C::TN];
-  gemm::mainloop<C, BUF>(W, D, H, D, V, M, D, v0, m0, smem, acc);
+  gemm::mainloop<C, BUF>(W, D, Hc + j0 * D, D, V, cnt, D, v0, t0, smem, acc);
 
   const int l = threadIdx.x & 63, half = l >> 5;
   const int w = threadIdx.x >> 6, wm = w / C::WN, wn = w % C::WN;
-  // vocabulary row of acc[i][*][r]: v0 + wm * WTM + 4 * half + i * 32 + 8 * (r / 4) + r % 4
-  const int64_t vrow0 = v0 + wm * C::WTM + 4 * half;
+  const int64_t vtile0 = v0 + wm * C::WTM;      // first vocabulary row of this wavefront
+  const int64_t crow0 = vtile0 + 4 * half;      // vocabulary row of (i = 0, r = 0)
+  const int stile = vt * C::WM + wm;            // statistics tile
   // Rows past the vocabulary (only in a wavefront whose rows reach V) are set
-  // to -inf once, so the max and the sum below need no per-element masks
-  // (masks kept live across both loops would cost 64 scalar register pairs).
-  if (v0 + wm * C::WTM + C::WTM > V) {
-    const int vlim = (int)(V - vrow0 < C::WTM ? V - vrow0 : C::WTM);
+  // to -inf once, so the max, the sum and E need no per-element masks.
+  if (vtile0 + C::WTM > V) {
+    const int vlim = (int)(V - crow0 < C::WTM ? V - crow0 : C::WTM);
 #pragma unroll
     for (int i = 0; i < C::TM; ++i)
 #pragma unroll
@@ -104,29 +220,23 @@ __global__ NF_GEMM_BOUNDS(C) void ce_stats_kernel(
         for (int r = 0; r < 16; ++r)
           if (i * 32 + 8 * (r >> 2) + (r & 3) >= vlim) acc[i][j][r] = -INFINITY;
   }
+  constexpr bool kStaged = ES == 2 && C::BM == 256 && C::BN == 256 && C::NT == 512 &&
+                           C::LDS_BYTES >= 256 * 512;
+  OutBuf<SB> eout;
+  eout.init(E, crows * ldp * ES);
 #pragma unroll
   for (int j = 0; j < C::TN; ++j) {
-    const int tl = wn * C::WTN + j * 32 + (l & 31);
-    const int64_t tok = m0 + tl;
+    const int tl = wn * C::WTN + j * 32 + (l & 31);  // token within the tile
+    const int64_t tok = t0 + tl;                     // token within the chunk
     float mx = -INFINITY;
 #pragma unroll
     for (int i = 0; i < C::TM; ++i)
 #pragma unroll
       for (int r = 0; r < 16; ++r) mx = fmaxf(mx, acc[i][j][r]);
     mx = fmaxf(mx, __shfl_xor(mx, 32));
-    // a column with no row inside the vocabulary keeps (-inf, 0)
-    const float mref = mx == -INFINITY ? 0.f : mx;
-    float s = 0.f;
-#pragma unroll
-    for (int i = 0; i < C::TM; ++i)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) s += exp_f32(acc[i][j][r] - mref);
-    s += __shfl_xor(s, 32);
-    if (half == 0) red[wm][tl] = make_float2(mx, s);
-
-    // the target logit, from the one lane that holds it
-    if (tok < M) {
-      const int64_t loc64 = targets[tok] - (v0 + wm * C::WTM);
+    // the target logit, from the one lane that holds it (before the exp)
+    if (tok < cnt) {
+      const int64_t loc64 = (int64_t)tcol[j0 + tok] - vtile0;
       const int loc = (int)(loc64 >= 0 && loc64 < C::WTM ? loc64 : -1);
       if (loc >= 0 && ((loc >> 2) & 1) == half) {
         const int want = ((loc >> 5) << 4) | (((loc & 31) >> 3) << 2) | (loc & 3);
@@ -135,47 +245,92 @@ __global__ NF_GEMM_BOUNDS(C) void ce_stats_kernel(
         for (int i = 0; i < C::TM; ++i)
 #pragma unroll
           for (int r = 0; r < 16; ++r) z = (i * 16 + r == want) ? acc[i][j][r] : z;
-        tgt_logit[tok] = z;
+        tgt[tok] = z;
       }
     }
-  }
-  __syncthreads();
-  for (int t = threadIdx.x; t < C::BN; t += C::NT) {
-    const int64_t tok = m0 + t;
-    if (tok >= M) continue;
-    float2 a = red[0][t];
+    // a wavefront with no row inside the vocabulary keeps (-inf, 0) and E = 0
+    const float mref = mx == -INFINITY ? 0.f : mx;
 #pragma unroll
-    for (int q = 1; q < C::WM; ++q) a = combine_stats(a, red[q][t]);
-    stats[(int64_t)vt * M + tok] = a;
+    for (int i = 0; i < C::TM; ++i)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = exp_f32(acc[i][j][r] - mref);
+    float s = 0.f;
+#pragma unroll
+    for (int i = 0; i < C::TM; ++i)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) s += acc[i][j][r];
+    s += __shfl_xor(s, 32);
+    if (half == 0 && tok < cnt) stats[(int64_t)stile * crows + tok] = make_float2(mx, s);
+
+#pragma unroll
+    for (int i = 0; i < C::TM; ++i)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int o = i * 32 + 8 * g;  // offset of r = 4g from crow0
+        TI ev[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) ev[q] = static_cast<TI>(acc[i][j][4 * g + q]);
+        if constexpr (kStaged) {
+          const int cl = wm * C::WTM + 4 * half + o;  // tile column (vocabulary)
+          u32x2 packed;
+          __builtin_memcpy(&packed, ev, 8);
+          *reinterpret_cast<u32x2 *>(smem + tl * 512 + 2 * (cl ^ e_swz(tl))) = packed;
+        } else if constexpr (ES == 2) {
+          u32x2 packed;
+          __builtin_memcpy(&packed, ev, 8);
+          const int64_t c = crow0 + o;
+          eout.st64((tok * ldp + c) * ES, tok < cnt && c < ldp, packed);
+        } else {
+          const int64_t c = crow0 + o;
+#pragma unroll
+          for (int q = 0; q < 4; ++q)
+            eout.st32((tok * ldp + c + q) * ES, tok < cnt && c + q < ldp,
+                      static_cast<float>(ev[q]));
+        }
+      }
+  }
+  if constexpr (kStaged) {
+    __syncthreads();
+    // wavefront w stores tile rows (tokens) 32 w .. 32 w + 31, two per
+    // instruction (one per half-wave), as 16-byte vectors; ldp is a multiple
+    // of 8, so a vector is wholly inside or outside the row
+    const int hv = l >> 5, c8 = 8 * (l & 31);
+#pragma unroll 4
+    for (int it = 0; it < 16; ++it) {
+      const int t = 32 * w + 2 * it + hv;
+      const u32x4 v = *reinterpret_cast<const u32x4 *>(smem + t * 512 + 2 * (c8 ^ e_swz(t)));
+      const int64_t tok = t0 + t, c = v0 + c8;
+      eout.st128((tok * ldp + c) * ES, tok < cnt && c < ldp, v);
+    }
   }
 }
 
 // ---------------------------------------------------------------------------
-// lse per token: a block takes 16 tokens and 16 parts; part q combines
-// vocabulary tiles q, q + 16, q + 32, ... of its token in that order (the
-// loads of four tiles issued before their combines, so a part waits for one
-// load latency per four tiles, not per tile), then the first part combines
-// the 16 partial results in order.  A row of 16 tokens is 128 contiguous
-// bytes of the [ntiles][M] stats.
+// 4. lse per row of a chunk: a block takes 16 rows and 16 parts; part q
+// combines statistics tiles q, q + 16, q + 32, ... of its row in that order
+// (four tiles' loads issued before their combines), then the first part
+// combines the 16 partial results in order.  A row of 16 tokens is 128
+// contiguous bytes of the [ntiles][crows] statistics.
 // ---------------------------------------------------------------------------
 constexpr int kLseRows = 16, kLseParts = 16;
 
 __global__ __launch_bounds__(kLseRows * kLseParts) void ce_lse_kernel(
-    const float2 *__restrict__ stats, int ntiles, const float *tgt_logit,
-    const int64_t *targets, int64_t M, int64_t V, int64_t ignore_index,
-    float *lse, int *tcol, float *loss_row, int *flags) {
+    const float2 *__restrict__ stats, int ntiles, int64_t crows, const float *tgt,
+    const int *n_ptr, int64_t j0, float *lse, float *loss_row) {
   __shared__ float2 part[kLseParts][kLseRows];
+  const int64_t cnt = chunk_count(n_ptr, j0, crows);
   const int rl = threadIdx.x % kLseRows, q = threadIdx.x / kLseRows;
   const int64_t row = (int64_t)blockIdx.x * kLseRows + rl;
+  if ((int64_t)blockIdx.x * kLseRows >= cnt) return;  // the whole block is past the chunk
   float2 a = make_float2(-INFINITY, 0.f);
-  if (row < M) {
+  if (row < cnt) {
     constexpr int kBatch = 4;
     for (int t0 = q; t0 < ntiles; t0 += kLseParts * kBatch) {
       float2 v[kBatch];
 #pragma unroll
       for (int u = 0; u < kBatch; ++u) {
         const int t = t0 + u * kLseParts;
-        v[u] = t < ntiles ? stats[(int64_t)t * M + row] : make_float2(-INFINITY, 0.f);
+        v[u] = t < ntiles ? stats[(int64_t)t * crows + row] : make_float2(-INFINITY, 0.f);
       }
 #pragma unroll
       for (int u = 0; u < kBatch; ++u) a = combine_stats(a, v[u]);
@@ -183,206 +338,150 @@ __global__ __launch_bounds__(kLseRows * kLseParts) void ce_lse_kernel(
   }
   part[q][rl] = a;
   __syncthreads();
-  if (q != 0 || row >= M) return;
+  if (q != 0 || row >= cnt) return;
 #pragma unroll
   for (int k = 1; k < kLseParts; ++k) a = combine_stats(a, part[k][rl]);
   const float ls = a.x + log_f32(a.y);
-  const int64_t tg = targets[row];
-  const bool in_range = tg >= 0 && tg < V;
-  const bool valid = tg != ignore_index && in_range;
   lse[row] = ls;
-  tcol[row] = valid ? (int)tg : -1;
-  loss_row[row] = valid ? ls - tgt_logit[row] : 0.f;
-  flags[row] = (valid ? 1 : 0) | ((tg != ignore_index && !in_range) ? 2 : 0);
+  loss_row[j0 + row] = ls - tgt[row];
 }
 
 // ---------------------------------------------------------------------------
-// loss, n_valid, inv_count: one block; each thread sums a strided share of
-// the rows, each wavefront reduces its lanes (fixed butterfly), and thread 0
-// adds the 16 wavefront sums in order.
+// 5. P = inv * (E * exp(tile max - lse) - onehot) for the rows of a chunk, in
+// place ([crows, ldp], columns V..ldp zero), and PT [V, crows] (rows count
+// .. round_up(count, 8) zero: the dW product's K padding).  A block takes a
+// 64 x 64 tile (64 rows, 64 vocabulary columns inside one statistics tile):
+// its 64 row factors come from the statistics once, the tile is read and
+// written as 16-byte row vectors and transposed through LDS into 16-byte
+// PT vectors.
+// ---------------------------------------------------------------------------
+template <typename TI>
+__global__ __launch_bounds__(256) void ce_fix_kernel(TI *__restrict__ P, int64_t ldp,
+                                                     TI *__restrict__ PT, int64_t crows,
+                                                     int64_t V, const float2 *__restrict__ stats,
+                                                     int wtm, const float *__restrict__ lse,
+                                                     const int *__restrict__ tcol,
+                                                     const int *n_ptr, int64_t j0,
+                                                     const float *inv_ptr) {
+  using U = typename std::conditional<sizeof(TI) == 2, uint16_t, uint32_t>::type;
+  constexpr int VE = 16 / (int)sizeof(TI);  // elements per 16-byte vector
+  constexpr int VPR = 64 / VE;              // vectors per 64-element row
+  constexpr int PITCH = 64 + (sizeof(TI) == 2 ? 2 : 1);
+  __shared__ U tile[64 * PITCH];
+  __shared__ float fac[64];
+  __shared__ int tcl[64];
+  const int64_t cnt = chunk_count(n_ptr, j0, crows);
+  const int64_t rows8 = (cnt + 7) / 8 * 8;
+  const int64_t r0 = (int64_t)blockIdx.x * 64, c0 = (int64_t)blockIdx.y * 64;
+  if (r0 >= rows8) return;
+  const int t = threadIdx.x;
+  if (t < 64) {
+    const int64_t r = r0 + t;
+    float f = 0.f;
+    int tc = -1;
+    if (r < cnt) {
+      const float m = stats[(c0 / wtm) * crows + r].x;
+      f = m == -INFINITY ? 0.f : exp_f32(m - lse[r]);
+      tc = tcol[j0 + r];
+    }
+    fac[t] = f;
+    tcl[t] = tc;
+  }
+  const float inv = *inv_ptr;
+  __syncthreads();
+  for (int idx = t; idx < 64 * VPR; idx += 256) {
+    const int rr = idx / VPR, cv = idx % VPR;
+    const int64_t r = r0 + rr, c = c0 + (int64_t)cv * VE;
+    if (c >= ldp) continue;  // ldp is a multiple of VE
+    TI *p = P + r * ldp + c;
+    TI e[VE];
+    if (r < cnt) {
+      *reinterpret_cast<u32x4 *>(e) = *reinterpret_cast<const u32x4 *>(p);
+      const float f = fac[rr];
+      const int tc = tcl[rr];
+#pragma unroll
+      for (int q = 0; q < VE; ++q) {
+        const int64_t col = c + q;
+        const float v = static_cast<float>(e[q]) * f - (col == tc ? 1.f : 0.f);
+        e[q] = static_cast<TI>(col < V ? v * inv : 0.f);
+      }
+    } else {
+#pragma unroll
+      for (int q = 0; q < VE; ++q) e[q] = static_cast<TI>(0.f);
+    }
+    if (r < crows) *reinterpret_cast<u32x4 *>(p) = *reinterpret_cast<const u32x4 *>(e);
+#pragma unroll
+    for (int q = 0; q < VE; ++q) {
+      U bits;
+      __builtin_memcpy(&bits, &e[q], sizeof(U));
+      tile[rr * PITCH + cv * VE + q] = bits;
+    }
+  }
+  __syncthreads();
+  for (int idx = t; idx < 64 * VPR; idx += 256) {
+    const int cc = idx / VPR, rv = idx % VPR;  // vocabulary column, row vector
+    const int64_t col = c0 + cc, r = r0 + (int64_t)rv * VE;
+    if (col >= V || r >= rows8) continue;  // rows8 is a multiple of VE
+    U e[VE];
+#pragma unroll
+    for (int q = 0; q < VE; ++q) e[q] = tile[(rv * VE + q) * PITCH + cc];
+    *reinterpret_cast<u32x4 *>(PT + col * crows + r) = *reinterpret_cast<const u32x4 *>(e);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// 6. loss = inv * sum of the valid rows' losses: one block; each thread sums
+// a strided share of the rows, each wavefront reduces its lanes (fixed
+// butterfly), and thread 0 adds the 16 wavefront sums in order.
 // ---------------------------------------------------------------------------
 constexpr int kLossThreads = 1024;
 
-__device__ __forceinline__ int wave_sum_int(int v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
-  return v;
-}
-
-__global__ __launch_bounds__(kLossThreads) void ce_loss_kernel(
-    const float *loss_row, const int *flags, int64_t M, float *loss,
-    float *inv_out, int *bad_out) {
+__global__ __launch_bounds__(kLossThreads) void ce_loss_kernel(const float *loss_row,
+                                                                const int *n_ptr,
+                                                                const float *inv_ptr,
+                                                                float *loss) {
   constexpr int kWaves = kLossThreads / 64;
   __shared__ float sl[kWaves];
-  __shared__ int sn[kWaves], sb[kWaves];
+  const int64_t n = *n_ptr;
   float a = 0.f;
-  int n = 0, bad = 0;
-  for (int64_t i = threadIdx.x; i < M; i += kLossThreads) {
-    a += loss_row[i];
-    n += flags[i] & 1;
-    bad += (flags[i] >> 1) & 1;
-  }
+  for (int64_t i = threadIdx.x; i < n; i += kLossThreads) a += loss_row[i];
   a = wave_sum(a);
-  n = wave_sum_int(n);
-  bad = wave_sum_int(bad);
-  const int w = threadIdx.x >> 6;
-  if ((threadIdx.x & 63) == 0) {
-    sl[w] = a;
-    sn[w] = n;
-    sb[w] = bad;
-  }
+  if ((threadIdx.x & 63) == 0) sl[threadIdx.x >> 6] = a;
   __syncthreads();
   if (threadIdx.x == 0) {
     float tl = 0.f;
-    int tn = 0, tb = 0;
-    for (int k = 0; k < kWaves; ++k) {
-      tl += sl[k];
-      tn += sn[k];
-      tb += sb[k];
-    }
-    const float inv = 1.f / (float)(tn > 1 ? tn : 1);
-    *loss = tl * inv;
-    *inv_out = inv;
-    if (bad_out) *bad_out = tb;
+    for (int k = 0; k < kWaves; ++k) tl += sl[k];
+    *loss = tl * *inv_ptr;
   }
 }
 
 // ---------------------------------------------------------------------------
-// probability epilogue: P = inv * (softmax - onehot) for one vocabulary
-// chunk, from the transposed product acc = Wc_tile H_tile^T (rows: chunk
-// columns, columns: tokens).  Each lane's TN tokens bring their lse, target
-// and scale in registers.  Writes P [M, ldp] (token rows; columns [Vc, kpad)
-// zero) and PT [Vc, ldpt] (chunk-column rows; tokens [M, ldpt) zero).
-//
-// 16-bit tiles of 256 x 256 go through LDS (free once the K loop ends): the
-// lanes write their values as a [token][chunk column] tile, 4 columns (8
-// bytes) at a time, and both outputs then leave as 16-byte row vectors, P
-// from the tile's rows and PT from its columns (8 two-byte LDS reads per
-// vector).  A lane's own values would give 8-byte P stores spread over 64
-// rows and 2-byte PT stores.  Element (t, c) sits at byte
-// t * 512 + 2 * (c ^ prob_swz(t)): the XOR term moves whole 8-element
-// vectors, so rows still read as vectors, and spreads the column reads of a
-// half-wave (tokens 8 l + k, l < 32) over the banks.
+// 7. dH[m, :] = g * dHc[pos[m], :] in dH's type, 0 where pos[m] < 0.
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ int prob_swz(int t) { return 8 * (((t >> 3) ^ (t & 7)) & 31); }
-
-template <class C, bool BUF, bool SB>
-__global__ NF_GEMM_BOUNDS(C) void ce_prob_kernel(
-    const typename C::TI *Wc, const typename C::TI *H, int64_t Vc, int64_t M, int64_t D,
-    int64_t vbase, const int *tcol, const float *lse, const float *inv_ptr,
-    typename C::TI *P, int64_t ldp, int64_t kpad, typename C::TI *PT, int64_t ldpt, int vtiles,
-    int mtiles) {
-  using TI = typename C::TI;
-  constexpr int ES = (int)sizeof(TI);
-  __shared__ __attribute__((aligned(16))) char smem[C::LDS_BYTES];
-  int vt, mt;
-  gemm::group_tile(gemm::xcd_order(blockIdx.x, vtiles * mtiles), vtiles, mtiles,
-                   gemm::kTileGroup, vt, mt);
-  const int64_t v0 = (int64_t)vt * C::BM;
-  const int64_t m0 = (int64_t)mt * C::BN;
-  floatx16 acc[C::TM][C::TN];
-  gemm::mainloop<C, BUF>(Wc, D, H, D, Vc, M, D, v0, m0, smem, acc);
-  const float inv = *inv_ptr;
-
-  const int l = threadIdx.x & 63, half = l >> 5;
-  const int w = threadIdx.x >> 6, wm = w / C::WN, wn = w % C::WN;
-  const int64_t crow0 = v0 + wm * C::WTM + 4 * half;  // chunk column of (i = 0, r = 0)
-  OutBuf<SB> pout, ptout;
-  pout.init(P, M * ldp * ES);
-  ptout.init(PT, Vc * ldpt * ES);
-  constexpr bool kStaged = ES == 2 && C::BM == 256 && C::BN == 256 && C::NT == 512 &&
-                           C::LDS_BYTES >= 256 * 512;
-  // Rows past the chunk (only in a wavefront whose rows reach Vc) are set to
-  // -inf once, so their probabilities come out 0 without per-element masks
-  // (masks kept live through the loop would cost 64 scalar register pairs).
-  if (v0 + wm * C::WTM + C::WTM > Vc) {
-    const int vlim = (int)(Vc - crow0 < C::WTM ? Vc - crow0 : C::WTM);
-#pragma unroll
-    for (int i = 0; i < C::TM; ++i)
-#pragma unroll
-      for (int j = 0; j < C::TN; ++j)
-#pragma unroll
-        for (int r = 0; r < 16; ++r)
-          if (i * 32 + 8 * (r >> 2) + (r & 3) >= vlim) acc[i][j][r] = -INFINITY;
-  }
-#pragma unroll
-  for (int j = 0; j < C::TN; ++j) {
-    const int64_t tok = m0 + wn * C::WTN + j * 32 + (l & 31);
-    const int tc = tok < M ? tcol[tok] : -1;
-    const float ls = tok < M ? lse[tok] : 0.f;
-    const bool keep = tc >= 0;  // counted token: P row = inv * (softmax - onehot)
-    // the target's offset from crow0 when it lies in this chunk's Vc columns,
-    // else -1 (a row past Vc may be a later chunk's column: no onehot there)
-    const int64_t tin = (int64_t)tc - vbase;
-    const int tloc = (keep && tin >= 0 && tin < Vc) ? (int)(tin - crow0) : -1;
-#pragma unroll
-    for (int i = 0; i < C::TM; ++i)
-#pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const int o = i * 32 + 8 * g;  // offset of r = 4g from crow0
-        float p[4];
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const float e = exp_f32(acc[i][j][4 * g + q] - ls) - (tloc == o + q ? 1.f : 0.f);
-          p[q] = keep ? e * inv : 0.f;
-        }
-        TI pv[4];
-#pragma unroll
-        for (int q = 0; q < 4; ++q) pv[q] = static_cast<TI>(p[q]);
-        const int64_t c = crow0 + o;
-        if constexpr (kStaged) {
-          const int t = wn * C::WTN + j * 32 + (l & 31);  // tile token
-          const int cl = wm * C::WTM + 4 * half + o;       // tile chunk column
-          u32x2 packed;
-          __builtin_memcpy(&packed, pv, 8);
-          *reinterpret_cast<u32x2 *>(smem + t * 512 + 2 * (cl ^ prob_swz(t))) = packed;
-        } else if constexpr (ES == 2) {
-          u32x2 packed;
-          __builtin_memcpy(&packed, pv, 8);
-          pout.st64((tok * ldp + c) * ES, tok < M && c < kpad, packed);
-#pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            uint16_t bits;
-            __builtin_memcpy(&bits, &pv[q], 2);
-            ptout.st16(((c + q) * ldpt + tok) * ES, c + q < Vc && tok < ldpt, bits);
-          }
-        } else {
-#pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            pout.st32((tok * ldp + c + q) * ES, tok < M && c + q < kpad, p[q]);
-            ptout.st32(((c + q) * ldpt + tok) * ES, c + q < Vc && tok < ldpt, p[q]);
-          }
-        }
-      }
-  }
-  if constexpr (kStaged) {
-    __syncthreads();
-    // Out-of-range tokens and chunk columns hold zeros in the tile; a vector
-    // is stored when its first element is in range (kpad and ldpt are
-    // multiples of 8, so a vector is wholly inside or outside).  Wavefront w
-    // stores tile rows (P) and tile columns (PT) 32 w .. 32 w + 31, two per
-    // instruction, one per half-wave.
-    const int hv = l >> 5, c8 = 8 * (l & 31);
-#pragma unroll 4
-    for (int it = 0; it < 16; ++it) {
-      const int t = 32 * w + 2 * it + hv;
-      const u32x4 v = *reinterpret_cast<const u32x4 *>(smem + t * 512 + 2 * (c8 ^ prob_swz(t)));
-      const int64_t tok = m0 + t, c = v0 + c8;
-      pout.st128((tok * ldp + c) * ES, tok < M && c < kpad, v);
+// VE elements per thread step (4 when D is a multiple of 4: one 16-byte load).
+template <int VE>
+__global__ __launch_bounds__(256) void ce_scatter_dh_kernel(const float *__restrict__ dHc,
+                                                            int64_t D,
+                                                            const int *__restrict__ pos,
+                                                            int64_t M, const float *g_ptr,
+                                                            void *dH, int dt) {
+  const float g = g_ptr ? *g_ptr : 1.f;
+  const int64_t dv = D / VE;
+  const int64_t total = M * dv;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total;
+       i += (int64_t)gridDim.x * 256) {
+    const int64_t m = i / dv, c = (i - m * dv) * VE;
+    const int p = pos[m];
+    float v[VE];
+    if constexpr (VE == 4) {
+      const float4 q = p >= 0 ? *reinterpret_cast<const float4 *>(dHc + (int64_t)p * D + c)
+                              : make_float4(0.f, 0.f, 0.f, 0.f);
+      v[0] = q.x; v[1] = q.y; v[2] = q.z; v[3] = q.w;
+    } else {
+      v[0] = p >= 0 ? dHc[(int64_t)p * D + c] : 0.f;
     }
-#pragma unroll 4
-    for (int it = 0; it < 16; ++it) {
-      const int c = 32 * w + 2 * it + hv;
-      uint16_t e[8];
 #pragma unroll
-      for (int k = 0; k < 8; ++k)
-        e[k] = *reinterpret_cast<const uint16_t *>(smem + (c8 + k) * 512 +
-                                                   2 * (c ^ prob_swz(c8 + k)));
-      u32x4 v;
-      __builtin_memcpy(&v, e, 16);
-      const int64_t crow = v0 + c, tok = m0 + c8;
-      ptout.st128((crow * ldpt + tok) * ES, crow < Vc && tok < ldpt, v);
-    }
+    for (int k = 0; k < VE; ++k) store_dyn(dH, dt, m * D + c + k, v[k] * g);
   }
 }
 
@@ -390,238 +489,242 @@ __global__ NF_GEMM_BOUNDS(C) void ce_prob_kernel(
 // host side
 // ---------------------------------------------------------------------------
 
-// K splits of a vocabulary chunk's two gradient products.  The chunk's dW
-// blocks (K = tokens) and dH blocks (K = chunk columns) run in one launch.
-// When that launch fits in one wave of the 256 CUs, its time is the longest
-// block's K; splitting the job with the longer K into S slices shortens it
-// at the cost of more blocks.  S is chosen (1 .. 64) to minimise
-// waves(blocks) x longest slice, ties to fewer slices: e.g. the reasoning
-// head (M 512, D 384, the whole vocabulary in one chunk: 4 dH tiles of K
-// 32000 beside 250 dW tiles of K 512) splits dH 63 ways, M 16384 with D 384
-// and 2048-column chunks (16 dW tiles of K 16384) splits dW 8 ways, and the
-// BASELINE shape (128 + 128 tiles of K 4096) is not split.  Slices are summed
-// by splitk_reduce_kernel in a fixed order.
+// K split of a chunk's dH product.  The launch holding a chunk's gradient
+// products has the dW blocks (K = the chunk's rows, crows) and the dH blocks
+// (K = V, long); dH is split into S slices to balance them: S minimises the
+// launch's makespan, max(longest block, total work / 256 CUs), plus the
+// write and read of the S fp32 slices, all in units of one 64-deep K stage of
+// a 256 x 256 tile (~2 us per CU at ~1.1 PFLOP/s, against ~5 TB/s of HBM).
+// A slice is at most kMaxSlice deep: a block streams 256 rows of each
+// operand over its K, and beyond ~2 MB per operand panel (4096 bf16 k) the
+// blocks an XCD runs at once no longer share their panels in its 4 MB L2 --
+// an unsplit K of 32000 measured 3.0 ms for the cfg4 gradients, bandwidth
+// bound, against ~0.9 ms of MFMA work.
+constexpr int64_t kMaxSlice = 4096;
 struct Split {
   int S;
   int64_t kslice;
 };
-struct SplitPlan {
-  Split w, h;  // dW, dH
-};
 template <class C>
-inline Split best_split(int64_t t_short, int64_t k_short, int64_t t_long, int64_t k_long) {
-  Split best{1, k_long};
-  int64_t best_t = -1;
-  for (int64_t S = 1; S <= 64; ++S) {
-    const int64_t ks = round_up((k_long + S - 1) / S, C::BK);
-    const int64_t se = (k_long + ks - 1) / ks;
-    const int64_t waves = (t_short + t_long * se + 255) / 256;
-    const int64_t t = waves * (k_short > ks ? k_short : ks);
-    if (best_t < 0 || t < best_t) {
+inline Split dh_split(int64_t crows, int64_t D, int64_t V, int64_t ldp) {
+  const int64_t tn = (D + C::BN - 1) / C::BN;
+  const double tw = (double)((V + C::BM - 1) / C::BM * tn);
+  const double th = (double)((crows + C::BM - 1) / C::BM * tn);
+  const double kw = (double)crows / C::BK;
+  const double stage_s = 2e-6, hbm_bps = 5e12;
+  Split best{1, ldp};
+  double best_t = -1.0;
+  for (int S = 1; S <= 64; ++S) {
+    const int64_t ks = round_up((ldp + S - 1) / S, C::BK);
+    const int64_t se = (ldp + ks - 1) / ks;
+    if (ks > kMaxSlice && S < 64) continue;
+    const double kh = (double)ks / C::BK;
+    const double work = tw * kw + th * (double)se * kh;
+    double t = work / 256.0;
+    if (kh > t) t = kh;
+    if (kw > t) t = kw;
+    if (se > 1) t += 2.0 * se * crows * D * 4.0 / hbm_bps / stage_s;
+    if (best_t < 0 || t < best_t - 1e-9) {
       best_t = t;
       best = {(int)se, ks};
     }
   }
   return best;
 }
-template <class C>
-inline SplitPlan chunk_split(int64_t vc, int64_t M, int64_t D) {
-  const int64_t tn = (D + C::BN - 1) / C::BN;
-  const int64_t tw = (vc + C::BM - 1) / C::BM * tn, th = (M + C::BM - 1) / C::BM * tn;
-  const int64_t kh = round_up(vc, 8), kw = round_up(M, 8);
-  SplitPlan p{{1, kw}, {1, kh}};
-  if (tw + th >= 256) return p;  // a full wave or more: the blocks already balance
-  if (kh >= kw)
-    p.h = best_split<C>(tw, kw, th, kh);
-  else
-    p.w = best_split<C>(th, kh, tw, kw);
-  return p;
-}
 
-// Per-row state the backward reads: lse [M], the target column [M] (-1: the
-// row has no gradient) and the scalars (inv = 1 / max(n_valid, 1)).
-struct StateLayout {
-  size_t off_lse, off_tcol, off_scal, total;
+struct Plan {
+  int64_t crows, nch;     // compacted rows per chunk (a multiple of 256), chunks
+  int64_t ldp, ldwt, ldht;
+  int wtm, ntiles;        // statistics tile height and count
+  int vtiles, ttiles;     // logits grid
+  Split split;            // dH product's K split
+  // state (kept from nf_ce_fwd to nf_ce_bwd)
+  size_t s_scal, s_pos, s_wt, s_hct, s_p, s_pt, s_dhc, s_dwacc, s_total;
+  // forward scratch
+  size_t f_hc, f_rows, f_tcol, f_stats, f_tgt, f_lse, f_loss, f_part, f_total;
+  // backward scratch
+  size_t b_part, b_total;
 };
-inline StateLayout state_layout(int64_t M) {
-  StateLayout L{};
+
+template <typename TI>
+inline Plan make_plan(int64_t M, int64_t D, int64_t V, int64_t chunk_rows) {
+  using C = MainCfg<TI>;
+  const size_t es = sizeof(TI);
+  Plan P{};
+  const int64_t mcap = round_up(M, 256);
+  int64_t cr = round_up(chunk_rows < 1 ? 1 : chunk_rows, 256);
+  P.crows = cr > mcap ? mcap : cr;
+  P.nch = (M + P.crows - 1) / P.crows;
+  P.ldp = round_up(V, 8);
+  P.ldwt = P.ldp;
+  P.ldht = round_up(M, 8);
+  P.wtm = C::WTM;
+  P.vtiles = (int)((V + C::BM - 1) / C::BM);
+  P.ntiles = P.vtiles * C::WM;
+  P.ttiles = (int)(P.crows / C::BN);
+  P.split = dh_split<C>(P.crows, D, V, P.ldp);
+  const size_t part = P.split.S > 1 ? (size_t)P.split.S * P.crows * D * sizeof(float) : 0;
   size_t o = 0;
   auto take = [&](size_t bytes) { const size_t at = o; o = align256(o + bytes); return at; };
-  L.off_lse = take((size_t)M * sizeof(float));
-  L.off_tcol = take((size_t)M * sizeof(int));
-  L.off_scal = take(64);
-  L.total = o;
-  return L;
+  P.s_scal = take(64);  // n_valid (int), inv (float)
+  P.s_pos = take((size_t)M * sizeof(int));
+  P.s_wt = take((size_t)D * P.ldwt * es);
+  P.s_hct = take((size_t)D * P.ldht * es);
+  P.s_p = take((size_t)P.crows * P.ldp * es);
+  P.s_pt = take((size_t)V * P.crows * es);
+  P.s_dhc = take((size_t)M * D * sizeof(float));
+  P.s_dwacc = take(P.nch > 1 ? (size_t)V * D * sizeof(float) : 0);
+  P.s_total = o;
+  o = 0;
+  P.f_hc = take((size_t)M * D * es);
+  P.f_rows = take((size_t)M * sizeof(int));
+  P.f_tcol = take((size_t)M * sizeof(int));
+  P.f_stats = take((size_t)P.ntiles * P.crows * sizeof(float2));
+  P.f_tgt = take((size_t)P.crows * sizeof(float));
+  P.f_lse = take((size_t)P.crows * sizeof(float));
+  P.f_loss = take((size_t)M * sizeof(float));
+  P.f_part = take(P.nch > 1 ? part : 0);
+  P.f_total = o;
+  o = 0;
+  P.b_part = take(part);
+  P.b_total = o;
+  return P;
 }
 
-// Forward scratch: per (vocabulary tile, token) stats, the target logits,
-// the row losses and the row flags.
-struct FwdLayout {
-  int64_t ntiles;
-  size_t off_stats, off_tgt, off_loss, off_flags, total;
+// Pointers into the state.
+template <typename TI>
+struct StateView {
+  int *n;
+  float *inv;
+  int *pos;
+  TI *Wt, *Hct, *P, *PT;
+  float *dHc, *dWacc;
+  StateView(const Plan &L, char *s)
+      : n(reinterpret_cast<int *>(s + L.s_scal)),
+        inv(reinterpret_cast<float *>(s + L.s_scal + 16)),
+        pos(reinterpret_cast<int *>(s + L.s_pos)),
+        Wt(reinterpret_cast<TI *>(s + L.s_wt)),
+        Hct(reinterpret_cast<TI *>(s + L.s_hct)),
+        P(reinterpret_cast<TI *>(s + L.s_p)),
+        PT(reinterpret_cast<TI *>(s + L.s_pt)),
+        dHc(reinterpret_cast<float *>(s + L.s_dhc)),
+        dWacc(reinterpret_cast<float *>(s + L.s_dwacc)) {}
 };
-inline FwdLayout fwd_layout(int64_t M, int64_t V, int es) {
-  FwdLayout L{};
-  const int64_t bm = es == 2 ? MainCfg<bf16>::BM : MainCfg<float>::BM;
-  L.ntiles = (V + bm - 1) / bm;  // vocabulary tiles
-  size_t o = 0;
-  auto take = [&](size_t bytes) { const size_t at = o; o = align256(o + bytes); return at; };
-  L.off_stats = take((size_t)L.ntiles * M * sizeof(float2));  // [ntiles][M]
-  L.off_tgt = take((size_t)M * sizeof(float));
-  L.off_loss = take((size_t)M * sizeof(float));
-  L.off_flags = take((size_t)M * sizeof(int));
-  L.total = o;
-  return L;
-}
 
-template <class C>
-inline size_t partial_bytes(int64_t M, int64_t D, int64_t V, int64_t vc) {
-  size_t most = 0;
-  for (int64_t vb = 0; vb < V; vb += vc) {
-    const int64_t c = V - vb < vc ? V - vb : vc;
-    const SplitPlan sp = chunk_split<C>(c, M, D);
-    const size_t bw = sp.w.S > 1 ? (size_t)sp.w.S * c * D * sizeof(float) : 0;
-    const size_t bh = sp.h.S > 1 ? (size_t)sp.h.S * M * D * sizeof(float) : 0;
-    const size_t b = bw > bh ? bw : bh;  // at most one of the two is split
-    if (b > most) most = b;
+// The gradient products of chunk c in one launch: dW (+)= PT_c Hc_c and
+// dHc_c = P_c Wt^T (split along K).  dW goes to `dw_out` (type dt_w, scaled
+// by g when given) on top of `dw_in` when given.
+template <typename TI>
+int launch_grads(const Plan &L, const StateView<TI> &S, int64_t c, int64_t D, int64_t V,
+                 const float *dw_in, void *dw_out, int dt_w, const float *g, float *part,
+                 hipStream_t s) {
+  using C = MainCfg<TI>;
+  const int64_t j0 = c * L.crows;
+  auto jw = make_job<C>(S.PT, L.crows, S.Hct + j0, L.ldht, dw_in, dw_out, dt_w, g, D, V, D,
+                        L.crows);
+  jw.dyn = S.n;
+  jw.dyn_base = j0;
+  jw.dyn_rows = 0;  // K: the chunk's rows
+  auto jh = make_job<C>(S.P, L.ldp, S.Wt, L.ldwt, nullptr, S.dHc + j0 * D, NF_DTYPE_F32,
+                        nullptr, D, L.crows, D, L.ldp);
+  jh.dyn = S.n;
+  jh.dyn_base = j0;
+  jh.dyn_rows = 1;  // M: the chunk's rows
+  if (L.split.S > 1) {
+    jh.ksplit = L.split.S;
+    jh.kslice = L.split.kslice;
+    jh.part = part;
+    jh.tiles *= L.split.S;
   }
-  return most;
+  // the longest blocks go first
+  return L.split.kslice > L.crows ? launch_gemm_store<C>(jh, jw, s)
+                                  : launch_gemm_store<C>(jw, jh, s);
 }
 
-// Backward scratch: W^T, H^T, one chunk's P and P^T, split-K partials, and
-// the fp32 dH accumulator when the vocabulary takes more than one chunk.
-struct BwdLayout {
-  int64_t ldwt, ldht, vc, ldp;
-  size_t off_wt, off_ht, off_p, off_pt, off_part, off_dh, total;
-};
-inline BwdLayout bwd_layout(int64_t M, int64_t D, int64_t V, int64_t vocab_chunk, int es) {
-  BwdLayout L{};
-  L.ldwt = round_up(V, 8);
-  L.ldht = round_up(M, 8);
-  L.vc = round_up(vocab_chunk < V ? vocab_chunk : V, 8);
-  L.ldp = L.vc;
-  const size_t part = es == 2 ? partial_bytes<MainCfg<bf16>>(M, D, V, L.vc)
-                              : partial_bytes<MainCfg<float>>(M, D, V, L.vc);
-  size_t o = 0;
-  auto take = [&](size_t bytes) { const size_t at = o; o = align256(o + bytes); return at; };
-  L.off_wt = take((size_t)D * L.ldwt * es);
-  L.off_ht = take((size_t)D * L.ldht * es);
-  L.off_p = take((size_t)M * L.ldp * es);
-  L.off_pt = take((size_t)L.vc * L.ldht * es);
-  L.off_part = take(part);
-  L.off_dh = take(V > L.vc ? (size_t)M * D * sizeof(float) : 0);
-  L.total = o;
-  return L;
-}
-
-// Forward: stats over the whole vocabulary, per-row lse and loss, the mean.
-// Writes loss, the state (lse, target columns, inv) and the bad-target count.
 template <typename TI>
 int ce_fwd_run(const TI *H, const TI *W, const int64_t *targets, int64_t M, int64_t D,
-               int64_t V, int64_t ignore_index, float *loss, int32_t *bad, char *state,
-               char *ws, hipStream_t s) {
+               int64_t V, int64_t ignore_index, int64_t chunk_rows, float *loss, int32_t *bad,
+               char *state, char *ws, hipStream_t s) {
   using C = MainCfg<TI>;
-  const StateLayout S = state_layout(M);
-  const FwdLayout L = fwd_layout(M, V, sizeof(TI));
-  float *lse = reinterpret_cast<float *>(state + S.off_lse);
-  int *tcol = reinterpret_cast<int *>(state + S.off_tcol);
-  float *inv = reinterpret_cast<float *>(state + S.off_scal);
-  float2 *stats = reinterpret_cast<float2 *>(ws + L.off_stats);
-  float *tgt = reinterpret_cast<float *>(ws + L.off_tgt);
-  float *loss_row = reinterpret_cast<float *>(ws + L.off_loss);
-  int *flags = reinterpret_cast<int *>(ws + L.off_flags);
+  using U = typename std::conditional<sizeof(TI) == 2, uint16_t, uint32_t>::type;
+  const Plan L = make_plan<TI>(M, D, V, chunk_rows);
+  const StateView<TI> S(L, state);
+  TI *Hc = reinterpret_cast<TI *>(ws + L.f_hc);
+  int *rows = reinterpret_cast<int *>(ws + L.f_rows);
+  int *tcol = reinterpret_cast<int *>(ws + L.f_tcol);
+  float2 *stats = reinterpret_cast<float2 *>(ws + L.f_stats);
+  float *tgt = reinterpret_cast<float *>(ws + L.f_tgt);
+  float *lse = reinterpret_cast<float *>(ws + L.f_lse);
+  float *loss_row = reinterpret_cast<float *>(ws + L.f_loss);
+  float *part = reinterpret_cast<float *>(ws + L.f_part);
   int e;
-  // blocks (vocabulary tile, token tile); the product is W H^T
-  const bool vk = buf_ok<TI>(H, D, M, D) && buf_ok<TI>(W, D, V, D);
-  const int mtiles = (int)((M + C::BN - 1) / C::BN);
-  const unsigned gs = (unsigned)(L.ntiles * mtiles);
-  if (vk)
-    ce_stats_kernel<C, true><<<gs, C::NT, 0, s>>>(W, H, V, M, D, targets, stats, tgt,
-                                                  (int)L.ntiles, mtiles);
-  else
-    ce_stats_kernel<C, false><<<gs, C::NT, 0, s>>>(W, H, V, M, D, targets, stats, tgt,
-                                                   (int)L.ntiles, mtiles);
-  if ((e = check_launch("ce_stats"))) return e;
-  ce_lse_kernel<<<(unsigned)((M + kLseRows - 1) / kLseRows), kLseRows * kLseParts, 0, s>>>(
-      stats, (int)L.ntiles, tgt, targets, M, V, ignore_index, lse, tcol, loss_row, flags);
-  if ((e = check_launch("ce_lse"))) return e;
-  ce_loss_kernel<<<1, kLossThreads, 0, s>>>(loss_row, flags, M, loss, inv, bad);
+
+  ce_compact_kernel<<<1, kCompactThreads, 0, s>>>(targets, M, V, ignore_index, rows, tcol,
+                                                  S.pos, S.n, S.inv, bad);
+  if ((e = check_launch("ce_compact"))) return e;
+  {
+    const bool vec = D % (16 / (int64_t)sizeof(TI)) == 0 && aligned16(H) && aligned16(Hc);
+    int64_t blocks = (M * D / (vec ? 16 / (int64_t)sizeof(TI) : 1) + 255) / 256;
+    if (blocks > 4096) blocks = 4096;
+    if (blocks < 1) blocks = 1;
+    if (vec)
+      ce_gather_kernel<TI, true><<<(unsigned)blocks, 256, 0, s>>>(H, D, rows, S.n, M, Hc);
+    else
+      ce_gather_kernel<TI, false><<<(unsigned)blocks, 256, 0, s>>>(H, D, rows, S.n, M, Hc);
+    if ((e = check_launch("ce_gather"))) return e;
+  }
+  if ((e = launch_transpose<U>(Hc, M, D, D, S.Hct, L.ldht, s))) return e;
+  if ((e = launch_transpose<U>(W, V, D, D, S.Wt, L.ldwt, s))) return e;
+
+  const bool vk = buf_ok<TI>(Hc, D, M, D) && buf_ok<TI>(W, D, V, D);
+  const bool sb = sb_ok(L.crows * L.ldp * (int64_t)sizeof(TI));
+  const unsigned glog = (unsigned)(L.vtiles * L.ttiles);
+  const dim3 gfix((unsigned)(L.crows / 64), (unsigned)((L.ldp + 63) / 64));
+  for (int64_t c = 0; c < L.nch; ++c) {
+    const int64_t j0 = c * L.crows;
+    if (vk && sb)
+      ce_logits_kernel<C, true, true><<<glog, C::NT, 0, s>>>(
+          W, Hc, V, D, j0, L.crows, S.n, tcol, stats, tgt, S.P, L.ldp, L.vtiles, L.ttiles);
+    else if (vk)
+      ce_logits_kernel<C, true, false><<<glog, C::NT, 0, s>>>(
+          W, Hc, V, D, j0, L.crows, S.n, tcol, stats, tgt, S.P, L.ldp, L.vtiles, L.ttiles);
+    else
+      ce_logits_kernel<C, false, false><<<glog, C::NT, 0, s>>>(
+          W, Hc, V, D, j0, L.crows, S.n, tcol, stats, tgt, S.P, L.ldp, L.vtiles, L.ttiles);
+    if ((e = check_launch("ce_logits"))) return e;
+    ce_lse_kernel<<<(unsigned)(L.crows / kLseRows), kLseRows * kLseParts, 0, s>>>(
+        stats, L.ntiles, L.crows, tgt, S.n, j0, lse, loss_row);
+    if ((e = check_launch("ce_lse"))) return e;
+    ce_fix_kernel<TI><<<gfix, 256, 0, s>>>(S.P, L.ldp, S.PT, L.crows, V, stats, L.wtm, lse,
+                                           tcol, S.n, j0, S.inv);
+    if ((e = check_launch("ce_fix"))) return e;
+    if (c + 1 < L.nch &&
+        (e = launch_grads<TI>(L, S, c, D, V, c > 0 ? S.dWacc : nullptr, S.dWacc, NF_DTYPE_F32,
+                              nullptr, part, s)))
+      return e;
+  }
+  ce_loss_kernel<<<1, kLossThreads, 0, s>>>(loss_row, S.n, S.inv, loss);
   return check_launch("ce_loss");
 }
 
-// Backward: per vocabulary chunk, P = inv * (softmax - onehot) from the
-// saved lse, then dW_c = g * P_c^T H and dH (+)= P_c W_c; the last chunk's dH
-// and every dW chunk are written scaled, in the caller's element types.
 template <typename TI>
-int ce_bwd_run(const TI *H, const TI *W, int64_t M, int64_t D, int64_t V, int64_t vocab_chunk,
-               const char *state, const float *g, void *dH, int dt_h, void *dW, int dt_w,
-               char *ws, hipStream_t s) {
-  using C = MainCfg<TI>;
-  const StateLayout S = state_layout(M);
-  const BwdLayout L = bwd_layout(M, D, V, vocab_chunk, sizeof(TI));
-  const float *lse = reinterpret_cast<const float *>(state + S.off_lse);
-  const int *tcol = reinterpret_cast<const int *>(state + S.off_tcol);
-  const float *inv = reinterpret_cast<const float *>(state + S.off_scal);
-  TI *Wt = reinterpret_cast<TI *>(ws + L.off_wt);
-  TI *Ht = reinterpret_cast<TI *>(ws + L.off_ht);
-  TI *P = reinterpret_cast<TI *>(ws + L.off_p);
-  TI *PT = reinterpret_cast<TI *>(ws + L.off_pt);
-  float *part = reinterpret_cast<float *>(ws + L.off_part);
-  float *dh_acc = reinterpret_cast<float *>(ws + L.off_dh);  // used when V > vc
+int ce_bwd_run(int64_t M, int64_t D, int64_t V, int64_t chunk_rows, char *state,
+               const float *g, void *dH, int dt_h, void *dW, int dt_w, char *ws, hipStream_t s) {
+  const Plan L = make_plan<TI>(M, D, V, chunk_rows);
+  const StateView<TI> S(L, state);
+  float *part = reinterpret_cast<float *>(ws + L.b_part);
   int e;
-
-  using U = typename std::conditional<sizeof(TI) == 2, uint16_t, uint32_t>::type;
-  if ((e = launch_transpose<U>(W, V, D, D, Wt, L.ldwt, s))) return e;
-  if ((e = launch_transpose<U>(H, M, D, D, Ht, L.ldht, s))) return e;
-
-  const bool vk = buf_ok<TI>(H, D, M, D) && buf_ok<TI>(W, D, V, D);
-  const int mtiles = (int)((M + C::BN - 1) / C::BN);
-  for (int64_t vb = 0; vb < V; vb += L.vc) {
-    const int64_t vc = (V - vb < L.vc) ? V - vb : L.vc;  // columns in this chunk
-    const int64_t kpad = round_up(vc, 8);
-    const TI *Wc = W + vb * D;
-    // blocks (chunk-column tile, token tile); the product is W_c H^T
-    const int vtiles = (int)((vc + C::BM - 1) / C::BM);
-    const unsigned gp = (unsigned)(vtiles * mtiles);
-    const bool sb = sb_ok(M * L.ldp * (int64_t)sizeof(TI)) &&
-                    sb_ok(vc * L.ldht * (int64_t)sizeof(TI));
-    const bool vb_ok = vk && buf_ok<TI>(Wc, D, vc, D);
-    if (vb_ok && sb)
-      ce_prob_kernel<C, true, true><<<gp, C::NT, 0, s>>>(Wc, H, vc, M, D, vb, tcol, lse, inv, P,
-                                                         L.ldp, kpad, PT, L.ldht, vtiles, mtiles);
-    else if (vb_ok)
-      ce_prob_kernel<C, true, false><<<gp, C::NT, 0, s>>>(Wc, H, vc, M, D, vb, tcol, lse, inv, P,
-                                                          L.ldp, kpad, PT, L.ldht, vtiles,
-                                                          mtiles);
-    else
-      ce_prob_kernel<C, false, false><<<gp, C::NT, 0, s>>>(Wc, H, vc, M, D, vb, tcol, lse, inv,
-                                                           P, L.ldp, kpad, PT, L.ldht, vtiles,
-                                                           mtiles);
-    if ((e = check_launch("ce_prob"))) return e;
-    // dW[vb:vb+vc, :] = g * P_c^T H   (K = tokens, zero-padded to ldht), final;
-    // dH (+)= P_c W_c                 (K = chunk columns, zero-padded to kpad)
-    // into the fp32 accumulator, the last chunk scaled into dH itself
-    const bool first = vb == 0, last = vb + L.vc >= V;
-    char *dw_c = static_cast<char *>(dW) + vb * D * dtype_bytes(dt_w);
-    auto jw = make_job<C>(PT, L.ldht, Ht, L.ldht, nullptr, dw_c, dt_w, g, D, vc, D, L.ldht);
-    auto jh = make_job<C>(P, L.ldp, Wt + vb, L.ldwt, first ? nullptr : dh_acc,
-                          last ? dH : static_cast<void *>(dh_acc),
-                          last ? dt_h : NF_DTYPE_F32, last ? g : nullptr, D, M, D, kpad);
-    const SplitPlan sp = chunk_split<C>(vc, M, D);
-    for (auto *jp : {&jw, &jh}) {
-      const Split &q = jp == &jw ? sp.w : sp.h;
-      if (q.S > 1) {
-        jp->ksplit = q.S;
-        jp->kslice = q.kslice;
-        jp->part = part;
-        jp->tiles *= q.S;
-      }
-    }
-    // a split job's slices are the longest blocks: dispatch them first
-    if ((e = sp.h.S > 1 ? launch_gemm_store<C>(jh, jw, s) : launch_gemm_store<C>(jw, jh, s)))
-      return e;
-  }
-  return NF_OK;
+  if ((e = launch_grads<TI>(L, S, L.nch - 1, D, V, L.nch > 1 ? S.dWacc : nullptr, dW, dt_w, g,
+                            part, s)))
+    return e;
+  const bool vec = D % 4 == 0;  // dHc rows are then 16-byte aligned
+  int64_t blocks = (M * (vec ? D / 4 : D) + 255) / 256;
+  if (blocks > 4096) blocks = 4096;
+  if (vec)
+    ce_scatter_dh_kernel<4><<<(unsigned)blocks, 256, 0, s>>>(S.dHc, D, S.pos, M, g, dH, dt_h);
+  else
+    ce_scatter_dh_kernel<1><<<(unsigned)blocks, 256, 0, s>>>(S.dHc, D, S.pos, M, g, dH, dt_h);
+  return check_launch("ce_scatter_dh");
 }
 
 }  // namespace ce
@@ -636,7 +739,7 @@ namespace {
 bool ce_sizes_ok(int64_t M, int64_t D, int64_t V) {
   const int64_t i32 = 0x7fffffffLL, cap = (int64_t)1 << 40;
   return M > 0 && D > 0 && V > 0 && M <= i32 && V <= i32 && D <= i32 && M * D <= cap &&
-         V * D <= cap;
+         V * D <= cap && M * V <= cap;
 }
 int ce_check_shape(const char *fn, int64_t M, int64_t D, int64_t V) {
   if (M <= 0 || D <= 0 || V <= 0)
@@ -652,110 +755,116 @@ int ce_check_dtype(const char *fn, int dtype) {
     return set_error(NF_ERR_DTYPE, "%s: dtype %d unsupported (bf16 or f32)", fn, dtype);
   return NF_OK;
 }
-size_t es_of(int dtype) { return dtype == NF_DTYPE_BF16 ? 2 : 4; }
+bool dtype_ok(int dtype) { return dtype == NF_DTYPE_BF16 || dtype == NF_DTYPE_F32; }
+Plan plan_of(int64_t M, int64_t D, int64_t V, int64_t chunk_rows, int dtype) {
+  return dtype == NF_DTYPE_BF16 ? make_plan<bf16>(M, D, V, chunk_rows)
+                                : make_plan<float>(M, D, V, chunk_rows);
+}
 }  // namespace
 
-extern "C" size_t nf_ce_state_bytes(int64_t M) {
-  return M > 0 && M <= 0x7fffffffLL ? state_layout(M).total : 0;
+extern "C" size_t nf_ce_state_bytes(int64_t M, int64_t D, int64_t V, int64_t chunk_rows,
+                                    int dtype) {
+  if (!ce_sizes_ok(M, D, V) || chunk_rows <= 0 || !dtype_ok(dtype)) return 0;
+  return plan_of(M, D, V, chunk_rows, dtype).s_total;
 }
 
-extern "C" size_t nf_ce_fwd_workspace(int64_t M, int64_t D, int64_t V, int dtype) {
-  if (!ce_sizes_ok(M, D, V)) return 0;
-  if (dtype != NF_DTYPE_BF16 && dtype != NF_DTYPE_F32) return 0;
-  return fwd_layout(M, V, (int)es_of(dtype)).total;
-}
-
-extern "C" size_t nf_ce_bwd_workspace(int64_t M, int64_t D, int64_t V, int64_t vocab_chunk,
+extern "C" size_t nf_ce_fwd_workspace(int64_t M, int64_t D, int64_t V, int64_t chunk_rows,
                                       int dtype) {
-  if (!ce_sizes_ok(M, D, V) || vocab_chunk <= 0) return 0;
-  if (dtype != NF_DTYPE_BF16 && dtype != NF_DTYPE_F32) return 0;
-  return bwd_layout(M, D, V, vocab_chunk, (int)es_of(dtype)).total;
+  if (!ce_sizes_ok(M, D, V) || chunk_rows <= 0 || !dtype_ok(dtype)) return 0;
+  return plan_of(M, D, V, chunk_rows, dtype).f_total;
+}
+
+extern "C" size_t nf_ce_bwd_workspace(int64_t M, int64_t D, int64_t V, int64_t chunk_rows,
+                                      int dtype) {
+  if (!ce_sizes_ok(M, D, V) || chunk_rows <= 0 || !dtype_ok(dtype)) return 0;
+  const size_t b = plan_of(M, D, V, chunk_rows, dtype).b_total;
+  return b > 0 ? b : 256;  // never 0 for a valid shape (0 marks a refusal)
 }
 
 extern "C" int nf_ce_fwd(const void *hidden, const void *weight, const int64_t *targets,
-                         int64_t M, int64_t D, int64_t V, int64_t ignore_index, int dtype,
-                         float *loss, int32_t *bad_targets, void *state, size_t state_bytes,
-                         void *workspace, size_t workspace_bytes, void *stream) {
+                         int64_t M, int64_t D, int64_t V, int64_t ignore_index,
+                         int64_t chunk_rows, int dtype, float *loss, int32_t *bad_targets,
+                         void *state, size_t state_bytes, void *workspace,
+                         size_t workspace_bytes, void *stream) {
   if (int e = ce_check_shape("nf_ce_fwd", M, D, V)) return e;
+  if (chunk_rows <= 0) return set_error(NF_ERR_ARG, "nf_ce_fwd: chunk_rows must be > 0");
   if (!hidden || !weight || !targets || !loss || !state)
     return set_error(NF_ERR_ARG, "nf_ce_fwd: null pointer");
   if (int e = ce_check_dtype("nf_ce_fwd", dtype)) return e;
-  const size_t need_s = nf_ce_state_bytes(M), need = nf_ce_fwd_workspace(M, D, V, dtype);
-  if (state_bytes < need_s || !aligned16(state))
+  const Plan L = plan_of(M, D, V, chunk_rows, dtype);
+  if (state_bytes < L.s_total || !aligned16(state))
     return set_error(NF_ERR_WORKSPACE, "nf_ce_fwd: state %zu bytes < required %zu",
-                     state_bytes, need_s);
-  if (!workspace || workspace_bytes < need || !aligned16(workspace))
+                     state_bytes, L.s_total);
+  if (!workspace || workspace_bytes < L.f_total || !aligned16(workspace))
     return set_error(NF_ERR_WORKSPACE, "nf_ce_fwd: workspace %zu bytes < required %zu",
-                     workspace_bytes, need);
+                     workspace_bytes, L.f_total);
   hipStream_t s = static_cast<hipStream_t>(stream);
   char *st = static_cast<char *>(state), *ws = static_cast<char *>(workspace);
   if (dtype == NF_DTYPE_BF16)
     return ce_fwd_run<bf16>((const bf16 *)hidden, (const bf16 *)weight, targets, M, D, V,
-                            ignore_index, loss, bad_targets, st, ws, s);
+                            ignore_index, chunk_rows, loss, bad_targets, st, ws, s);
   return ce_fwd_run<float>((const float *)hidden, (const float *)weight, targets, M, D, V,
-                           ignore_index, loss, bad_targets, st, ws, s);
+                           ignore_index, chunk_rows, loss, bad_targets, st, ws, s);
 }
 
-extern "C" int nf_ce_bwd(const void *hidden, const void *weight, int64_t M, int64_t D,
-                         int64_t V, int64_t vocab_chunk, int dtype, const void *state,
-                         size_t state_bytes, const float *grad_output, void *dhidden,
-                         int dt_hidden, void *dweight, int dt_weight, void *workspace,
-                         size_t workspace_bytes, void *stream) {
+extern "C" int nf_ce_bwd(int64_t M, int64_t D, int64_t V, int64_t chunk_rows, int dtype,
+                         void *state, size_t state_bytes, const float *grad_output,
+                         void *dhidden, int dt_hidden, void *dweight, int dt_weight,
+                         void *workspace, size_t workspace_bytes, void *stream) {
   if (int e = ce_check_shape("nf_ce_bwd", M, D, V)) return e;
-  if (vocab_chunk <= 0) return set_error(NF_ERR_ARG, "nf_ce_bwd: vocab_chunk must be > 0");
-  if (!hidden || !weight || !state || !dhidden || !dweight)
-    return set_error(NF_ERR_ARG, "nf_ce_bwd: null pointer");
+  if (chunk_rows <= 0) return set_error(NF_ERR_ARG, "nf_ce_bwd: chunk_rows must be > 0");
+  if (!state || !dhidden || !dweight) return set_error(NF_ERR_ARG, "nf_ce_bwd: null pointer");
   if (int e = ce_check_dtype("nf_ce_bwd", dtype)) return e;
   if (!is_dtype(dt_hidden) || !is_dtype(dt_weight))
     return set_error(NF_ERR_DTYPE, "nf_ce_bwd: gradient dtypes %d, %d", dt_hidden, dt_weight);
-  const size_t need_s = nf_ce_state_bytes(M), need = nf_ce_bwd_workspace(M, D, V, vocab_chunk,
-                                                                         dtype);
-  if (state_bytes < need_s || !aligned16(state))
+  const Plan L = plan_of(M, D, V, chunk_rows, dtype);
+  if (state_bytes < L.s_total || !aligned16(state))
     return set_error(NF_ERR_WORKSPACE, "nf_ce_bwd: state %zu bytes < required %zu",
-                     state_bytes, need_s);
+                     state_bytes, L.s_total);
+  const size_t need = nf_ce_bwd_workspace(M, D, V, chunk_rows, dtype);
   if (!workspace || workspace_bytes < need || !aligned16(workspace))
     return set_error(NF_ERR_WORKSPACE, "nf_ce_bwd: workspace %zu bytes < required %zu",
                      workspace_bytes, need);
   hipStream_t s = static_cast<hipStream_t>(stream);
-  const char *st = static_cast<const char *>(state);
-  char *ws = static_cast<char *>(workspace);
+  char *st = static_cast<char *>(state), *ws = static_cast<char *>(workspace);
   if (dtype == NF_DTYPE_BF16)
-    return ce_bwd_run<bf16>((const bf16 *)hidden, (const bf16 *)weight, M, D, V, vocab_chunk, st,
-                            grad_output, dhidden, dt_hidden, dweight, dt_weight, ws, s);
-  return ce_bwd_run<float>((const float *)hidden, (const float *)weight, M, D, V, vocab_chunk,
-                           st, grad_output, dhidden, dt_hidden, dweight, dt_weight, ws, s);
+    return ce_bwd_run<bf16>(M, D, V, chunk_rows, st, grad_output, dhidden, dt_hidden, dweight,
+                            dt_weight, ws, s);
+  return ce_bwd_run<float>(M, D, V, chunk_rows, st, grad_output, dhidden, dt_hidden, dweight,
+                           dt_weight, ws, s);
 }
 
 // one call: [state | forward and backward scratch, overlapped]
-extern "C" size_t nf_ce_workspace(int64_t M, int64_t D, int64_t V, int64_t vocab_chunk,
+extern "C" size_t nf_ce_workspace(int64_t M, int64_t D, int64_t V, int64_t chunk_rows,
                                   int dtype) {
-  const size_t f = nf_ce_fwd_workspace(M, D, V, dtype);
-  const size_t b = nf_ce_bwd_workspace(M, D, V, vocab_chunk, dtype);
-  if (!f || !b) return 0;
-  return nf_ce_state_bytes(M) + (f > b ? f : b);
+  const size_t st = nf_ce_state_bytes(M, D, V, chunk_rows, dtype);
+  const size_t f = nf_ce_fwd_workspace(M, D, V, chunk_rows, dtype);
+  const size_t b = nf_ce_bwd_workspace(M, D, V, chunk_rows, dtype);
+  if (!st || !f || !b) return 0;
+  return st + (f > b ? f : b);
 }
 
 extern "C" int nf_ce_fwd_bwd(const void *hidden, const void *weight, const int64_t *targets,
                              int64_t M, int64_t D, int64_t V, int64_t ignore_index,
-                             int64_t vocab_chunk, int dtype, float *loss, float *dhidden,
+                             int64_t chunk_rows, int dtype, float *loss, float *dhidden,
                              float *dweight, int32_t *bad_targets, void *workspace,
                              size_t workspace_bytes, void *stream) {
   if (int e = ce_check_shape("nf_ce_fwd_bwd", M, D, V)) return e;
-  if (vocab_chunk <= 0) return set_error(NF_ERR_ARG, "nf_ce_fwd_bwd: vocab_chunk must be > 0");
+  if (chunk_rows <= 0) return set_error(NF_ERR_ARG, "nf_ce_fwd_bwd: chunk_rows must be > 0");
   if (!hidden || !weight || !targets || !loss || !dhidden || !dweight)
     return set_error(NF_ERR_ARG, "nf_ce_fwd_bwd: null pointer");
   if (int e = ce_check_dtype("nf_ce_fwd_bwd", dtype)) return e;
-  const size_t need = nf_ce_workspace(M, D, V, vocab_chunk, dtype);
+  const size_t need = nf_ce_workspace(M, D, V, chunk_rows, dtype);
   if (!workspace || workspace_bytes < need || !aligned16(workspace))
     return set_error(NF_ERR_WORKSPACE, "nf_ce_fwd_bwd: workspace %zu bytes < required %zu",
                      workspace_bytes, need);
-  const size_t sb = nf_ce_state_bytes(M);
+  const size_t sb = nf_ce_state_bytes(M, D, V, chunk_rows, dtype);
   char *ws = static_cast<char *>(workspace);
-  if (int e = nf_ce_fwd(hidden, weight, targets, M, D, V, ignore_index, dtype, loss,
+  if (int e = nf_ce_fwd(hidden, weight, targets, M, D, V, ignore_index, chunk_rows, dtype, loss,
                         bad_targets, ws, sb, ws + sb, workspace_bytes - sb, stream))
     return e;
-  return nf_ce_bwd(hidden, weight, M, D, V, vocab_chunk, dtype, ws, sb, nullptr, dhidden,
-                   NF_DTYPE_F32, dweight, NF_DTYPE_F32, ws + sb, workspace_bytes - sb, stream);
+  return nf_ce_bwd(M, D, V, chunk_rows, dtype, ws, sb, nullptr, dhidden, NF_DTYPE_F32, dweight,
+                   NF_DTYPE_F32, ws + sb, workspace_bytes - sb, stream);
 }
 
 extern "C" int nf_gemm_nt(const void *A, int64_t lda, const void *B, int64_t ldb, float *C,

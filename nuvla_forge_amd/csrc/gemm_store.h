@@ -86,6 +86,12 @@ inline bool sb_ok(int64_t bytes) { return bytes < ((int64_t)1 << 31) - 64; }
 // stage width): block (tile, s) writes the partial product over slice s to
 // part[s] ([M, N], dense, fp32) and splitk_reduce_kernel adds the slices in
 // order, then Cin, scales and converts.
+//
+// A job with `dyn` set takes one extent from device memory, so a caller can
+// size work by a count it never reads back: e = clamp(*dyn - dyn_base, 0, X)
+// replaces M (dyn_rows: blocks past the e rows exit, rows past e are not
+// written) or K (rounded up to 8; the operands must hold zeros between e and
+// that).  The static M, N, K still give the grid and the buffer extents.
 template <typename TI>
 struct GemmJob {
   const TI *A;
@@ -100,7 +106,28 @@ struct GemmJob {
   int ksplit;    // K slices (1: no split)
   int64_t kslice;
   float *part;   // [ksplit, M, N] partial products when ksplit > 1
+  const int *dyn;    // device count giving the dynamic extent, or null
+  int64_t dyn_base;  // the extent is *dyn - dyn_base, clamped to [0, M or K]
+  int dyn_rows;      // 1: the dynamic extent is M; 0: it is K
 };
+
+// The job's (M, K) after its dynamic extent, if any.
+template <typename TI>
+__device__ __forceinline__ void job_extents(const GemmJob<TI> &j, int64_t &M, int64_t &K) {
+  M = j.M;
+  K = j.K;
+  if (j.dyn) {
+    int64_t e = (int64_t)__builtin_amdgcn_readfirstlane(*j.dyn) - j.dyn_base;
+    const int64_t cap = j.dyn_rows ? j.M : j.K;
+    e = e < 0 ? 0 : (e > cap ? cap : e);
+    if (j.dyn_rows) {
+      M = e;
+    } else {
+      e = (e + 7) / 8 * 8;
+      K = e < j.K ? e : j.K;
+    }
+  }
+}
 
 __host__ __device__ inline int dtype_bytes(int dt) { return dt == NF_DTYPE_F32 ? 4 : 2; }
 
@@ -130,18 +157,22 @@ __global__ NF_GEMM_BOUNDS(C) void gemm_store_kernel(GemmJob<typename C::TI> j0,
   gemm::group_tile(t % per_split, j.tiles_m, per_split / j.tiles_m, gemm::kTileGroup, tm, tn);
   const int64_t m0 = (int64_t)tm * C::BM;
   const int64_t n0 = (int64_t)tn * C::BN;
-  const int64_t M = j.M, N = j.N;
+  int64_t M, K;
+  job_extents(j, M, K);
+  if (m0 >= M) return;  // a dynamic row count left this tile without rows
+  const int64_t N = j.N;
   const bool split = j.ksplit > 1;
   const int64_t k0 = ks * j.kslice;
-  const int64_t klen = j.K - k0 < j.kslice ? j.K - k0 : j.kslice;
+  int64_t klen = K - k0 < j.kslice ? K - k0 : j.kslice;
+  if (klen < 0) klen = 0;
   // a split block writes its fp32 partial densely; the reduce does the rest
   const int64_t ldc = split ? N : j.ldc;
   const int cdt = split ? NF_DTYPE_F32 : j.cdt;
   const bool preload = !split && j.Cin != nullptr;
   OutBuf<SB> out, cin;
-  out.init(split ? static_cast<void *>(j.part + ks * M * N) : j.C,
-           M * ldc * (int64_t)dtype_bytes(cdt));
-  cin.init(const_cast<float *>(j.Cin), M * ldc * (int64_t)sizeof(float));
+  out.init(split ? static_cast<void *>(j.part + ks * j.M * N) : j.C,
+           j.M * ldc * (int64_t)dtype_bytes(cdt));
+  cin.init(const_cast<float *>(j.Cin), j.M * ldc * (int64_t)sizeof(float));
   const int w = threadIdx.x >> 6, wm = w / C::WN, wn = w % C::WN;
   // element (i, jj, r) of this lane sits at byte offset base + i * 32 rows
   // + 8 * (r / 4) + (r % 4) rows + jj * 32 columns
@@ -187,15 +218,23 @@ __global__ NF_GEMM_BOUNDS(C) void gemm_store_kernel(GemmJob<typename C::TI> j0,
 }
 
 // C[m, n] = scale * (Cin[m, n] + sum over s = 0 .. S-1 of part[s, m, n]),
-// the slices added in order; C of element type cdt.
+// the slices added in order; C of element type cdt.  With `dyn`, only the
+// first clamp(*dyn - dyn_base, 0, M) rows (the slices keep their M x N size).
 static __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float *__restrict__ part,
                                                             int S, int64_t M, int64_t N,
                                                             const float *Cin, void *C,
                                                             int64_t ldc, int cdt,
-                                                            const float *scale) {
-  const int64_t total = M * N;
+                                                            const float *scale, const int *dyn,
+                                                            int64_t dyn_base) {
+  const int64_t total = M * N;  // slice stride
+  int64_t rows = M;
+  if (dyn) {
+    rows = (int64_t)*dyn - dyn_base;
+    rows = rows < 0 ? 0 : (rows > M ? M : rows);
+  }
+  const int64_t live = rows * N;
   const float g = scale ? *scale : 1.f;
-  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < live;
        i += (int64_t)gridDim.x * 256) {
     // slices added in order 0 .. S-1; 8 loads in flight per batch
     constexpr int kBatch = 8;
@@ -313,6 +352,9 @@ GemmJob<typename C::TI> make_job(const typename C::TI *A, int64_t lda, const typ
   j.ksplit = 1;
   j.kslice = K;
   j.part = nullptr;
+  j.dyn = nullptr;
+  j.dyn_base = 0;
+  j.dyn_rows = 0;
   return j;
 }
 
@@ -351,9 +393,9 @@ int launch_gemm_store(const GemmJob<typename C::TI> &j0, const GemmJob<typename 
     if (jp->tiles == 0 || jp->ksplit <= 1) continue;
     int64_t blocks = (jp->M * jp->N + 255) / 256;
     if (blocks > 2048) blocks = 2048;
-    splitk_reduce_kernel<<<(unsigned)blocks, 256, 0, s>>>(jp->part, jp->ksplit, jp->M, jp->N,
-                                                         jp->Cin, jp->C, jp->ldc, jp->cdt,
-                                                         jp->scale);
+    splitk_reduce_kernel<<<(unsigned)blocks, 256, 0, s>>>(
+        jp->part, jp->ksplit, jp->M, jp->N, jp->Cin, jp->C, jp->ldc, jp->cdt, jp->scale,
+        jp->dyn_rows ? jp->dyn : nullptr, jp->dyn_base);
     if (int e = check_launch("splitk_reduce")) return e;
   }
   return NF_OK;

@@ -7,29 +7,31 @@ returns 6 values, chunked_ce.py:120-182) and the same public
 ``chunked_cross_entropy(hidden, lm_weight, targets, chunk_size=1024,
 ignore_index=-100, force_reference=False)`` (chunked_ce.py:185-208).
 
-The device path is two calls.  ``nf_ce_fwd`` produces logits tiles on bf16
-(or fp32) MFMA and reduces them to per-row log-sum-exp without storing them;
-the loss and a per-row state (lse, target column, 1/n) come out.
-``nf_ce_bwd`` recomputes the logits one vocabulary chunk at a time to form
-``(softmax - onehot) / n`` and both gradient GEMMs, and writes the gradients
-already multiplied by ``grad_output`` in each input's dtype.  The reference
-forms fp32 gradients in the forward pass, keeps them (dW alone is [V, D]
-fp32) until the backward and then scales and casts them; here nothing
-between the two passes is larger than the state, and the results are the
-same.  The valid-token count stays on the device, so a device call makes no
-host synchronisation at all (the reference's ``.item()`` at chunked_ce.py:126
-is gone): targets outside ``[0, V)`` that are not ``ignore_index`` are
-counted on the device and treated as ignored.  Setting ``VALIDATE_TARGETS =
-True`` opts into raising ``ValueError`` for them instead, at the price of one
+The device path is two calls.  ``nf_ce_fwd`` compacts the valid rows on the
+device and, ``chunk_size`` of them at a time, forms their logits once on
+bf16 (or fp32) MFMA, turns them into ``(softmax - onehot) / n`` in place
+(fp32 log-sum-exp from per-tile statistics), and runs the gradient products
+of every chunk but the last; the loss comes out.  ``nf_ce_bwd`` runs the last
+chunk's products with ``grad_output`` known and writes both gradients scaled,
+in each input's dtype.  The reference forms fp32 gradients in the forward
+pass and scales and casts them in the backward; the results are the same.
+The valid-token count stays on the device, so a device call makes no host
+synchronisation at all (the reference's ``.item()`` at chunked_ce.py:126 is
+gone): targets outside ``[0, V)`` that are not ``ignore_index`` are counted
+on the device and treated as ignored.  Setting ``VALIDATE_TARGETS = True``
+opts into raising ``ValueError`` for them instead, at the price of one
 device-to-host read per call (skipped while a graph is being captured).
 
 Host tensors (and ``force_reference=True``) run the reference's own row-chunk
 loop in ATen (chunked_ce.py:133-167 with ``_ce_chunk_torch``, :101-117).
 
-``chunk_size`` keeps its meaning as the memory budget: the reference holds a
-[chunk_size, V] fp32 logits tile; this path holds an [M, vc] probability tile
-with vc = chunk_size * V / M rounded up to the 128-column MFMA tile (at most
-V).  Results do not depend on it beyond fp rounding.
+``chunk_size`` keeps the reference's meaning, rows per chunk (rounded up to
+the 256-row MFMA tile here, and counting only valid rows): a chunk's
+probabilities are held in the input type in both layouts the two gradient
+products read, 4 * chunk_size * V bytes in bf16 -- the reference's
+[chunk_size, V] fp32 logits tile.  Bigger chunks are faster (fewer passes
+over the fp32 dW accumulator); results do not depend on it beyond fp
+rounding.
 
 Element types: under bf16 autocast for the device the products run in bf16
 (MFMA, fp32 accumulation) whatever the input types, as the reference's
@@ -51,13 +53,11 @@ from .utils import device_of, use_fused
 VALIDATE_TARGETS = False
 
 
-def vocab_chunk_for(chunk_size: int, m: int, v: int) -> int:
-    """Vocabulary columns per chunk holding the reference's [chunk_size, V] budget."""
-    if chunk_size <= 0:
+def chunk_rows_for(chunk_size: int) -> int:
+    """Rows per chunk the device path is asked for (the library rounds up to 256)."""
+    if int(chunk_size) <= 0:
         raise ValueError(f"chunk_size must be positive, got {chunk_size}")
-    vc = -(-int(chunk_size) * v // max(m, 1))
-    vc = -(-vc // 128) * 128
-    return max(128, min(vc, -(-v // 8) * 8))
+    return int(chunk_size)
 
 
 def _compute_dtype(hidden: torch.Tensor, lm_weight: torch.Tensor) -> torch.dtype:
@@ -111,31 +111,45 @@ def _forward_eager(hidden, lm_weight, targets, chunk_size, ignore_index):
     return loss_total, d_hidden, d_weight
 
 
-def _forward_hip(hidden, lm_weight, targets, ignore_index):
-    """Loss and the state for ``_backward_hip``: (loss, h, w, state)."""
+class _DeviceCall:
+    """What the two device calls share: the shape, the compute type and the
+    state nf_ce_fwd leaves for nf_ce_bwd."""
+
+    def __init__(self, m, d, v, chunk_rows, cdt):
+        self.m, self.d, self.v, self.chunk_rows, self.cdt = m, d, v, chunk_rows, cdt
+        self.code = _lib.dtype_code(cdt)
+        self.state = None
+
+
+def _forward_hip(hidden, lm_weight, targets, chunk_size, ignore_index):
+    """Loss and the call record for ``_backward_hip``."""
     m, d = hidden.shape
     v = lm_weight.shape[0]
     cdt = _compute_dtype(hidden, lm_weight)
-    h = hidden.to(cdt).contiguous()
-    w = lm_weight.to(cdt).contiguous()
+    call = _DeviceCall(m, d, v, chunk_rows_for(chunk_size), cdt)
     dev = hidden.device
     loss = torch.empty((), dtype=torch.float32, device=dev)
     if m == 0:
-        return loss.zero_(), h, w, None
+        return loss.zero_(), call
+    h = hidden.to(cdt).contiguous()
+    w = lm_weight.to(cdt).contiguous()
     tg = targets.to(torch.int64).contiguous()
     validate = VALIDATE_TARGETS and not torch.cuda.is_current_stream_capturing()
     bad = torch.empty(1, dtype=torch.int32, device=dev) if validate else None
     L = _lib.lib()
-    code = _lib.dtype_code(cdt)
-    st_bytes = L.nf_ce_state_bytes(m)
-    state = torch.empty(st_bytes, dtype=torch.uint8, device=dev)
-    ws_bytes = L.nf_ce_fwd_workspace(m, d, v, code)
+    shape = (m, d, v, call.chunk_rows, call.code)
+    st_bytes = L.nf_ce_state_bytes(*shape)
+    ws_bytes = L.nf_ce_fwd_workspace(*shape)
+    if not st_bytes or not ws_bytes:
+        raise ValueError(f"chunked_cross_entropy: shape M={m} D={d} V={v} is beyond the kernels")
+    call.state = torch.empty(st_bytes, dtype=torch.uint8, device=dev)
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
     with device_of(hidden):
         _lib.check(
             L.nf_ce_fwd(h.data_ptr(), w.data_ptr(), tg.data_ptr(), m, d, v, int(ignore_index),
-                        code, loss.data_ptr(), _lib.ptr(bad), state.data_ptr(), st_bytes,
-                        ws.data_ptr(), ws_bytes, _lib.stream_of(hidden)),
+                        call.chunk_rows, call.code, loss.data_ptr(), _lib.ptr(bad),
+                        call.state.data_ptr(), st_bytes, ws.data_ptr(), ws_bytes,
+                        _lib.stream_of(hidden)),
             "nf_ce_fwd",
         )
     if validate:
@@ -143,30 +157,26 @@ def _forward_hip(hidden, lm_weight, targets, ignore_index):
         if nbad:
             raise ValueError(f"chunked_cross_entropy: {nbad} target(s) outside [0, {v}) "
                              f"and not ignore_index={ignore_index}")
-    return loss, h, w, state
+    return loss, call
 
 
-def _backward_hip(h, w, state, chunk_size, grad_output, hidden_dtype, weight_dtype):
+def _backward_hip(call, grad_output, hidden_dtype, weight_dtype, dev):
     """(grad_output * dL/dhidden, grad_output * dL/dweight) in the inputs' dtypes."""
-    m, d = h.shape
-    v = w.shape[0]
-    dev = h.device
+    m, d, v = call.m, call.d, call.v
     dh = torch.empty((m, d), dtype=hidden_dtype, device=dev)
     dw = torch.empty((v, d), dtype=weight_dtype, device=dev)
     if m == 0:
         return dh, dw.zero_()
     g = grad_output.to(torch.float32).contiguous()
-    vc = vocab_chunk_for(chunk_size, m, v)
     L = _lib.lib()
-    code = _lib.dtype_code(h.dtype)
-    ws_bytes = L.nf_ce_bwd_workspace(m, d, v, vc, code)
+    ws_bytes = L.nf_ce_bwd_workspace(m, d, v, call.chunk_rows, call.code)
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
-    with device_of(h):
+    with device_of(dh):
         _lib.check(
-            L.nf_ce_bwd(h.data_ptr(), w.data_ptr(), m, d, v, vc, code, state.data_ptr(),
-                        state.numel(), g.data_ptr(), dh.data_ptr(), _lib.dtype_code(dh),
+            L.nf_ce_bwd(m, d, v, call.chunk_rows, call.code, call.state.data_ptr(),
+                        call.state.numel(), g.data_ptr(), dh.data_ptr(), _lib.dtype_code(dh),
                         dw.data_ptr(), _lib.dtype_code(dw), ws.data_ptr(), ws_bytes,
-                        _lib.stream_of(h)),
+                        _lib.stream_of(dh)),
             "nf_ce_bwd",
         )
     return dh, dw
@@ -190,10 +200,8 @@ class _ChunkedCrossEntropy(torch.autograd.Function):
                                                       ignore_index)
             ctx.save_for_backward(d_hidden, d_weight)
             return loss
-        vocab_chunk_for(chunk_size, hidden.shape[0], lm_weight.shape[0])  # validates chunk_size
-        loss, h, w, state = _forward_hip(hidden, lm_weight, targets, ignore_index)
-        ctx.save_for_backward(h, w, state)
-        ctx.chunk_size = chunk_size
+        loss, ctx.call = _forward_hip(hidden, lm_weight, targets, chunk_size, ignore_index)
+        ctx.device = hidden.device
         return loss
 
     @staticmethod
@@ -203,9 +211,8 @@ class _ChunkedCrossEntropy(torch.autograd.Function):
             g = grad_output
             return ((d_hidden * g).to(ctx.hidden_dtype), (d_weight * g).to(ctx.weight_dtype),
                     None, None, None, None)
-        h, w, state = ctx.saved_tensors
-        dh, dw = _backward_hip(h, w, state, ctx.chunk_size, grad_output, ctx.hidden_dtype,
-                               ctx.weight_dtype)
+        dh, dw = _backward_hip(ctx.call, grad_output, ctx.hidden_dtype, ctx.weight_dtype,
+                               ctx.device)
         return dh, dw, None, None, None, None
 
 

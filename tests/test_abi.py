@@ -71,7 +71,7 @@ def test_header_is_c_and_the_c_program_links_the_library():
 
 
 def test_abi_version():
-    assert _lib.lib().nf_abi_version() == _lib.ABI_VERSION == 2
+    assert _lib.lib().nf_abi_version() == _lib.ABI_VERSION == 3
     assert K.HAS_HIP and K.HAS_TRITON
 
 
@@ -183,49 +183,87 @@ def test_adaln_argument_validation():
                                  64, 1024, 8, 1, 1, 1, 1, None) == NF_OK  # nothing requested
 
 
+def _ceil(a: int, b: int) -> int:
+    return -(-a // b)
+
+
+def _ce_state_closed_form(m, d, v, chunk_rows, es=2):
+    """The state nf_ce_fwd leaves for nf_ce_bwd, term by term (each buffer
+    256-byte aligned): scalars, pos [M], W^T [D, V8], Hc^T [D, M8], one chunk's
+    P [C, V8] and PT [V, C], fp32 dH rows [M, D], and the fp32 dW accumulator
+    when more than one chunk (C = chunk_rows rounded up to 256, at most M
+    rounded up to 256)."""
+    a = lambda x: _ceil(x, 256) * 256  # noqa: E731
+    c = min(_ceil(chunk_rows, 256) * 256, _ceil(m, 256) * 256)
+    v8, m8 = _ceil(v, 8) * 8, _ceil(m, 8) * 8
+    nch = _ceil(m, c)
+    return (a(64) + a(4 * m) + a(es * d * v8) + a(es * d * m8) + a(es * c * v8) + a(es * v * c)
+            + a(4 * m * d) + (a(4 * v * d) if nch > 1 else 0))
+
+
+def sb_at(L, chunk_rows):
+    return L.nf_ce_state_bytes(4096, 2048, 32000, chunk_rows, 1)
+
+
+def test_ce_state_and_workspace_sizes():
+    L = _lib.lib()
+    for m, d, v, cr in [(4096, 2048, 32000, 1024), (4096, 2048, 32000, 4096),
+                        (512, 384, 32000, 1024), (300, 72, 1030, 100), (17, 36, 333, 7)]:
+        assert L.nf_ce_state_bytes(m, d, v, cr, 1) == _ce_state_closed_form(m, d, v, cr), (m, cr)
+        assert L.nf_ce_state_bytes(m, d, v, cr, 0) == _ce_state_closed_form(m, d, v, cr, es=4)
+    # a chunk's P and PT (bf16) are the reference's [chunk_size, V] fp32 logits
+    # tile: each 1024 more rows per chunk hold 4 * 1024 * 32000 more bytes
+    more = L.nf_ce_state_bytes(4096, 2048, 32000, 2048, 1) - sb_at(L, 1024)
+    assert more == 4 * 1024 * 32000
+    assert L.nf_ce_state_bytes(4096, 2048, 32000, 1024, 2) == 0  # fp16 unsupported
+    assert L.nf_ce_state_bytes(0, 2048, 32000, 1024, 1) == 0
+    assert L.nf_ce_state_bytes(4096, 2048, 32000, 0, 1) == 0
+    sb = L.nf_ce_state_bytes(4096, 2048, 32000, 1024, 1)
+    fws = L.nf_ce_fwd_workspace(4096, 2048, 32000, 1024, 1)
+    bws = L.nf_ce_bwd_workspace(4096, 2048, 32000, 1024, 1)
+    assert fws > 4096 * 2048 * 2 and bws > 0  # the forward holds the gathered rows
+    assert L.nf_ce_workspace(4096, 2048, 32000, 1024, 1) == sb + max(fws, bws)
+
+
 def test_ce_argument_validation():
     L = _lib.lib()
     # sizes no buffer could have are refused before any byte count is formed
     assert L.nf_ce_workspace(4096, 1 << 40, 32000, 4096, 1) == 0
-    assert L.nf_ce_fwd(FAKE, FAKE, FAKE, 16, 1 << 40, 50, -100, 1, FAKE, None, FAKE, 1 << 20,
+    assert L.nf_ce_fwd(FAKE, FAKE, FAKE, 16, 1 << 40, 50, -100, 64, 1, FAKE, None, FAKE, 1 << 20,
                        FAKE, 1 << 20, None) == NF_ERR_ARG and "2^40" in _err()
     assert L.nf_gemm_nt(FAKE, 1 << 40, FAKE, 1 << 40, FAKE, 16, 16, 16, 1 << 40, 1,
                         None) == NF_ERR_ARG and "int32" in _err()
-    ws = L.nf_ce_workspace(4096, 2048, 32000, 4096, 1)
-    assert ws > 2048 * 32000 * 2  # holds W^T
-    assert L.nf_ce_workspace(4096, 2048, 32000, 4096, 2) == 0  # fp16 unsupported
+    ws = L.nf_ce_workspace(16, 8, 50, 64, 1)
     base = [FAKE, FAKE, FAKE]
     out = [FAKE, FAKE, FAKE, None, FAKE]
     assert L.nf_ce_fwd_bwd(*base, 16, 8, 50, -100, 0, 1, *out, ws, None) == NF_ERR_ARG
     assert L.nf_ce_fwd_bwd(*base, 16, 8, 50, -100, 64, 2, *out, ws, None) == NF_ERR_DTYPE
     assert L.nf_ce_fwd_bwd(*base, 16, 8, 50, -100, 64, 1, *out, 16, None) == NF_ERR_WORKSPACE
-    # the two-call form: state and scratch sizes, shapes, dtypes, buffers
-    sb = L.nf_ce_state_bytes(4096)
-    assert sb >= 4096 * 8 and L.nf_ce_state_bytes(0) == 0
-    fws = L.nf_ce_fwd_workspace(4096, 2048, 32000, 1)
-    bws = L.nf_ce_bwd_workspace(4096, 2048, 32000, 4096, 1)
-    assert bws > 2048 * 32000 * 2 and fws > 0 and ws == sb + max(fws, bws)
-    assert L.nf_ce_fwd_workspace(4096, 2048, 32000, 2) == 0
-    fwd = [FAKE, FAKE, FAKE, 16, 8, 50, -100, 1, FAKE, None, FAKE, sb, FAKE, fws, None]
+    # the two-call form: shapes, chunk rows, dtypes, buffers
+    sb = L.nf_ce_state_bytes(16, 8, 50, 64, 1)
+    fws = L.nf_ce_fwd_workspace(16, 8, 50, 64, 1)
+    bws = L.nf_ce_bwd_workspace(16, 8, 50, 64, 1)
+    fwd = [FAKE, FAKE, FAKE, 16, 8, 50, -100, 64, 1, FAKE, None, FAKE, sb, FAKE, fws, None]
     assert L.nf_ce_fwd(*fwd[:3], 0, *fwd[4:]) == NF_ERR_ARG
-    assert L.nf_ce_fwd(*fwd[:7], 2, *fwd[8:]) == NF_ERR_DTYPE
-    assert L.nf_ce_fwd(*fwd[:11], 8, *fwd[12:]) == NF_ERR_WORKSPACE  # state too small
-    assert L.nf_ce_fwd(*fwd[:13], 8, None) == NF_ERR_WORKSPACE
-    bwd = [FAKE, FAKE, 16, 8, 50, 64, 1, FAKE, sb, None, FAKE, 1, FAKE, 0, FAKE, bws, None]
-    assert L.nf_ce_bwd(*bwd[:5], 0, *bwd[6:]) == NF_ERR_ARG  # vocab_chunk
-    assert L.nf_ce_bwd(*bwd[:10], None, *bwd[11:]) == NF_ERR_ARG  # dhidden
-    assert L.nf_ce_bwd(*bwd[:11], 7, *bwd[12:]) == NF_ERR_DTYPE  # gradient dtype
-    assert L.nf_ce_bwd(*bwd[:15], 8, None) == NF_ERR_WORKSPACE
+    assert L.nf_ce_fwd(*fwd[:7], 0, *fwd[8:]) == NF_ERR_ARG and "chunk_rows" in _err()
+    assert L.nf_ce_fwd(*fwd[:8], 2, *fwd[9:]) == NF_ERR_DTYPE
+    assert L.nf_ce_fwd(*fwd[:12], sb - 1, *fwd[13:]) == NF_ERR_WORKSPACE  # state too small
+    assert L.nf_ce_fwd(*fwd[:14], fws - 1, None) == NF_ERR_WORKSPACE
+    # M, D, V, chunk_rows, dtype, state, state_bytes, g, dh, dt_h, dw, dt_w, ws, bytes, stream
+    bwd = [16, 8, 50, 64, 1, FAKE, sb, None, FAKE, 1, FAKE, 0, FAKE, bws, None]
+    assert L.nf_ce_bwd(*bwd[:3], 0, *bwd[4:]) == NF_ERR_ARG  # chunk_rows
+    assert L.nf_ce_bwd(*bwd[:8], None, *bwd[9:]) == NF_ERR_ARG  # dhidden
+    assert L.nf_ce_bwd(*bwd[:9], 7, *bwd[10:]) == NF_ERR_DTYPE  # gradient dtype
+    assert L.nf_ce_bwd(*bwd[:6], sb - 1, *bwd[7:]) == NF_ERR_WORKSPACE
+    assert L.nf_ce_bwd(*bwd[:13], bws - 1, None) == NF_ERR_WORKSPACE
     assert L.nf_gemm_nt(FAKE, 4, FAKE, 4, FAKE, 2, 2, 2, 8, 1, None) == NF_ERR_ARG  # lda < K
 
 
-def test_vocab_chunk_budget():
-    assert chunked_ce.vocab_chunk_for(512, 4096, 32000) == 4096
-    assert chunked_ce.vocab_chunk_for(1024, 4096, 32000) == 8064
-    assert chunked_ce.vocab_chunk_for(4096, 512, 1000) == 1000
-    assert chunked_ce.vocab_chunk_for(1, 4096, 1000) == 128
+def test_chunk_rows_argument():
+    assert chunked_ce.chunk_rows_for(1024) == 1024
+    assert chunked_ce.chunk_rows_for(7) == 7
     with pytest.raises(ValueError):
-        chunked_ce.vocab_chunk_for(0, 10, 10)
+        chunked_ce.chunk_rows_for(0)
 
 
 # ---------------------------------------------------------------------------

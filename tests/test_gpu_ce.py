@@ -146,13 +146,17 @@ def test_ce_ragged_shapes(cuda, dtype, m, d, v, chunk):
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-def test_ce_one_call_entry_point(cuda, dtype):
+@pytest.mark.parametrize("chunk_rows", [256, 100000])
+def test_ce_one_call_entry_point(cuda, dtype, chunk_rows):
     """nf_ce_fwd_bwd (the reference's structure: loss and unscaled fp32
     gradients in one call) through the C ABI: parity with the oracle, and
     bit-identical to the two-call path asked for fp32 gradients with
-    grad_output 1 (the same kernels in the same order)."""
-    note(f"ce one-call entry point dtype={dtype}")
-    m, d, v, vc = 300, 72, 1030, 256
+    grad_output 1 (the same kernels in the same order); with 256-row chunks
+    (the 500 valid rows of 600, every 6th ignored, in two chunks: the first
+    chunk's products in the forward, the second's in the backward) and with
+    one chunk holding every row."""
+    note(f"ce one-call entry point dtype={dtype} chunk_rows={chunk_rows}")
+    m, d, v = 600, 72, 1030
     hid, w, tgt = _ce_inputs(m, d, v, dtype, cuda, seed=11, w_std=0.2,
                              ignore=slice(None, None, 6))
     L = _lib.lib()
@@ -161,29 +165,30 @@ def test_ce_one_call_entry_point(cuda, dtype):
     dh = torch.empty(m, d, device=cuda)
     dw = torch.empty(v, d, device=cuda)
     bad = torch.empty(1, dtype=torch.int32, device=cuda)
-    nb = L.nf_ce_workspace(m, d, v, vc, code)
+    nb = L.nf_ce_workspace(m, d, v, chunk_rows, code)
     ws = torch.empty(nb, dtype=torch.uint8, device=cuda)
-    _lib.check(L.nf_ce_fwd_bwd(hid.data_ptr(), w.data_ptr(), tgt.data_ptr(), m, d, v, -100, vc,
-                               code, loss.data_ptr(), dh.data_ptr(), dw.data_ptr(), bad.data_ptr(),
-                               ws.data_ptr(), nb, s), "nf_ce_fwd_bwd")
+    _lib.check(L.nf_ce_fwd_bwd(hid.data_ptr(), w.data_ptr(), tgt.data_ptr(), m, d, v, -100,
+                               chunk_rows, code, loss.data_ptr(), dh.data_ptr(), dw.data_ptr(),
+                               bad.data_ptr(), ws.data_ptr(), nb, s), "nf_ce_fwd_bwd")
     torch.cuda.synchronize()
     assert int(bad.item()) == 0
     _check_ce(hid, w, tgt, loss, dh, dw, TOL[dtype], f"one call {dtype}")
     # the same through nf_ce_fwd + nf_ce_bwd
-    sb = L.nf_ce_state_bytes(m)
+    shape = (m, d, v, chunk_rows, code)
+    sb = L.nf_ce_state_bytes(*shape)
     state = torch.empty(sb, dtype=torch.uint8, device=cuda)
-    fw, bw = L.nf_ce_fwd_workspace(m, d, v, code), L.nf_ce_bwd_workspace(m, d, v, vc, code)
+    fw, bw = L.nf_ce_fwd_workspace(*shape), L.nf_ce_bwd_workspace(*shape)
     ws1 = torch.empty(fw, dtype=torch.uint8, device=cuda)
     ws2 = torch.empty(bw, dtype=torch.uint8, device=cuda)
     loss2, dh2, dw2 = torch.empty_like(loss), torch.empty_like(dh), torch.empty_like(dw)
     one = torch.ones((), device=cuda)
-    _lib.check(L.nf_ce_fwd(hid.data_ptr(), w.data_ptr(), tgt.data_ptr(), m, d, v, -100, code,
-                           loss2.data_ptr(), None, state.data_ptr(), sb, ws1.data_ptr(), fw, s),
-               "nf_ce_fwd")
+    _lib.check(L.nf_ce_fwd(hid.data_ptr(), w.data_ptr(), tgt.data_ptr(), m, d, v, -100,
+                           chunk_rows, code, loss2.data_ptr(), None, state.data_ptr(), sb,
+                           ws1.data_ptr(), fw, s), "nf_ce_fwd")
     f32 = _lib.dtype_code(torch.float32)
-    _lib.check(L.nf_ce_bwd(hid.data_ptr(), w.data_ptr(), m, d, v, vc, code, state.data_ptr(), sb,
-                           one.data_ptr(), dh2.data_ptr(), f32, dw2.data_ptr(), f32,
-                           ws2.data_ptr(), bw, s), "nf_ce_bwd")
+    _lib.check(L.nf_ce_bwd(m, d, v, chunk_rows, code, state.data_ptr(), sb, one.data_ptr(),
+                           dh2.data_ptr(), f32, dw2.data_ptr(), f32, ws2.data_ptr(), bw, s),
+               "nf_ce_bwd")
     torch.cuda.synchronize()
     assert torch.equal(loss, loss2) and torch.equal(dh, dh2) and torch.equal(dw, dw2)
 
@@ -277,8 +282,8 @@ def test_ce_cfg4_bf16_full_size_and_deterministic(cuda):
     tgt = torch.randint(0, v, (m,), generator=g)
     tgt[torch.randperm(m, generator=g)[:409]] = -100
     tgt = tgt.to(cuda)
-    loss, dh, dw = _run_ce(hid, w, tgt, 512)  # 512 rows of budget -> 4096-column vocab chunks
-    loss2, dh2, dw2 = _run_ce(hid, w, tgt, 512)
+    loss, dh, dw = _run_ce(hid, w, tgt, 1024)  # the default: 1024-row chunks, four here
+    loss2, dh2, dw2 = _run_ce(hid, w, tgt, 1024)
     assert torch.equal(loss, loss2) and torch.equal(dh, dh2) and torch.equal(dw, dw2)
     H = hid.float().cpu().numpy()
     W = w.float().cpu().numpy()
