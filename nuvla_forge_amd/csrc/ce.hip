@@ -495,12 +495,13 @@ __global__ __launch_bounds__(256) void ce_scatter_dh_kernel(const float *__restr
 // launch's makespan, max(longest block, total work / 256 CUs), plus the
 // write and read of the S fp32 slices, all in units of one 64-deep K stage of
 // a 256 x 256 tile (~2 us per CU at ~1.1 PFLOP/s, against ~5 TB/s of HBM).
-// A slice is at most kMaxSlice deep: a block streams 256 rows of each
-// operand over its K, and beyond ~2 MB per operand panel (4096 bf16 k) the
-// blocks an XCD runs at once no longer share their panels in its 4 MB L2 --
-// an unsplit K of 32000 measured 3.0 ms for the cfg4 gradients, bandwidth
-// bound, against ~0.9 ms of MFMA work.
-constexpr int64_t kMaxSlice = 4096;
+// At cfg4 in one chunk (3687 rows) it does not split (128 dH blocks of K
+// 32000 beside 1000 dW blocks of K 3687 balance by themselves): measured
+// against forcing slices of at most 2048 / 4096 / 8192 / 16384 (16 / 8 / 4 /
+// 2 slices), 1.64-1.66 ms against 1.85 / 1.77-1.80 / 1.72-1.74 / 1.67-1.69 ms
+// per fwd+bwd: the extra fp32 slice traffic costs more than shorter blocks
+// gain.  (This holds with the long job's blocks spread over all XCDs, see
+// gemm_store_kernel.)
 struct Split {
   int S;
   int64_t kslice;
@@ -517,7 +518,6 @@ inline Split dh_split(int64_t crows, int64_t D, int64_t V, int64_t ldp) {
   for (int S = 1; S <= 64; ++S) {
     const int64_t ks = round_up((ldp + S - 1) / S, C::BK);
     const int64_t se = (ldp + ks - 1) / ks;
-    if (ks > kMaxSlice && S < 64) continue;
     const double kh = (double)ks / C::BK;
     const double work = tw * kw + th * (double)se * kh;
     double t = work / 256.0;

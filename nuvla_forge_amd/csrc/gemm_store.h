@@ -147,10 +147,17 @@ template <class C, bool BUF, bool SB>
 __global__ NF_GEMM_BOUNDS(C) void gemm_store_kernel(GemmJob<typename C::TI> j0,
                                                     GemmJob<typename C::TI> j1) {
   __shared__ __attribute__((aligned(16))) char smem[C::LDS_BYTES];
-  int t = gemm::xcd_order(blockIdx.x, j0.tiles + j1.tiles);
-  const bool second = t >= j0.tiles;
+  // The job comes from the raw block index, so j0's blocks are dispatched
+  // first and spread over all 8 XCDs (block b runs on XCD b % 8); the
+  // XCD-grouped tile order applies within each job.  (Grouping the two jobs
+  // together put a long first job on the first XCDs only: the cross-entropy
+  // gradient launch with 256 long split-K blocks ahead of 1000 short ones
+  // ran 2.4x its work on 64 of the 256 CUs.)  A job starting at a block
+  // index that is not a multiple of 8 has its XCD groups rotated, which
+  // keeps each group on one XCD.
+  const bool second = (int)blockIdx.x >= j0.tiles;
   const GemmJob<typename C::TI> &j = second ? j1 : j0;
-  if (second) t -= j0.tiles;
+  int t = gemm::xcd_order(second ? (int)blockIdx.x - j0.tiles : (int)blockIdx.x, j.tiles);
   const int per_split = j.tiles / j.ksplit;
   const int ks = t / per_split;  // K slice of this block
   int tm, tn;
