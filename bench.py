@@ -59,7 +59,7 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--no-extra", action="store_true", help="headline workload only")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baselines")
     ap.add_argument("--only", choices=("swiglu", "ce", "stress", "traffic", "dit", "head",
-                                       "gateup"),
+                                       "gateup", "copy", "adaln"),
                     default=None,
                     help="run one secondary workload alone (for profiling) and print its "
                          "record instead of the headline line")
@@ -272,6 +272,7 @@ def bench_adaln(args, dev):
 
     # per-kernel durations: back-to-back launches of each C-ABI entry point
     kern_ms = adaln_kernel_ms(inp, t, dh, dout, args.steps)
+    instep_ms = adaln_in_step_ms(inp, t, dh, dout, args.steps)
 
     alg = adaln_alg_bytes(b, t, n)
     bwd_alg = (6 * m * n + 2 * b * n + n) * 2
@@ -281,11 +282,59 @@ def bench_adaln(args, dev):
     return {
         "b": b, "t": t, "n": n, "alg_bytes": alg, "graph_ms": graph_ms, "eager_ms": eager_ms,
         "graph1_ms": graph1_ms,
-        "graph_matches_eager": graph_ok, "kernel_ms": kern_ms,
+        "graph_matches_eager": graph_ok, "kernel_ms": kern_ms, "in_step_ms": instep_ms,
         "bwd_alg_bytes": bwd_alg, "bwd_gbs": bwd_gbs, "fwd_alg_bytes": fwd_alg, "fwd_gbs": fwd_gbs,
+        "bwd_gbs_in_step": bwd_alg / (instep_ms["nf_adaln_bwd"] * 1e-3) / 1e9,
         "gbs": alg / (graph_ms * 1e-3) / 1e9, "gbs_eager": alg / (eager_ms * 1e-3) / 1e9,
         "ref_style_gbs_11MNe": 11 * m * n * 2 / (graph_ms * 1e-3) / 1e9,
     }
+
+
+def bench_copy(args, dev):
+    """Streaming ceilings for context (never the roofline denominator): torch's
+    own element-wise kernels -- copy (1 read + 1 write), add (2 + 1),
+    addcmul (3 + 1) -- on bf16 tensors of the cfg2 activation size (16 MiB,
+    [8192, 1024]: the working set stays in the 256 MB Infinity Cache) and of
+    1 GiB ([32768, 16384]: beyond it), each as the mean of 20 back-to-back
+    launches in a HIP graph."""
+    import torch
+
+    out = {}
+    for label, shape in (("cfg2_16MiB", (8192, 1024)), ("beyond_cache_1GiB", (32768, 16384))):
+        a, b, c, d = (torch.randn(*shape, device=dev).to(torch.bfloat16) for _ in range(4))
+        nb = a.numel() * a.element_size()
+        cases = {"copy_1r1w": (lambda: d.copy_(a), 2 * nb),
+                 "add_2r1w": (lambda: torch.add(a, b, out=d), 3 * nb),
+                 "addcmul_3r1w": (lambda: torch.addcmul(a, b, c, out=d), 4 * nb)}
+        out[label] = {}
+        for name, (fn, nbytes) in cases.items():
+            ms = per_launch_ms(fn, max(5, args.steps // 5))
+            out[label][name] = {"us": ms * 1e3, "gbs": nbytes / (ms * 1e-3) / 1e9,
+                                "frac_of_8tbs": nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS}
+        del a, b, c, d
+    return out
+
+
+def adaln_in_step_ms(inp, t, dh, dout, steps, reps=10):
+    """Each adaLN kernel's share of the step as it runs inside the step:
+    `reps` repetitions of forward -> backward -> reduction launched through
+    the C ABI in one HIP graph, minus the same graph with that one launch
+    left out (the others' inputs and outputs are unchanged, so their cache
+    state is the step's).  Milliseconds per launch; 'sequence' is the whole
+    three-launch sequence."""
+    fwd, bwd, red = adaln_launchers(inp, t, dh, dout)
+    seq = {"nf_adaln_fwd": fwd, "nf_adaln_bwd": bwd, "nf_adaln_bwd_reduce": red}
+
+    def timed(names):
+        def launch():
+            for k in names:
+                seq[k]()
+        return per_launch_ms(launch, steps, reps)
+
+    full = timed(list(seq))
+    out = {k: full - timed([j for j in seq if j != k]) for k in seq}
+    out["sequence"] = full
+    return out
 
 
 def bench_swiglu(args, dev, m=8192, h=4096):
@@ -572,7 +621,8 @@ def main() -> int:
     if args.only:
         fn = {"swiglu": bench_swiglu, "ce": bench_ce, "stress": bench_stress,
               "traffic": bench_traffic, "dit": bench_dit_seam,
-              "head": bench_ce_reasoning_head, "gateup": bench_gate_up}[args.only]
+              "head": bench_ce_reasoning_head, "gateup": bench_gate_up, "copy": bench_copy,
+              "adaln": bench_adaln}[args.only]
         print(json.dumps({"workload": args.only, **fn(args, dev)}), flush=True)
         return 0
 
@@ -634,6 +684,7 @@ def main() -> int:
             "graph1_ms_per_step": round(ad["graph1_ms"], 5),
             "graph_matches_eager": ad["graph_matches_eager"],
             "kernel_ms": {k: round(v, 5) for k, v in ad["kernel_ms"].items()},
+            "in_step_kernel_ms": {k: round(v, 5) for k, v in ad["in_step_ms"].items()},
             "fwd_kernel_gbs": round(ad["fwd_gbs"], 1),
             "ref_style_gbs_11MNe": round(ad["ref_style_gbs_11MNe"], 1),
         },
@@ -648,6 +699,11 @@ def main() -> int:
             "traffic_source": TRAFFIC_FILE,
             "alg_bytes_per_launch": ad["bwd_alg_bytes"],
             "mean_launch_ms": round(bwd_ms, 5),
+            # the same kernel inside the fwd -> bwd -> reduce sequence (graph
+            # of the sequence minus the graph without it), beside the
+            # back-to-back launches above
+            "in_step_ms": round(ad["in_step_ms"]["nf_adaln_bwd"], 5),
+            "frac_in_step": round(ad["bwd_gbs_in_step"] / HBM_PEAK_GBS, 4),
         },
         "cpu_baseline": None if cpu is None else {
             k: cpu["adaln"][k] for k in ("value", "unit", "cores", "kind", "sample")
