@@ -59,7 +59,7 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--no-extra", action="store_true", help="headline workload only")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baselines")
     ap.add_argument("--only", choices=("swiglu", "ce", "stress", "traffic", "dit", "head",
-                                       "gateup", "copy", "adaln"),
+                                       "gateup", "copy", "adaln", "ce_gemm_ceiling"),
                     default=None,
                     help="run one secondary workload alone (for profiling) and print its "
                          "record instead of the headline line")
@@ -288,6 +288,36 @@ def bench_adaln(args, dev):
         "gbs": alg / (graph_ms * 1e-3) / 1e9, "gbs_eager": alg / (eager_ms * 1e-3) / 1e9,
         "ref_style_gbs_11MNe": 11 * m * n * 2 / (graph_ms * 1e-3) / 1e9,
     }
+
+
+def bench_ce_gemm_ceiling(args, dev):
+    """The vendor GEMM library on the products of the CE at cfg4 (bf16 in,
+    fp32 accumulate; torch.mm -> hipBLASLt), for context: the logits
+    S = H_valid W^T ([3687, 2048] x [2048, 32000]), dH = P W ([3687, 32000] x
+    [32000, 2048]) and dW = P^T H_valid ([32000, 3687] x [3687, 2048]) --
+    6 M_valid V D flops in all, each timed as 20 back-to-back launches in a
+    HIP graph, with fp32 outputs as this build's fp32 accumulators where the
+    product is accumulated, bf16 where it is final."""
+    import torch
+
+    g = torch.Generator().manual_seed(50)
+    mv, d, v = 3687, 2048, 32000
+    h = torch.randn(mv, d, generator=g).to(torch.bfloat16).to(dev)
+    w = (torch.randn(v, d, generator=g) * 0.02).to(torch.bfloat16).to(dev)
+    p = (torch.randn(mv, v, generator=g) * 1e-4).to(torch.bfloat16).to(dev)
+    pt = p.t().contiguous()
+    out = {}
+    cases = {"logits_S": (lambda: torch.mm(h, w.t()), 2 * mv * v * d),
+             "dH": (lambda: torch.mm(p, w), 2 * mv * v * d),
+             "dW": (lambda: torch.mm(pt, h), 2 * mv * v * d)}
+    total = 0.0
+    for name, (fn, flops) in cases.items():
+        ms = per_launch_ms(fn, max(5, args.steps // 5))
+        total += ms
+        out[name] = {"us": ms * 1e3, "tflops": flops / (ms * 1e-3) / 1e12}
+    out["sum_us"] = total * 1e3
+    out["tflops_6MvVD"] = 6 * mv * v * d / (total * 1e-3) / 1e12
+    return out
 
 
 def bench_copy(args, dev):
@@ -622,7 +652,7 @@ def main() -> int:
         fn = {"swiglu": bench_swiglu, "ce": bench_ce, "stress": bench_stress,
               "traffic": bench_traffic, "dit": bench_dit_seam,
               "head": bench_ce_reasoning_head, "gateup": bench_gate_up, "copy": bench_copy,
-              "adaln": bench_adaln}[args.only]
+              "adaln": bench_adaln, "ce_gemm_ceiling": bench_ce_gemm_ceiling}[args.only]
         print(json.dumps({"workload": args.only, **fn(args, dev)}), flush=True)
         return 0
 
