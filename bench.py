@@ -514,18 +514,29 @@ def bench_dit_seam(args, dev, b=8, t=6, n=384):
 def bench_ce_reasoning_head(args, dev, m=512, d=384, v=32000):
     """The reasoning head at the reference's model shape (model/nuvla.py:150-164:
     batch 8 x 64 text tokens, width 384, vocabulary 32000, chunk_size 1024):
-    bf16 hidden, fp32 lm_head, under bf16 autocast; fused vs the reference's
-    eager chunk loop, tokens/s of forward + backward."""
+    fp32 lm_head under bf16 autocast, with bf16 hidden and, as the model feeds
+    it (the fp32 residual stream out of the text blocks), fp32 hidden; fused vs
+    the reference's eager chunk loop, tokens/s of forward + backward."""
     import torch
 
-    from nuvla_forge_amd.kernels import chunked_cross_entropy
-
     g = torch.Generator().manual_seed(41)
-    hid = torch.randn(m, d, generator=g).to(torch.bfloat16).to(dev)
+    hid = torch.randn(m, d, generator=g)
     w = (torch.randn(v, d, generator=g) * 0.02).to(dev)
     tgt = torch.randint(0, v, (m,), generator=g)
     tgt[::7] = -100
     tgt = tgt.to(dev)
+    out = {"m": m, "d": d, "v": v}
+    out.update(_head_case(args, hid.to(torch.bfloat16).to(dev), w, tgt))
+    out["hidden_fp32"] = _head_case(args, hid.to(dev), w, tgt)
+    return out
+
+
+def _head_case(args, hid, w, tgt):
+    import torch
+
+    from nuvla_forge_amd.kernels import chunked_cross_entropy
+
+    m = hid.shape[0]
 
     def make(force):
         lh, lw = hid.detach().requires_grad_(True), w.detach().requires_grad_(True)
@@ -544,7 +555,8 @@ def bench_ce_reasoning_head(args, dev, m=512, d=384, v=32000):
     fused_ms = time_eager(make(False), steps, warm)
     eager_ms = time_eager(make(True), steps, warm)
     fused_graph_ms, _, _ = time_graph(lambda: make(False), steps, warm)
-    return {"m": m, "d": d, "v": v, "fused_ms": fused_ms, "eager_ms": eager_ms,
+    return {"hidden_dtype": str(hid.dtype).replace("torch.", ""), "lm_head_dtype": "float32",
+            "fused_ms": fused_ms, "eager_ms": eager_ms,
             "fused_graph_ms": fused_graph_ms, "timing": "both eager launches, events",
             "tokens_per_s": m / (fused_ms * 1e-3), "eager_tokens_per_s": m / (eager_ms * 1e-3),
             "speedup": eager_ms / fused_ms}

@@ -182,17 +182,29 @@ __global__ __launch_bounds__(256) void ce_gather_kernel(const T *__restrict__ H,
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ int e_swz(int t) { return 8 * (((t >> 3) ^ (t & 7)) & 31); }
 
+// Blocks past the vtiles x ttiles logits tiles run the transpose regions of
+// `tp` (16-bit inputs only): dispatched last, they fill the CUs that the
+// final partial wave of tiles leaves idle.
 template <class C, bool BUF, bool SB>
 __global__ NF_GEMM_BOUNDS(C) void ce_logits_kernel(
     const typename C::TI *W, const typename C::TI *Hc, int64_t V, int64_t D, int64_t j0,
     int64_t crows, const int *n_ptr, const int *tcol, float2 *stats, float *tgt,
-    typename C::TI *E, int64_t ldp, int vtiles, int ttiles) {
+    typename C::TI *E, int64_t ldp, int vtiles, int ttiles, gemm::TpJobs tp) {
   using TI = typename C::TI;
   constexpr int ES = (int)sizeof(TI);
   // one LDS buffer only: a second __shared__ object makes the compiler wait
   // for every direct-to-LDS copy in flight before each operand read of the
-  // K loop; the E staging reuses the operand stages after the K loop
+  // K loop; the E staging and the transposes reuse the operand stages
   __shared__ __attribute__((aligned(16))) char smem[C::LDS_BYTES];
+  if constexpr (ES == 2) {
+    static_assert(C::LDS_BYTES >= gemm::kTpRegionRows * gemm::kTpRegionPitch * 2,
+                  "transpose region does not fit the LDS");
+    const int q = (int)blockIdx.x - vtiles * ttiles;
+    if (q >= 0) {
+      if (q < tp.n) gemm::tp_jobs_run<C::NT>(tp, q, reinterpret_cast<uint16_t *>(smem));
+      return;
+    }
+  }
   int vt, tt;
   gemm::group_tile(gemm::xcd_order(blockIdx.x, vtiles * ttiles), vtiles, ttiles,
                    gemm::kTileGroup, vt, tt);
@@ -673,8 +685,32 @@ int ce_fwd_run(const TI *H, const TI *W, const int64_t *targets, int64_t M, int6
       ce_gather_kernel<TI, false><<<(unsigned)blocks, 256, 0, s>>>(H, D, rows, S.n, M, Hc);
     if ((e = check_launch("ce_gather"))) return e;
   }
-  if ((e = launch_transpose<U>(Hc, M, D, D, S.Hct, L.ldht, s))) return e;
-  if ((e = launch_transpose<U>(W, V, D, D, S.Wt, L.ldwt, s))) return e;
+  // W^T and Hc^T are only read by the gradient products: with 16-bit
+  // elements and 16-byte rows they are formed by extra blocks at the end of
+  // the first logits launch, otherwise by their own launches here
+  gemm::TpJobs tp{};
+  const bool fold = sizeof(TI) == 2 && D % 8 == 0 && L.ldwt % 8 == 0 && L.ldht % 8 == 0 &&
+                    aligned16(W) && aligned16(Hc) && aligned16(S.Wt) && aligned16(S.Hct);
+  if (fold) {
+    const void *src[2] = {W, Hc};
+    void *dst[2] = {S.Wt, S.Hct};
+    const int64_t rows[2] = {V, M}, ldo[2] = {L.ldwt, L.ldht};
+    for (int j = 0; j < 2; ++j) {
+      tp.in[j] = static_cast<const uint16_t *>(src[j]);
+      tp.out[j] = static_cast<uint16_t *>(dst[j]);
+      tp.R[j] = rows[j];
+      tp.Cn[j] = D;
+      tp.ldi[j] = D;
+      tp.ldo[j] = ldo[j];
+      tp.rb[j] = (int)((ldo[j] + gemm::kTpRegionRows - 1) / gemm::kTpRegionRows);
+      tp.cb[j] = (int)((D + gemm::kTpRegionCols - 1) / gemm::kTpRegionCols);
+    }
+    tp.n = tp.rb[0] * tp.cb[0] + tp.rb[1] * tp.cb[1];
+  } else {
+    if ((e = launch_transpose<U>(Hc, M, D, D, S.Hct, L.ldht, s))) return e;
+    if ((e = launch_transpose<U>(W, V, D, D, S.Wt, L.ldwt, s))) return e;
+  }
+  const gemm::TpJobs none{};
 
   const bool vk = buf_ok<TI>(Hc, D, M, D) && buf_ok<TI>(W, D, V, D);
   const bool sb = sb_ok(L.crows * L.ldp * (int64_t)sizeof(TI));
@@ -682,15 +718,17 @@ int ce_fwd_run(const TI *H, const TI *W, const int64_t *targets, int64_t M, int6
   const dim3 gfix((unsigned)(L.crows / 64), (unsigned)((L.ldp + 63) / 64));
   for (int64_t c = 0; c < L.nch; ++c) {
     const int64_t j0 = c * L.crows;
+    const gemm::TpJobs &tj = c == 0 ? tp : none;
+    const unsigned grid = glog + (unsigned)tj.n;
     if (vk && sb)
-      ce_logits_kernel<C, true, true><<<glog, C::NT, 0, s>>>(
-          W, Hc, V, D, j0, L.crows, S.n, tcol, stats, tgt, S.P, L.ldp, L.vtiles, L.ttiles);
+      ce_logits_kernel<C, true, true><<<grid, C::NT, 0, s>>>(
+          W, Hc, V, D, j0, L.crows, S.n, tcol, stats, tgt, S.P, L.ldp, L.vtiles, L.ttiles, tj);
     else if (vk)
-      ce_logits_kernel<C, true, false><<<glog, C::NT, 0, s>>>(
-          W, Hc, V, D, j0, L.crows, S.n, tcol, stats, tgt, S.P, L.ldp, L.vtiles, L.ttiles);
+      ce_logits_kernel<C, true, false><<<grid, C::NT, 0, s>>>(
+          W, Hc, V, D, j0, L.crows, S.n, tcol, stats, tgt, S.P, L.ldp, L.vtiles, L.ttiles, tj);
     else
-      ce_logits_kernel<C, false, false><<<glog, C::NT, 0, s>>>(
-          W, Hc, V, D, j0, L.crows, S.n, tcol, stats, tgt, S.P, L.ldp, L.vtiles, L.ttiles);
+      ce_logits_kernel<C, false, false><<<grid, C::NT, 0, s>>>(
+          W, Hc, V, D, j0, L.crows, S.n, tcol, stats, tgt, S.P, L.ldp, L.vtiles, L.ttiles, tj);
     if ((e = check_launch("ce_logits"))) return e;
     ce_lse_kernel<<<(unsigned)(L.crows / kLseRows), kLseRows * kLseParts, 0, s>>>(
         stats, L.ntiles, L.crows, tgt, S.n, j0, lse, loss_row);

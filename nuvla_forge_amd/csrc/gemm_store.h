@@ -322,6 +322,83 @@ static __global__ __launch_bounds__(256) void transpose16_kernel(
 }
 
 
+// The same transpose as one region of work inside another kernel (a GEMM
+// launch whose last blocks transpose while its final partial wave of tiles
+// leaves CUs idle): rows [r0, r0 + 256) x columns [c0, c0 + 128) of `in`
+// become the corresponding columns / rows of `out`, rows R .. ldo - 1 of the
+// region written as zeros.  NTH threads (a multiple of 256), all of which
+// call it; `lds` holds kTpRegionRows * kTpRegionPitch elements.  Same
+// requirements as transpose16_kernel.  Every thread first issues its eight
+// 16-byte row loads, then writes them to LDS as 32-bit pairs; a half-wave's
+// column reads cover 8 row segments x 4 column pairs, 32 distinct banks
+// (pitch 130 elements: 8 rows = 520 dwords, 8 mod 64).
+constexpr int kTpRegionRows = 256, kTpRegionCols = 128, kTpRegionPitch = 130;
+template <int NTH>
+__device__ __forceinline__ void transpose16_region(const uint16_t *__restrict__ in, int64_t R,
+                                                   int64_t Cn, int64_t ldi,
+                                                   uint16_t *__restrict__ out, int64_t ldo,
+                                                   int64_t r0, int64_t c0, uint16_t *lds) {
+  constexpr int VPR = kTpRegionCols / 8;           // 16-byte vectors per input row
+  constexpr int NV = kTpRegionRows * VPR / NTH;    // input vectors per thread
+  constexpr int SEGS = kTpRegionRows / 8;          // 16-byte vectors per output row
+  constexpr int NO = kTpRegionCols * SEGS / NTH;   // output vectors per thread
+  static_assert(NTH % 256 == 0 && NV >= 1 && NO >= 1 && NV * NTH == kTpRegionRows * VPR &&
+                    NO * NTH == kTpRegionCols * SEGS, "region / thread mismatch");
+  const int t = threadIdx.x;
+  u32x4 v[NV];
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int idx = t + i * NTH, row = idx / VPR, vec = idx % VPR;
+    const int64_t r = r0 + row, c = c0 + 8 * vec;
+    v[i] = u32x4{0u, 0u, 0u, 0u};
+    if (r < R && c < Cn) v[i] = *reinterpret_cast<const u32x4 *>(in + r * ldi + c);
+  }
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int idx = t + i * NTH, row = idx / VPR, vec = idx % VPR;
+    uint32_t *d = reinterpret_cast<uint32_t *>(lds + row * kTpRegionPitch + 8 * vec);
+    d[0] = v[i][0]; d[1] = v[i][1]; d[2] = v[i][2]; d[3] = v[i][3];
+  }
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < NO; ++i) {
+    // lanes: 8 consecutive row segments x 8 columns; seg = low 3 bits of t
+    // plus 8 per pair of iterations, column = t / 8 + 64 * (i % 2) (NTH 512)
+    const int idx = t + i * NTH;
+    const int seg = (idx % 8) + 8 * (idx / (8 * kTpRegionCols));
+    const int oc = (idx / 8) % kTpRegionCols;
+    const int64_t c = c0 + oc, r = r0 + 8 * seg;
+    uint16_t e[8];
+#pragma unroll
+    for (int q = 0; q < 8; ++q) e[q] = lds[(8 * seg + q) * kTpRegionPitch + oc];
+    u32x4 o;
+    __builtin_memcpy(&o, e, 16);
+    if (c < Cn && r < ldo) *reinterpret_cast<u32x4 *>(out + c * ldo + r) = o;
+  }
+}
+
+// Transposes folded into a launch: up to two 16-bit matrices, each cut into
+// regions of kTpRegionRows x kTpRegionCols (rb x cb of them); `n` regions in
+// all (0: none).
+struct TpJobs {
+  const uint16_t *in[2];
+  uint16_t *out[2];
+  int64_t R[2], Cn[2], ldi[2], ldo[2];
+  int rb[2], cb[2];
+  int n;
+};
+
+// Region `q` of the jobs (q < n): which matrix, and its region row / column.
+template <int NTH>
+__device__ __forceinline__ void tp_jobs_run(const TpJobs &tp, int q, uint16_t *lds) {
+  const int n0 = tp.rb[0] * tp.cb[0];
+  const int j = q < n0 ? 0 : 1;
+  const int k = j ? q - n0 : q;
+  const int rr = k % tp.rb[j], cc = k / tp.rb[j];
+  transpose16_region<NTH>(tp.in[j], tp.R[j], tp.Cn[j], tp.ldi[j], tp.out[j], tp.ldo[j],
+                          (int64_t)rr * kTpRegionRows, (int64_t)cc * kTpRegionCols, lds);
+}
+
 // rows x cols 16-bit elements of a matrix with row stride ld set to zero (a
 // kernel rather than hipMemset2DAsync, so that a captured graph holds no
 // memset node)
