@@ -9,9 +9,10 @@
 // Forward (nf_ce_fwd):
 //   1. ce_compact: the valid rows in order -> rows[], their target columns,
 //      pos[m] (compacted index or -1), n_valid, inv = 1 / max(n_valid, 1).
-//   2. gather + transposes: Hc = H[rows] ([M, D], zero past n_valid), its
-//      transpose Hct [D, M], and Wt = W^T [D, V] (zero-padded), so every GEMM
-//      below reads K-contiguous operands.
+//   2. gather: Hc = H[rows] ([M, D], zero past n_valid).  Its transpose Hct
+//      [D, M] and Wt = W^T [D, V] (zero-padded), which make every gradient
+//      operand K-contiguous, are formed by the first logits launch's last
+//      blocks (16-bit inputs) or by transpose launches here (fp32).
 //   3. per chunk of `crows` compacted rows:
 //      ce_logits: S = Hc_c W^T tile by tile (formed transposed, W Hc_c^T, so a
 //                 lane holds each token's logits along the vocabulary); per
@@ -21,11 +22,11 @@
 //      ce_lse:    lse per row from the tile statistics (fixed order), and the
 //                 row's loss lse - S[target];
 //      ce_fix:    P = inv * (E * exp(max - lse) - onehot) in place, and its
-//                 transpose PT [V, crows];
+//                 transpose PT [V, crows]; in the last chunk's launch, also
+//                 the mean loss over the valid rows;
 //      gradient products of every chunk but the last (one launch):
 //                 dW_acc (+)= PT_c Hc_c      (fp32 [V, D], K = the chunk's rows)
 //                 dHc_c   = P_c Wt^T         (fp32, K = V, split along K)
-//   4. ce_loss:   the mean over the valid rows.
 // Backward (nf_ce_bwd, with the loss's grad_output g): the last chunk's
 // products, dW = g * (dW_acc + PT H_c) written in dweight's type, and the
 // scatter of dHc back to the hidden rows as g * dH (0 for ignored rows).
@@ -366,15 +367,20 @@ __global__ __launch_bounds__(kLseRows * kLseParts) void ce_lse_kernel(
 // its 64 row factors come from the statistics once, the tile is read and
 // written as 16-byte row vectors and transposed through LDS into 16-byte
 // PT vectors.
+// With `loss` set (the last chunk's launch, when every row's loss is known),
+// block (0, 0) first writes the mean loss: each thread sums a strided share
+// of the n valid rows' losses, each wavefront reduces its lanes (fixed
+// butterfly), and thread 0 adds the 4 wavefront sums in order.  This saves
+// the launch a one-block loss kernel would cost.
 // ---------------------------------------------------------------------------
+constexpr int kFixThreads = 256;
+
 template <typename TI>
-__global__ __launch_bounds__(256) void ce_fix_kernel(TI *__restrict__ P, int64_t ldp,
-                                                     TI *__restrict__ PT, int64_t crows,
-                                                     int64_t V, const float2 *__restrict__ stats,
-                                                     int wtm, const float *__restrict__ lse,
-                                                     const int *__restrict__ tcol,
-                                                     const int *n_ptr, int64_t j0,
-                                                     const float *inv_ptr) {
+__global__ __launch_bounds__(kFixThreads) void ce_fix_kernel(
+    TI *__restrict__ P, int64_t ldp, TI *__restrict__ PT, int64_t crows, int64_t V,
+    const float2 *__restrict__ stats, int wtm, const float *__restrict__ lse,
+    const int *__restrict__ tcol, const int *n_ptr, int64_t j0, const float *inv_ptr,
+    const float *__restrict__ loss_row, float *loss) {
   using U = typename std::conditional<sizeof(TI) == 2, uint16_t, uint32_t>::type;
   constexpr int VE = 16 / (int)sizeof(TI);  // elements per 16-byte vector
   constexpr int VPR = 64 / VE;              // vectors per 64-element row
@@ -382,6 +388,20 @@ __global__ __launch_bounds__(256) void ce_fix_kernel(TI *__restrict__ P, int64_t
   __shared__ U tile[64 * PITCH];
   __shared__ float fac[64];
   __shared__ int tcl[64];
+  if (loss != nullptr && blockIdx.x == 0 && blockIdx.y == 0) {
+    __shared__ float sl[kFixThreads / 64];
+    const int64_t n = *n_ptr;
+    float a = 0.f;
+    for (int64_t i = threadIdx.x; i < n; i += kFixThreads) a += loss_row[i];
+    a = wave_sum(a);
+    if ((threadIdx.x & 63) == 0) sl[threadIdx.x >> 6] = a;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      float tl = 0.f;
+      for (int k = 0; k < kFixThreads / 64; ++k) tl += sl[k];
+      *loss = tl * *inv_ptr;
+    }
+  }
   const int64_t cnt = chunk_count(n_ptr, j0, crows);
   const int64_t rows8 = (cnt + 7) / 8 * 8;
   const int64_t r0 = (int64_t)blockIdx.x * 64, c0 = (int64_t)blockIdx.y * 64;
@@ -401,7 +421,7 @@ __global__ __launch_bounds__(256) void ce_fix_kernel(TI *__restrict__ P, int64_t
   }
   const float inv = *inv_ptr;
   __syncthreads();
-  for (int idx = t; idx < 64 * VPR; idx += 256) {
+  for (int idx = t; idx < 64 * VPR; idx += kFixThreads) {
     const int rr = idx / VPR, cv = idx % VPR;
     const int64_t r = r0 + rr, c = c0 + (int64_t)cv * VE;
     if (c >= ldp) continue;  // ldp is a multiple of VE
@@ -430,7 +450,7 @@ __global__ __launch_bounds__(256) void ce_fix_kernel(TI *__restrict__ P, int64_t
     }
   }
   __syncthreads();
-  for (int idx = t; idx < 64 * VPR; idx += 256) {
+  for (int idx = t; idx < 64 * VPR; idx += kFixThreads) {
     const int cc = idx / VPR, rv = idx % VPR;  // vocabulary column, row vector
     const int64_t col = c0 + cc, r = r0 + (int64_t)rv * VE;
     if (col >= V || r >= rows8) continue;  // rows8 is a multiple of VE
@@ -442,33 +462,7 @@ __global__ __launch_bounds__(256) void ce_fix_kernel(TI *__restrict__ P, int64_t
 }
 
 // ---------------------------------------------------------------------------
-// 6. loss = inv * sum of the valid rows' losses: one block; each thread sums
-// a strided share of the rows, each wavefront reduces its lanes (fixed
-// butterfly), and thread 0 adds the 16 wavefront sums in order.
-// ---------------------------------------------------------------------------
-constexpr int kLossThreads = 1024;
-
-__global__ __launch_bounds__(kLossThreads) void ce_loss_kernel(const float *loss_row,
-                                                                const int *n_ptr,
-                                                                const float *inv_ptr,
-                                                                float *loss) {
-  constexpr int kWaves = kLossThreads / 64;
-  __shared__ float sl[kWaves];
-  const int64_t n = *n_ptr;
-  float a = 0.f;
-  for (int64_t i = threadIdx.x; i < n; i += kLossThreads) a += loss_row[i];
-  a = wave_sum(a);
-  if ((threadIdx.x & 63) == 0) sl[threadIdx.x >> 6] = a;
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    float tl = 0.f;
-    for (int k = 0; k < kWaves; ++k) tl += sl[k];
-    *loss = tl * *inv_ptr;
-  }
-}
-
-// ---------------------------------------------------------------------------
-// 7. dH[m, :] = g * dHc[pos[m], :] in dH's type, 0 where pos[m] < 0.
+// 6. dH[m, :] = g * dHc[pos[m], :] in dH's type, 0 where pos[m] < 0.
 // ---------------------------------------------------------------------------
 // VE elements per thread step (4 when D is a multiple of 4: one 16-byte load).
 template <int VE>
@@ -733,16 +727,17 @@ int ce_fwd_run(const TI *H, const TI *W, const int64_t *targets, int64_t M, int6
     ce_lse_kernel<<<(unsigned)(L.crows / kLseRows), kLseRows * kLseParts, 0, s>>>(
         stats, L.ntiles, L.crows, tgt, S.n, j0, lse, loss_row);
     if ((e = check_launch("ce_lse"))) return e;
-    ce_fix_kernel<TI><<<gfix, 256, 0, s>>>(S.P, L.ldp, S.PT, L.crows, V, stats, L.wtm, lse,
-                                           tcol, S.n, j0, S.inv);
+    const bool last = c + 1 == L.nch;  // the mean loss comes with the last chunk's fix-up
+    ce_fix_kernel<TI><<<gfix, kFixThreads, 0, s>>>(S.P, L.ldp, S.PT, L.crows, V, stats, L.wtm,
+                                                   lse, tcol, S.n, j0, S.inv, loss_row,
+                                                   last ? loss : nullptr);
     if ((e = check_launch("ce_fix"))) return e;
-    if (c + 1 < L.nch &&
+    if (!last &&
         (e = launch_grads<TI>(L, S, c, D, V, c > 0 ? S.dWacc : nullptr, S.dWacc, NF_DTYPE_F32,
                               nullptr, part, s)))
       return e;
   }
-  ce_loss_kernel<<<1, kLossThreads, 0, s>>>(loss_row, S.n, S.inv, loss);
-  return check_launch("ce_loss");
+  return NF_OK;
 }
 
 template <typename TI>
