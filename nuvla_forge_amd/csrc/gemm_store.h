@@ -157,16 +157,29 @@ __global__ NF_GEMM_BOUNDS(C) void gemm_store_kernel(GemmJob<typename C::TI> j0,
   // keeps each group on one XCD.
   const bool second = (int)blockIdx.x >= j0.tiles;
   const GemmJob<typename C::TI> &j = second ? j1 : j0;
-  int t = gemm::xcd_order(second ? (int)blockIdx.x - j0.tiles : (int)blockIdx.x, j.tiles);
-  const int per_split = j.tiles / j.ksplit;
-  const int ks = t / per_split;  // K slice of this block
-  int tm, tn;
-  gemm::group_tile(t % per_split, j.tiles_m, per_split / j.tiles_m, gemm::kTileGroup, tm, tn);
-  const int64_t m0 = (int64_t)tm * C::BM;
-  const int64_t n0 = (int64_t)tn * C::BN;
+  const int b = second ? (int)blockIdx.x - j0.tiles : (int)blockIdx.x;
   int64_t M, K;
   job_extents(j, M, K);
-  if (m0 >= M) return;  // a dynamic row count left this tile without rows
+  // With a device row count the job's tiles are renumbered over the rows
+  // that exist, so its real blocks are the first ones and the rest exit at
+  // once.  The dispatcher hands out blocks in order, round-robin over the
+  // XCDs; exiting blocks left among the real ones (the last tile row of every
+  // K slice) gathered on two XCDs, which then filled all their CUs with long
+  // blocks and held up the dispatch of every later block.
+  const int tiles_n = j.tiles / j.ksplit / j.tiles_m;
+  int tiles_m = j.tiles_m, tiles = j.tiles;
+  if (j.dyn && j.dyn_rows) {
+    tiles_m = (int)((M + C::BM - 1) / C::BM);
+    tiles = tiles_m * tiles_n * j.ksplit;
+  }
+  if (b >= tiles) return;
+  int t = gemm::xcd_order(b, tiles);
+  const int per_split = tiles_m * tiles_n;
+  const int ks = t / per_split;  // K slice of this block
+  int tm, tn;
+  gemm::group_tile(t % per_split, tiles_m, tiles_n, gemm::kTileGroup, tm, tn);
+  const int64_t m0 = (int64_t)tm * C::BM;
+  const int64_t n0 = (int64_t)tn * C::BN;
   const int64_t N = j.N;
   const bool split = j.ksplit > 1;
   const int64_t k0 = ks * j.kslice;
