@@ -141,45 +141,74 @@ __global__ __launch_bounds__(kCompactThreads) void ce_compact_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// 2. Hc[r, :] = H[rows[r], :] for r < n_valid, 0 for n_valid <= r < R.
-// VEC: 16-byte vectors (D a multiple of the vector width, aligned rows).
+// 2. Hc[r, :] = H[rows[r], :] for r < n_valid, 0 for n_valid <= r < R, and
+// the row's reference logit mref[r] = H[rows[r], :] . W[tcol[r], :] (fp32, a
+// fixed-order sum; 0 past n_valid).  One wavefront per row.  E is stored
+// relative to mref (exp(S - mref)), so mref needs only to lie within the
+// exponent range of the row's largest logit; the target logit does for every
+// row whose loss is below ~75 nats, and the statistics pass sends any other
+// row through an exact recomputation (ce_lse_kernel).  VEC: 16-byte vectors
+// (D a multiple of the vector width, aligned rows).
 // ---------------------------------------------------------------------------
+constexpr int kGatherThreads = 256;
+
 template <typename T, bool VEC>
-__global__ __launch_bounds__(256) void ce_gather_kernel(const T *__restrict__ H, int64_t D,
-                                                        const int *__restrict__ rows,
-                                                        const int *n_ptr, int64_t R,
-                                                        T *__restrict__ Hc) {
+__global__ __launch_bounds__(kGatherThreads) void ce_gather_kernel(
+    const T *__restrict__ H, const T *__restrict__ W, int64_t D, const int *__restrict__ rows,
+    const int *__restrict__ tcol, const int *n_ptr, int64_t R, T *__restrict__ Hc,
+    float *__restrict__ mref) {
+  constexpr int kWaves = kGatherThreads / 64;
   const int64_t n = *n_ptr;
   constexpr int VE = VEC ? 16 / (int)sizeof(T) : 1;
-  const int64_t dv = D / VE;
-  const int64_t total = R * dv;
-  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total;
-       i += (int64_t)gridDim.x * 256) {
-    const int64_t r = i / dv, c = (i % dv) * VE;
-    if constexpr (VEC) {
-      u32x4 v = {0u, 0u, 0u, 0u};
-      if (r < n) v = *reinterpret_cast<const u32x4 *>(H + (int64_t)rows[r] * D + c);
-      *reinterpret_cast<u32x4 *>(Hc + r * D + c) = v;
-    } else {
-      Hc[r * D + c] = r < n ? H[(int64_t)rows[r] * D + c] : static_cast<T>(0.f);
+  const int l = threadIdx.x & 63;
+  for (int64_t r = (int64_t)blockIdx.x * kWaves + (threadIdx.x >> 6); r < R;
+       r += (int64_t)gridDim.x * kWaves) {
+    const bool live = r < n;
+    const T *h = live ? H + (int64_t)rows[r] * D : nullptr;
+    const T *w = live ? W + (int64_t)tcol[r] * D : nullptr;
+    float dot = 0.f;
+    for (int64_t c = (int64_t)l * VE; c < D; c += 64 * VE) {
+      if constexpr (VEC) {
+        u32x4 hv = {0u, 0u, 0u, 0u}, wv = {0u, 0u, 0u, 0u};
+        if (live) {
+          hv = *reinterpret_cast<const u32x4 *>(h + c);
+          wv = *reinterpret_cast<const u32x4 *>(w + c);
+        }
+        *reinterpret_cast<u32x4 *>(Hc + r * D + c) = hv;
+        T he[VE], we[VE];
+        __builtin_memcpy(he, &hv, 16);
+        __builtin_memcpy(we, &wv, 16);
+#pragma unroll
+        for (int q = 0; q < VE; ++q) dot += static_cast<float>(he[q]) * static_cast<float>(we[q]);
+      } else {
+        const T hv = live ? h[c] : static_cast<T>(0.f);
+        Hc[r * D + c] = hv;
+        if (live) dot += static_cast<float>(hv) * static_cast<float>(w[c]);
+      }
     }
+    dot = wave_sum(dot);
+    if (l == 0) mref[r] = live ? dot : 0.f;
   }
 }
 
 // ---------------------------------------------------------------------------
-// 3. logits of one chunk, their tile statistics and E = exp(S - tile max).
-// The product is formed transposed, acc = W_tile Hc_tile^T (rows: vocabulary
-// entries, columns: tokens), so each lane holds 16 * TM logits of each of its
-// TN tokens: a wavefront's max and sum of exp over its WTM vocabulary rows
-// are reductions in registers plus one exchange between the lane halves.
-// Statistics tile t covers vocabulary rows [t * WTM, (t + 1) * WTM):
-// stats[t * crows + token] = (max, sum exp(S - max)).  The target logit comes
-// from the one lane holding it.  E goes out row-major [token, ldp] (columns
-// V..ldp zero): with 16-bit 256 x 256 tiles through LDS (free once the K loop
-// ends) as 16-byte row vectors -- element (t, c) at byte t * 512 +
-// 2 * (c ^ e_swz(t)), the XOR moving whole 8-element vectors so rows still
-// read as vectors while the writes of a half-wave spread over the banks;
-// otherwise straight from the accumulators.
+// 3. logits of one chunk, their tile statistics and E = exp(S - mref) in the
+// input type, row-major and transposed.  The product is formed transposed,
+// acc = W_tile Hc_tile^T (rows: vocabulary entries, columns: tokens), so each
+// lane holds 16 * TM logits of each of its TN tokens: a wavefront's max and
+// sum of exp over its WTM vocabulary rows are reductions in registers plus
+// one exchange between the lane halves.  Statistics tile t covers vocabulary
+// rows [t * WTM, (t + 1) * WTM): stats[t * crows + token] = (max, sum
+// exp(S - max)), exact in fp32 whatever mref is.  The target logit comes from
+// the one lane holding it.  E = exp(S - max) * exp(max - mref) goes out
+// row-major [token, ldp] (columns V..ldp zero) and transposed [V, ldet]
+// (tokens past the chunk's rows zero up to a multiple of 8): with 16-bit
+// 256 x 256 tiles through LDS (free once the K loop ends) -- element (t, c)
+// at byte t * 512 + 2 * (c ^ e_swz(t)), the XOR moving whole 8-element
+// vectors so rows still read as 16-byte vectors while the writes of a
+// half-wave spread over the banks, and a column gathers its 8 tokens per
+// vector from 8 rows; otherwise straight from the accumulators.  With a row
+// factor P = inv * exp(mref - lse) (ce_lse_kernel), P * E is the softmax.
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ int e_swz(int t) { return 8 * (((t >> 3) ^ (t & 7)) & 31); }
 
@@ -189,8 +218,9 @@ __device__ __forceinline__ int e_swz(int t) { return 8 * (((t >> 3) ^ (t & 7)) &
 template <class C, bool BUF, bool SB>
 __global__ NF_GEMM_BOUNDS(C) void ce_logits_kernel(
     const typename C::TI *W, const typename C::TI *Hc, int64_t V, int64_t D, int64_t j0,
-    int64_t crows, const int *n_ptr, const int *tcol, float2 *stats, float *tgt,
-    typename C::TI *E, int64_t ldp, int vtiles, int ttiles, gemm::TpJobs tp) {
+    int64_t crows, const int *n_ptr, const int *tcol, const float *mref, float2 *stats,
+    float *tgt, typename C::TI *E, int64_t ldp, typename C::TI *ET, int64_t ldet, int vtiles,
+    int ttiles, gemm::TpJobs tp) {
   using TI = typename C::TI;
   constexpr int ES = (int)sizeof(TI);
   // one LDS buffer only: a second __shared__ object makes the compiler wait
@@ -235,8 +265,10 @@ __global__ NF_GEMM_BOUNDS(C) void ce_logits_kernel(
   }
   constexpr bool kStaged = ES == 2 && C::BM == 256 && C::BN == 256 && C::NT == 512 &&
                            C::LDS_BYTES >= 256 * 512;
-  OutBuf<SB> eout;
+  OutBuf<SB> eout, etout;
   eout.init(E, crows * ldp * ES);
+  etout.init(ET, V * ldet * ES);
+  const int64_t cnt8 = (cnt + 7) / 8 * 8;
 #pragma unroll
   for (int j = 0; j < C::TN; ++j) {
     const int tl = wn * C::WTN + j * 32 + (l & 31);  // token within the tile
@@ -262,11 +294,11 @@ __global__ NF_GEMM_BOUNDS(C) void ce_logits_kernel(
       }
     }
     // a wavefront with no row inside the vocabulary keeps (-inf, 0) and E = 0
-    const float mref = mx == -INFINITY ? 0.f : mx;
+    const float mt = mx == -INFINITY ? 0.f : mx;
 #pragma unroll
     for (int i = 0; i < C::TM; ++i)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) acc[i][j][r] = exp_f32(acc[i][j][r] - mref);
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = exp_f32(acc[i][j][r] - mt);
     float s = 0.f;
 #pragma unroll
     for (int i = 0; i < C::TM; ++i)
@@ -274,6 +306,9 @@ __global__ NF_GEMM_BOUNDS(C) void ce_logits_kernel(
       for (int r = 0; r < 16; ++r) s += acc[i][j][r];
     s += __shfl_xor(s, 32);
     if (half == 0 && tok < cnt) stats[(int64_t)stile * crows + tok] = make_float2(mx, s);
+    // E relative to the row's reference: exp(S - mt) * exp(mt - mref); a
+    // factor that overflows marks a row the statistics pass recomputes
+    const float k = mx == -INFINITY ? 0.f : exp_f32(mx - (tok < cnt ? mref[j0 + tok] : 0.f));
 
 #pragma unroll
     for (int i = 0; i < C::TM; ++i)
@@ -282,23 +317,31 @@ __global__ NF_GEMM_BOUNDS(C) void ce_logits_kernel(
         const int o = i * 32 + 8 * g;  // offset of r = 4g from crow0
         TI ev[4];
 #pragma unroll
-        for (int q = 0; q < 4; ++q) ev[q] = static_cast<TI>(acc[i][j][4 * g + q]);
+        for (int q = 0; q < 4; ++q) ev[q] = static_cast<TI>(acc[i][j][4 * g + q] * k);
         if constexpr (kStaged) {
           const int cl = wm * C::WTM + 4 * half + o;  // tile column (vocabulary)
           u32x2 packed;
           __builtin_memcpy(&packed, ev, 8);
           *reinterpret_cast<u32x2 *>(smem + tl * 512 + 2 * (cl ^ e_swz(tl))) = packed;
-        } else if constexpr (ES == 2) {
-          u32x2 packed;
-          __builtin_memcpy(&packed, ev, 8);
-          const int64_t c = crow0 + o;
-          eout.st64((tok * ldp + c) * ES, tok < cnt && c < ldp, packed);
         } else {
+          // straight from the accumulators: E row-major and E^T (zero past
+          // the chunk's rows, up to the K padding of the dW product)
           const int64_t c = crow0 + o;
 #pragma unroll
-          for (int q = 0; q < 4; ++q)
-            eout.st32((tok * ldp + c + q) * ES, tok < cnt && c + q < ldp,
-                      static_cast<float>(ev[q]));
+          for (int q = 0; q < 4; ++q) {
+            const TI e = tok < cnt ? ev[q] : static_cast<TI>(0.f);
+            if constexpr (ES == 2) {
+              uint16_t bits;
+              __builtin_memcpy(&bits, &e, 2);
+              eout.st16((tok * ldp + c + q) * ES, tok < cnt && c + q < ldp, bits);
+              etout.st16(((c + q) * ldet + tok) * ES, c + q < V && tok < cnt8, bits);
+            } else {
+              eout.st32((tok * ldp + c + q) * ES, tok < cnt && c + q < ldp,
+                        static_cast<float>(e));
+              etout.st32(((c + q) * ldet + tok) * ES, c + q < V && tok < cnt8,
+                         static_cast<float>(e));
+            }
+          }
         }
       }
   }
@@ -315,6 +358,25 @@ __global__ NF_GEMM_BOUNDS(C) void ce_logits_kernel(
       const int64_t tok = t0 + t, c = v0 + c8;
       eout.st128((tok * ldp + c) * ES, tok < cnt && c < ldp, v);
     }
+    // E^T: a half-wave stores one vocabulary row's 256 tokens (32 vectors of
+    // 8 tokens, each gathered from 8 tile rows); tokens past the chunk's
+    // rows are zero up to cnt8 (the dW product's K padding), none beyond
+#pragma unroll 2
+    for (int it = 0; it < 16; ++it) {
+      const int idx = it * C::NT + (int)threadIdx.x;
+      const int tv = idx & 31, c = idx >> 5;  // token vector, tile column
+      const int64_t v = v0 + c, tok = t0 + 8 * tv;
+      uint16_t e[8];
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        const int t = 8 * tv + q;
+        const uint16_t b = *reinterpret_cast<const uint16_t *>(smem + t * 512 + 2 * (c ^ e_swz(t)));
+        e[q] = tok + q < cnt ? b : (uint16_t)0;
+      }
+      u32x4 pk;
+      __builtin_memcpy(&pk, e, 16);
+      etout.st128((v * ldet + tok) * ES, v < V && tok < cnt8, pk);
+    }
   }
 }
 
@@ -325,12 +387,29 @@ __global__ NF_GEMM_BOUNDS(C) void ce_logits_kernel(
 // combines the 16 partial results in order.  A row of 16 tokens is 128
 // contiguous bytes of the [ntiles][crows] statistics.
 // ---------------------------------------------------------------------------
-constexpr int kLseRows = 16, kLseParts = 16;
+// The row factor cfac = inv * exp(mref - lse), so that cfac * E is the
+// softmax over the row scaled by 1 / n.  The one-hot term goes into E itself:
+// the target entry becomes exp(z - mref) - exp(lse - mref), so cfac * E is
+// (softmax - onehot) / n, the gradient of the mean loss by the logits.  A row
+// whose largest logit lies more than kRefGap above mref (its E entries would
+// leave the exponent range) is recomputed exactly by its block: fp32 dot
+// products in a fixed order, E relative to the recomputed row max, written to
+// both layouts.  (The target logit is within kRefGap of the row max for any
+// row whose loss is under kRefGap nats.)
+constexpr float kRefGap = 75.f;
+constexpr int kLseRows = 16, kLseParts = 16, kLseThreads = kLseRows * kLseParts;
 
-__global__ __launch_bounds__(kLseRows * kLseParts) void ce_lse_kernel(
+template <typename TI>
+__global__ __launch_bounds__(kLseThreads) void ce_lse_kernel(
     const float2 *__restrict__ stats, int ntiles, int64_t crows, const float *tgt,
-    const int *n_ptr, int64_t j0, float *lse, float *loss_row) {
+    const int *n_ptr, int64_t j0, const float *inv_ptr, const int *__restrict__ tcol,
+    float *__restrict__ mref, float *__restrict__ cfac, float *loss_row, TI *P, int64_t ldp,
+    TI *PT, int64_t ldet, const TI *__restrict__ W, const TI *__restrict__ Hc, int64_t D,
+    int64_t V) {
   __shared__ float2 part[kLseParts][kLseRows];
+  __shared__ float lse_s[kLseRows];
+  __shared__ int redo[kLseRows];
+  __shared__ float red[kLseThreads / 64];
   const int64_t cnt = chunk_count(n_ptr, j0, crows);
   const int rl = threadIdx.x % kLseRows, q = threadIdx.x / kLseRows;
   const int64_t row = (int64_t)blockIdx.x * kLseRows + rl;
@@ -351,113 +430,145 @@ __global__ __launch_bounds__(kLseRows * kLseParts) void ce_lse_kernel(
   }
   part[q][rl] = a;
   __syncthreads();
-  if (q != 0 || row >= cnt) return;
+  const float inv = *inv_ptr;
+  if (q == 0) {
+    int again = 0;
+    if (row < cnt) {
 #pragma unroll
-  for (int k = 1; k < kLseParts; ++k) a = combine_stats(a, part[k][rl]);
-  const float ls = a.x + log_f32(a.y);
-  lse[row] = ls;
-  loss_row[j0 + row] = ls - tgt[row];
+      for (int k = 1; k < kLseParts; ++k) a = combine_stats(a, part[k][rl]);
+      const float ls = a.x + log_f32(a.y);
+      const float z = tgt[row];
+      loss_row[j0 + row] = ls - z;
+      lse_s[rl] = ls;
+      const float m = mref[j0 + row];
+      again = !(a.x - m <= kRefGap);  // also for a NaN / inf row
+      if (!again) {
+        cfac[j0 + row] = inv * exp_f32(m - ls);
+        const int64_t tc = tcol[j0 + row];
+        const TI e = static_cast<TI>(exp_f32(z - m) - exp_f32(ls - m));
+        P[row * ldp + tc] = e;
+        PT[tc * ldet + row] = e;
+      }
+    }
+    redo[rl] = again;
+  }
+  __syncthreads();
+  // the recomputation of rows outside the reference's range (rare)
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  for (int k = 0; k < kLseRows; ++k) {
+    if (!redo[k]) continue;  // uniform across the block
+    const int64_t r = (int64_t)blockIdx.x * kLseRows + k;
+    const TI *h = Hc + (j0 + r) * D;
+    auto logit = [&](int64_t v) {
+      const TI *w = W + v * D;
+      float s = 0.f;
+      for (int64_t d = 0; d < D; ++d) s += static_cast<float>(h[d]) * static_cast<float>(w[d]);
+      return s;
+    };
+    float mx = -INFINITY;
+    for (int64_t v = threadIdx.x; v < V; v += kLseThreads) mx = fmaxf(mx, logit(v));
+    mx = wave_max(mx);
+    if (lane == 0) red[wv] = mx;
+    __syncthreads();
+    mx = red[0];
+    for (int u = 1; u < kLseThreads / 64; ++u) mx = fmaxf(mx, red[u]);
+    __syncthreads();
+    const float ls = lse_s[k];
+    const int64_t tc = tcol[j0 + r];
+    for (int64_t v = threadIdx.x; v < ldp; v += kLseThreads) {
+      float e = 0.f;
+      if (v < V) {
+        e = exp_f32(logit(v) - mx);
+        if (v == tc) e -= exp_f32(ls - mx);
+      }
+      const TI te = static_cast<TI>(e);
+      P[r * ldp + v] = te;
+      if (v < V) PT[v * ldet + r] = te;
+    }
+    if (threadIdx.x == 0) {
+      mref[j0 + r] = mx;
+      cfac[j0 + r] = inv * exp_f32(mx - ls);
+    }
+  }
 }
 
 // ---------------------------------------------------------------------------
-// 5. P = inv * (E * exp(tile max - lse) - onehot) for the rows of a chunk, in
-// place ([crows, ldp], columns V..ldp zero), and PT [V, crows] (rows count
-// .. round_up(count, 8) zero: the dW product's K padding).  A block takes a
-// 64 x 64 tile (64 rows, 64 vocabulary columns inside one statistics tile):
-// its 64 row factors come from the statistics once, the tile is read and
-// written as 16-byte row vectors and transposed through LDS into 16-byte
-// PT vectors.
+// 5. The dW product's B operand for a chunk: Hct[d, j0 + r] = cfac[j0 + r] *
+// Hc[j0 + r, d] in the input type for r < count, 0 for count <= r <
+// round_up(count, 8) (the product's K padding): the row factor enters the
+// product over the rows through this operand.  64 x 64 tiles through LDS;
+// VEC: 16-byte row vectors in and column vectors out (D a multiple of the
+// vector width), else one element per access.
 // With `loss` set (the last chunk's launch, when every row's loss is known),
 // block (0, 0) first writes the mean loss: each thread sums a strided share
 // of the n valid rows' losses, each wavefront reduces its lanes (fixed
 // butterfly), and thread 0 adds the 4 wavefront sums in order.  This saves
 // the launch a one-block loss kernel would cost.
 // ---------------------------------------------------------------------------
-constexpr int kFixThreads = 256;
+constexpr int kPrepThreads = 256;
 
-template <typename TI>
-__global__ __launch_bounds__(kFixThreads) void ce_fix_kernel(
-    TI *__restrict__ P, int64_t ldp, TI *__restrict__ PT, int64_t crows, int64_t V,
-    const float2 *__restrict__ stats, int wtm, const float *__restrict__ lse,
-    const int *__restrict__ tcol, const int *n_ptr, int64_t j0, const float *inv_ptr,
-    const float *__restrict__ loss_row, float *loss) {
+template <typename TI, bool VEC>
+__global__ __launch_bounds__(kPrepThreads) void ce_scale_hct_kernel(
+    const TI *__restrict__ Hc, int64_t D, const float *__restrict__ cfac,
+    const int *n_ptr, int64_t j0, int64_t crows, TI *__restrict__ Hct, int64_t ldht,
+    const float *__restrict__ loss_row, const float *inv_ptr, float *loss) {
   using U = typename std::conditional<sizeof(TI) == 2, uint16_t, uint32_t>::type;
-  constexpr int VE = 16 / (int)sizeof(TI);  // elements per 16-byte vector
-  constexpr int VPR = 64 / VE;              // vectors per 64-element row
+  constexpr int VE = VEC ? 16 / (int)sizeof(TI) : 1;  // elements per access
   constexpr int PITCH = 64 + (sizeof(TI) == 2 ? 2 : 1);
   __shared__ U tile[64 * PITCH];
-  __shared__ float fac[64];
-  __shared__ int tcl[64];
   if (loss != nullptr && blockIdx.x == 0 && blockIdx.y == 0) {
-    __shared__ float sl[kFixThreads / 64];
+    __shared__ float sl[kPrepThreads / 64];
     const int64_t n = *n_ptr;
     float a = 0.f;
-    for (int64_t i = threadIdx.x; i < n; i += kFixThreads) a += loss_row[i];
+    for (int64_t i = threadIdx.x; i < n; i += kPrepThreads) a += loss_row[i];
     a = wave_sum(a);
     if ((threadIdx.x & 63) == 0) sl[threadIdx.x >> 6] = a;
     __syncthreads();
     if (threadIdx.x == 0) {
       float tl = 0.f;
-      for (int k = 0; k < kFixThreads / 64; ++k) tl += sl[k];
+      for (int k = 0; k < kPrepThreads / 64; ++k) tl += sl[k];
       *loss = tl * *inv_ptr;
     }
   }
   const int64_t cnt = chunk_count(n_ptr, j0, crows);
-  const int64_t rows8 = (cnt + 7) / 8 * 8;
-  const int64_t r0 = (int64_t)blockIdx.x * 64, c0 = (int64_t)blockIdx.y * 64;
-  if (r0 >= rows8) return;
+  const int64_t cnt8 = (cnt + 7) / 8 * 8;
+  const int64_t r0 = (int64_t)blockIdx.x * 64, d0 = (int64_t)blockIdx.y * 64;
+  if (r0 >= cnt8) return;
   const int t = threadIdx.x;
-  if (t < 64) {
-    const int64_t r = r0 + t;
-    float f = 0.f;
-    int tc = -1;
-    if (r < cnt) {
-      const float m = stats[(c0 / wtm) * crows + r].x;
-      f = m == -INFINITY ? 0.f : exp_f32(m - lse[r]);
-      tc = tcol[j0 + r];
-    }
-    fac[t] = f;
-    tcl[t] = tc;
-  }
-  const float inv = *inv_ptr;
-  __syncthreads();
-  for (int idx = t; idx < 64 * VPR; idx += kFixThreads) {
+  constexpr int VPR = 64 / VE;  // accesses per 64-element tile row
+  for (int idx = t; idx < 64 * VPR; idx += kPrepThreads) {
     const int rr = idx / VPR, cv = idx % VPR;
-    const int64_t r = r0 + rr, c = c0 + (int64_t)cv * VE;
-    if (c >= ldp) continue;  // ldp is a multiple of VE
-    TI *p = P + r * ldp + c;
+    const int64_t r = r0 + rr, d = d0 + (int64_t)cv * VE;
     TI e[VE];
-    if (r < cnt) {
-      *reinterpret_cast<u32x4 *>(e) = *reinterpret_cast<const u32x4 *>(p);
-      const float f = fac[rr];
-      const int tc = tcl[rr];
-#pragma unroll
-      for (int q = 0; q < VE; ++q) {
-        const int64_t col = c + q;
-        const float v = static_cast<float>(e[q]) * f - (col == tc ? 1.f : 0.f);
-        e[q] = static_cast<TI>(col < V ? v * inv : 0.f);
-      }
+    const float f = r < cnt ? cfac[j0 + r] : 0.f;
+    if constexpr (VEC) {
+      u32x4 v = {0u, 0u, 0u, 0u};
+      if (r < cnt && d < D) v = *reinterpret_cast<const u32x4 *>(Hc + (j0 + r) * D + d);
+      __builtin_memcpy(e, &v, 16);
     } else {
-#pragma unroll
-      for (int q = 0; q < VE; ++q) e[q] = static_cast<TI>(0.f);
+      e[0] = (r < cnt && d < D) ? Hc[(j0 + r) * D + d] : static_cast<TI>(0.f);
     }
-    if (r < crows) *reinterpret_cast<u32x4 *>(p) = *reinterpret_cast<const u32x4 *>(e);
 #pragma unroll
     for (int q = 0; q < VE; ++q) {
+      const TI sc = static_cast<TI>(static_cast<float>(e[q]) * f);
       U bits;
-      __builtin_memcpy(&bits, &e[q], sizeof(U));
+      __builtin_memcpy(&bits, &sc, sizeof(U));
       tile[rr * PITCH + cv * VE + q] = bits;
     }
   }
   __syncthreads();
-  for (int idx = t; idx < 64 * VPR; idx += kFixThreads) {
-    const int cc = idx / VPR, rv = idx % VPR;  // vocabulary column, row vector
-    const int64_t col = c0 + cc, r = r0 + (int64_t)rv * VE;
-    if (col >= V || r >= rows8) continue;  // rows8 is a multiple of VE
+  for (int idx = t; idx < 64 * VPR; idx += kPrepThreads) {
+    const int dc = idx / VPR, rv = idx % VPR;  // output row (d), row vector
+    const int64_t d = d0 + dc, r = r0 + (int64_t)rv * VE;
+    if (d >= D || r >= cnt8) continue;  // cnt8 is a multiple of VE
     U e[VE];
 #pragma unroll
-    for (int q = 0; q < VE; ++q) e[q] = tile[(rv * VE + q) * PITCH + cc];
-    *reinterpret_cast<u32x4 *>(PT + col * crows + r) = *reinterpret_cast<const u32x4 *>(e);
+    for (int q = 0; q < VE; ++q) e[q] = tile[(rv * VE + q) * PITCH + dc];
+    if constexpr (VEC) {
+      *reinterpret_cast<u32x4 *>(Hct + d * ldht + j0 + r) = *reinterpret_cast<const u32x4 *>(e);
+    } else {
+      __builtin_memcpy(Hct + d * ldht + j0 + r, e, sizeof(U));
+    }
   }
 }
 
@@ -545,9 +656,9 @@ struct Plan {
   int vtiles, ttiles;     // logits grid
   Split split;            // dH product's K split
   // state (kept from nf_ce_fwd to nf_ce_bwd)
-  size_t s_scal, s_pos, s_wt, s_hct, s_p, s_pt, s_dhc, s_dwacc, s_total;
+  size_t s_scal, s_pos, s_cfac, s_wt, s_hct, s_p, s_pt, s_dhc, s_dwacc, s_total;
   // forward scratch
-  size_t f_hc, f_rows, f_tcol, f_stats, f_tgt, f_lse, f_loss, f_part, f_total;
+  size_t f_hc, f_rows, f_tcol, f_mref, f_stats, f_tgt, f_loss, f_part, f_total;
   // backward scratch
   size_t b_part, b_total;
 };
@@ -574,6 +685,7 @@ inline Plan make_plan(int64_t M, int64_t D, int64_t V, int64_t chunk_rows) {
   auto take = [&](size_t bytes) { const size_t at = o; o = align256(o + bytes); return at; };
   P.s_scal = take(64);  // n_valid (int), inv (float)
   P.s_pos = take((size_t)M * sizeof(int));
+  P.s_cfac = take((size_t)M * sizeof(float));
   P.s_wt = take((size_t)D * P.ldwt * es);
   P.s_hct = take((size_t)D * P.ldht * es);
   P.s_p = take((size_t)P.crows * P.ldp * es);
@@ -585,9 +697,9 @@ inline Plan make_plan(int64_t M, int64_t D, int64_t V, int64_t chunk_rows) {
   P.f_hc = take((size_t)M * D * es);
   P.f_rows = take((size_t)M * sizeof(int));
   P.f_tcol = take((size_t)M * sizeof(int));
+  P.f_mref = take((size_t)M * sizeof(float));
   P.f_stats = take((size_t)P.ntiles * P.crows * sizeof(float2));
   P.f_tgt = take((size_t)P.crows * sizeof(float));
-  P.f_lse = take((size_t)P.crows * sizeof(float));
   P.f_loss = take((size_t)M * sizeof(float));
   P.f_part = take(P.nch > 1 ? part : 0);
   P.f_total = o;
@@ -603,12 +715,14 @@ struct StateView {
   int *n;
   float *inv;
   int *pos;
+  float *cfac;  // per compacted row: inv * exp(mref - lse)
   TI *Wt, *Hct, *P, *PT;
   float *dHc, *dWacc;
   StateView(const Plan &L, char *s)
       : n(reinterpret_cast<int *>(s + L.s_scal)),
         inv(reinterpret_cast<float *>(s + L.s_scal + 16)),
         pos(reinterpret_cast<int *>(s + L.s_pos)),
+        cfac(reinterpret_cast<float *>(s + L.s_cfac)),
         Wt(reinterpret_cast<TI *>(s + L.s_wt)),
         Hct(reinterpret_cast<TI *>(s + L.s_hct)),
         P(reinterpret_cast<TI *>(s + L.s_p)),
@@ -617,9 +731,11 @@ struct StateView {
         dWacc(reinterpret_cast<float *>(s + L.s_dwacc)) {}
 };
 
-// The gradient products of chunk c in one launch: dW (+)= PT_c Hc_c and
-// dHc_c = P_c Wt^T (split along K).  dW goes to `dw_out` (type dt_w, scaled
-// by g when given) on top of `dw_in` when given.
+// The gradient products of chunk c in one launch: dW (+)= PT_c Hct_c^T (Hct
+// holding the chunk's rows already times their factor cfac) and dHc_c =
+// cfac_c * (P_c Wt^T) (the factor per output row, split along K).  dW goes
+// to `dw_out` (type dt_w, scaled by g when given) on top of `dw_in` when
+// given.
 template <typename TI>
 int launch_grads(const Plan &L, const StateView<TI> &S, int64_t c, int64_t D, int64_t V,
                  const float *dw_in, void *dw_out, int dt_w, const float *g, float *part,
@@ -636,6 +752,7 @@ int launch_grads(const Plan &L, const StateView<TI> &S, int64_t c, int64_t D, in
   jh.dyn = S.n;
   jh.dyn_base = j0;
   jh.dyn_rows = 1;  // M: the chunk's rows
+  jh.row_scale = S.cfac + j0;
   if (L.split.S > 1) {
     jh.ksplit = L.split.S;
     jh.kslice = L.split.kslice;
@@ -660,7 +777,7 @@ int ce_fwd_run(const TI *H, const TI *W, const int64_t *targets, int64_t M, int6
   int *tcol = reinterpret_cast<int *>(ws + L.f_tcol);
   float2 *stats = reinterpret_cast<float2 *>(ws + L.f_stats);
   float *tgt = reinterpret_cast<float *>(ws + L.f_tgt);
-  float *lse = reinterpret_cast<float *>(ws + L.f_lse);
+  float *mref = reinterpret_cast<float *>(ws + L.f_mref);
   float *loss_row = reinterpret_cast<float *>(ws + L.f_loss);
   float *part = reinterpret_cast<float *>(ws + L.f_part);
   int e;
@@ -668,70 +785,74 @@ int ce_fwd_run(const TI *H, const TI *W, const int64_t *targets, int64_t M, int6
   ce_compact_kernel<<<1, kCompactThreads, 0, s>>>(targets, M, V, ignore_index, rows, tcol,
                                                   S.pos, S.n, S.inv, bad);
   if ((e = check_launch("ce_compact"))) return e;
+  const bool vec = D % (16 / (int64_t)sizeof(TI)) == 0 && aligned16(H) && aligned16(W) &&
+                   aligned16(Hc);
   {
-    const bool vec = D % (16 / (int64_t)sizeof(TI)) == 0 && aligned16(H) && aligned16(Hc);
-    int64_t blocks = (M * D / (vec ? 16 / (int64_t)sizeof(TI) : 1) + 255) / 256;
+    constexpr int kRowsPerBlock = kGatherThreads / 64;
+    int64_t blocks = (M + kRowsPerBlock - 1) / kRowsPerBlock;
     if (blocks > 4096) blocks = 4096;
-    if (blocks < 1) blocks = 1;
     if (vec)
-      ce_gather_kernel<TI, true><<<(unsigned)blocks, 256, 0, s>>>(H, D, rows, S.n, M, Hc);
+      ce_gather_kernel<TI, true><<<(unsigned)blocks, kGatherThreads, 0, s>>>(
+          H, W, D, rows, tcol, S.n, M, Hc, mref);
     else
-      ce_gather_kernel<TI, false><<<(unsigned)blocks, 256, 0, s>>>(H, D, rows, S.n, M, Hc);
+      ce_gather_kernel<TI, false><<<(unsigned)blocks, kGatherThreads, 0, s>>>(
+          H, W, D, rows, tcol, S.n, M, Hc, mref);
     if ((e = check_launch("ce_gather"))) return e;
   }
-  // W^T and Hc^T are only read by the gradient products: with 16-bit
-  // elements and 16-byte rows they are formed by extra blocks at the end of
-  // the first logits launch, otherwise by their own launches here
+  // W^T is only read by the dH product: with 16-bit elements and 16-byte
+  // rows it is formed by extra blocks at the end of the first logits launch,
+  // otherwise by its own launch here
   gemm::TpJobs tp{};
-  const bool fold = sizeof(TI) == 2 && D % 8 == 0 && L.ldwt % 8 == 0 && L.ldht % 8 == 0 &&
-                    aligned16(W) && aligned16(Hc) && aligned16(S.Wt) && aligned16(S.Hct);
+  const bool fold = sizeof(TI) == 2 && D % 8 == 0 && L.ldwt % 8 == 0 && aligned16(W) &&
+                    aligned16(S.Wt);
   if (fold) {
-    const void *src[2] = {W, Hc};
-    void *dst[2] = {S.Wt, S.Hct};
-    const int64_t rows[2] = {V, M}, ldo[2] = {L.ldwt, L.ldht};
-    for (int j = 0; j < 2; ++j) {
-      tp.in[j] = static_cast<const uint16_t *>(src[j]);
-      tp.out[j] = static_cast<uint16_t *>(dst[j]);
-      tp.R[j] = rows[j];
-      tp.Cn[j] = D;
-      tp.ldi[j] = D;
-      tp.ldo[j] = ldo[j];
-      tp.rb[j] = (int)((ldo[j] + gemm::kTpRegionRows - 1) / gemm::kTpRegionRows);
-      tp.cb[j] = (int)((D + gemm::kTpRegionCols - 1) / gemm::kTpRegionCols);
-    }
-    tp.n = tp.rb[0] * tp.cb[0] + tp.rb[1] * tp.cb[1];
-  } else {
-    if ((e = launch_transpose<U>(Hc, M, D, D, S.Hct, L.ldht, s))) return e;
-    if ((e = launch_transpose<U>(W, V, D, D, S.Wt, L.ldwt, s))) return e;
+    tp.in[0] = reinterpret_cast<const uint16_t *>(W);
+    tp.out[0] = reinterpret_cast<uint16_t *>(S.Wt);
+    tp.R[0] = V;
+    tp.Cn[0] = D;
+    tp.ldi[0] = D;
+    tp.ldo[0] = L.ldwt;
+    tp.rb[0] = (int)((L.ldwt + gemm::kTpRegionRows - 1) / gemm::kTpRegionRows);
+    tp.cb[0] = (int)((D + gemm::kTpRegionCols - 1) / gemm::kTpRegionCols);
+    tp.n = tp.rb[0] * tp.cb[0];
+  } else if ((e = launch_transpose<U>(W, V, D, D, S.Wt, L.ldwt, s))) {
+    return e;
   }
   const gemm::TpJobs none{};
 
   const bool vk = buf_ok<TI>(Hc, D, M, D) && buf_ok<TI>(W, D, V, D);
   const bool sb = sb_ok(L.crows * L.ldp * (int64_t)sizeof(TI));
   const unsigned glog = (unsigned)(L.vtiles * L.ttiles);
-  const dim3 gfix((unsigned)(L.crows / 64), (unsigned)((L.ldp + 63) / 64));
+  const dim3 gprep((unsigned)(L.crows / 64), (unsigned)((D + 63) / 64));
   for (int64_t c = 0; c < L.nch; ++c) {
     const int64_t j0 = c * L.crows;
     const gemm::TpJobs &tj = c == 0 ? tp : none;
     const unsigned grid = glog + (unsigned)tj.n;
     if (vk && sb)
       ce_logits_kernel<C, true, true><<<grid, C::NT, 0, s>>>(
-          W, Hc, V, D, j0, L.crows, S.n, tcol, stats, tgt, S.P, L.ldp, L.vtiles, L.ttiles, tj);
+          W, Hc, V, D, j0, L.crows, S.n, tcol, mref, stats, tgt, S.P, L.ldp, S.PT, L.crows,
+          L.vtiles, L.ttiles, tj);
     else if (vk)
       ce_logits_kernel<C, true, false><<<grid, C::NT, 0, s>>>(
-          W, Hc, V, D, j0, L.crows, S.n, tcol, stats, tgt, S.P, L.ldp, L.vtiles, L.ttiles, tj);
+          W, Hc, V, D, j0, L.crows, S.n, tcol, mref, stats, tgt, S.P, L.ldp, S.PT, L.crows,
+          L.vtiles, L.ttiles, tj);
     else
       ce_logits_kernel<C, false, false><<<grid, C::NT, 0, s>>>(
-          W, Hc, V, D, j0, L.crows, S.n, tcol, stats, tgt, S.P, L.ldp, L.vtiles, L.ttiles, tj);
+          W, Hc, V, D, j0, L.crows, S.n, tcol, mref, stats, tgt, S.P, L.ldp, S.PT, L.crows,
+          L.vtiles, L.ttiles, tj);
     if ((e = check_launch("ce_logits"))) return e;
-    ce_lse_kernel<<<(unsigned)(L.crows / kLseRows), kLseRows * kLseParts, 0, s>>>(
-        stats, L.ntiles, L.crows, tgt, S.n, j0, lse, loss_row);
+    ce_lse_kernel<TI><<<(unsigned)(L.crows / kLseRows), kLseThreads, 0, s>>>(
+        stats, L.ntiles, L.crows, tgt, S.n, j0, S.inv, tcol, mref, S.cfac, loss_row, S.P, L.ldp,
+        S.PT, L.crows, W, Hc, D, V);
     if ((e = check_launch("ce_lse"))) return e;
-    const bool last = c + 1 == L.nch;  // the mean loss comes with the last chunk's fix-up
-    ce_fix_kernel<TI><<<gfix, kFixThreads, 0, s>>>(S.P, L.ldp, S.PT, L.crows, V, stats, L.wtm,
-                                                   lse, tcol, S.n, j0, S.inv, loss_row,
-                                                   last ? loss : nullptr);
-    if ((e = check_launch("ce_fix"))) return e;
+    const bool last = c + 1 == L.nch;  // the mean loss comes with the last chunk's launch
+    if (vec)
+      ce_scale_hct_kernel<TI, true><<<gprep, kPrepThreads, 0, s>>>(
+          Hc, D, S.cfac, S.n, j0, L.crows, S.Hct, L.ldht, loss_row, S.inv, last ? loss : nullptr);
+    else
+      ce_scale_hct_kernel<TI, false><<<gprep, kPrepThreads, 0, s>>>(
+          Hc, D, S.cfac, S.n, j0, L.crows, S.Hct, L.ldht, loss_row, S.inv, last ? loss : nullptr);
+    if ((e = check_launch("ce_scale_hct"))) return e;
     if (!last &&
         (e = launch_grads<TI>(L, S, c, D, V, c > 0 ? S.dWacc : nullptr, S.dWacc, NF_DTYPE_F32,
                               nullptr, part, s)))

@@ -80,7 +80,9 @@ inline bool sb_ok(int64_t bytes) { return bytes < ((int64_t)1 << 31) - 64; }
 // K loop, so the load latency overlaps the first operand copies and the
 // epilogue only stores.  C has element type cdt (fp32, bf16 or fp16: the
 // last product of a gradient goes straight to the caller's type) and
-// scale, when given, is a device fp32 scalar (the loss's grad_output).
+// scale, when given, is a device fp32 scalar (the loss's grad_output), and
+// row_scale a device fp32 vector over the rows of C (a per-row factor that
+// could not enter the product: the cross entropy's softmax normaliser).
 // ---------------------------------------------------------------------------
 // A job with ksplit > 1 divides K into slices of kslice (a multiple of the
 // stage width): block (tile, s) writes the partial product over slice s to
@@ -99,6 +101,7 @@ struct GemmJob {
   const float *Cin;    // fp32 [M, ldc] added to the product, or null
   void *C;             // [M, ldc] of cdt
   const float *scale;  // device scalar multiplying the result, or null
+  const float *row_scale;  // device fp32 per output row multiplying it, or null
   int64_t lda, ldb, ldc, M, N, K;
   int cdt;       // NF_DTYPE_F32 / BF16 / F16
   int tiles_m;   // tiles along M
@@ -211,20 +214,34 @@ __global__ NF_GEMM_BOUNDS(C) void gemm_store_kernel(GemmJob<typename C::TI> j0,
       }
   gemm::mainloop<C, BUF, false>(j.A + k0, j.lda, j.B + k0, j.ldb, M, N, klen, m0, n0, smem, acc);
   const float g = (!split && j.scale) ? *j.scale : 1.f;
+  // the per-row factor of the lane's 16 rows of MFMA tile i (rows past M: 0)
+  const float *rsc = split ? nullptr : j.row_scale;
+  auto row_factors = [&](int i, float (&f)[16]) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int64_t row = row0 + i * 32 + 8 * (r >> 2) + (r & 3);
+      f[r] = rsc ? (row < M ? rsc[row] * g : 0.f) : g;
+    }
+  };
   if (cdt == NF_DTYPE_F32) {
 #pragma unroll
-    for (int i = 0; i < C::TM; ++i)
+    for (int i = 0; i < C::TM; ++i) {
+      float f[16];
+      row_factors(i, f);
 #pragma unroll
       for (int jj = 0; jj < C::TN; ++jj)
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
           const int dr = i * 32 + 8 * (r >> 2) + (r & 3);
           const bool ok = row0 + dr < M && col0 + jj * 32 < N;
-          out.st32(((row0 + dr) * ldc + col0 + jj * 32) * 4, ok, acc[i][jj][r] * g);
+          out.st32(((row0 + dr) * ldc + col0 + jj * 32) * 4, ok, acc[i][jj][r] * f[r]);
         }
+    }
   } else {
 #pragma unroll
-    for (int i = 0; i < C::TM; ++i)
+    for (int i = 0; i < C::TM; ++i) {
+      float f[16];
+      row_factors(i, f);
 #pragma unroll
       for (int jj = 0; jj < C::TN; ++jj)
 #pragma unroll
@@ -232,20 +249,22 @@ __global__ NF_GEMM_BOUNDS(C) void gemm_store_kernel(GemmJob<typename C::TI> j0,
           const int dr = i * 32 + 8 * (r >> 2) + (r & 3);
           const bool ok = row0 + dr < M && col0 + jj * 32 < N;
           out.st16(((row0 + dr) * ldc + col0 + jj * 32) * 2, ok,
-                   to_half_bits(acc[i][jj][r] * g, cdt));
+                   to_half_bits(acc[i][jj][r] * f[r], cdt));
         }
+    }
   }
 }
 
-// C[m, n] = scale * (Cin[m, n] + sum over s = 0 .. S-1 of part[s, m, n]),
-// the slices added in order; C of element type cdt.  With `dyn`, only the
+// C[m, n] = scale * row_scale[m] * (Cin[m, n] + sum over s = 0 .. S-1 of
+// part[s, m, n]), the slices added in order; C of element type cdt.  With `dyn`, only the
 // first clamp(*dyn - dyn_base, 0, M) rows (the slices keep their M x N size).
 static __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float *__restrict__ part,
                                                             int S, int64_t M, int64_t N,
                                                             const float *Cin, void *C,
                                                             int64_t ldc, int cdt,
-                                                            const float *scale, const int *dyn,
-                                                            int64_t dyn_base) {
+                                                            const float *scale,
+                                                            const float *row_scale,
+                                                            const int *dyn, int64_t dyn_base) {
   const int64_t total = M * N;  // slice stride
   int64_t rows = M;
   if (dyn) {
@@ -269,7 +288,7 @@ static __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float *
     }
     const int64_t o = ldc == N ? i : (i / N) * ldc + i % N;  // dense C skips the division
     if (Cin) a = Cin[o] + a;
-    store_dyn(C, cdt, o, a * g);
+    store_dyn(C, cdt, o, a * (row_scale ? row_scale[i / N] * g : g));
   }
 }
 
@@ -441,7 +460,7 @@ GemmJob<typename C::TI> make_job(const typename C::TI *A, int64_t lda, const typ
                                  const float *scale, int64_t ldc, int64_t M, int64_t N,
                                  int64_t K) {
   GemmJob<typename C::TI> j;
-  j.A = A; j.B = B; j.Cin = Cin; j.C = Cout; j.scale = scale;
+  j.A = A; j.B = B; j.Cin = Cin; j.C = Cout; j.scale = scale; j.row_scale = nullptr;
   j.lda = lda; j.ldb = ldb; j.ldc = ldc; j.M = M; j.N = N; j.K = K;
   j.cdt = cdt;
   j.tiles_m = (int)((M + C::BM - 1) / C::BM);
@@ -492,6 +511,7 @@ int launch_gemm_store(const GemmJob<typename C::TI> &j0, const GemmJob<typename 
     if (blocks > 2048) blocks = 2048;
     splitk_reduce_kernel<<<(unsigned)blocks, 256, 0, s>>>(
         jp->part, jp->ksplit, jp->M, jp->N, jp->Cin, jp->C, jp->ldc, jp->cdt, jp->scale,
+        jp->row_scale,
         jp->dyn_rows ? jp->dyn : nullptr, jp->dyn_base);
     if (int e = check_launch("splitk_reduce")) return e;
   }

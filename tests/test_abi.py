@@ -189,16 +189,16 @@ def _ceil(a: int, b: int) -> int:
 
 def _ce_state_closed_form(m, d, v, chunk_rows, es=2):
     """The state nf_ce_fwd leaves for nf_ce_bwd, term by term (each buffer
-    256-byte aligned): scalars, pos [M], W^T [D, V8], Hc^T [D, M8], one chunk's
-    P [C, V8] and PT [V, C], fp32 dH rows [M, D], and the fp32 dW accumulator
-    when more than one chunk (C = chunk_rows rounded up to 256, at most M
-    rounded up to 256)."""
+    256-byte aligned): scalars, pos [M], the fp32 row factors [M], W^T
+    [D, V8], the scaled Hc^T [D, M8], one chunk's E [C, V8] and E^T [V, C],
+    fp32 dH rows [M, D], and the fp32 dW accumulator when more than one chunk
+    (C = chunk_rows rounded up to 256, at most M rounded up to 256)."""
     a = lambda x: _ceil(x, 256) * 256  # noqa: E731
     c = min(_ceil(chunk_rows, 256) * 256, _ceil(m, 256) * 256)
     v8, m8 = _ceil(v, 8) * 8, _ceil(m, 8) * 8
     nch = _ceil(m, c)
-    return (a(64) + a(4 * m) + a(es * d * v8) + a(es * d * m8) + a(es * c * v8) + a(es * v * c)
-            + a(4 * m * d) + (a(4 * v * d) if nch > 1 else 0))
+    return (a(64) + a(4 * m) + a(4 * m) + a(es * d * v8) + a(es * d * m8) + a(es * c * v8)
+            + a(es * v * c) + a(4 * m * d) + (a(4 * v * d) if nch > 1 else 0))
 
 
 def sb_at(L, chunk_rows):

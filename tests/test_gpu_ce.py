@@ -135,6 +135,38 @@ def test_ce_all_ignored_is_zero(cuda):
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("chunk", [64, 4096])
+def test_ce_rows_far_from_their_reference(cuda, dtype, chunk):
+    """Logits of standard deviation ~32 in every other row (hidden rows
+    N(0, 1) x 4, weights N(0, 1)), so that in about a third of the rows the
+    largest logit lies more than 75 above the target logit: E is stored relative to
+    the target logit, and those rows leave its exponent range and go through
+    the exact recomputation; the others keep the fast path.  Against the fp64
+    oracle on the same rounded inputs.  Tolerances: bf16 2e-2; fp32 1e-4,
+    because an fp32 logit of magnitude ~100 carries an absolute rounding
+    error of ~1e-5, which exp turns into a relative error of the same size in
+    every probability (the fp64 oracle has none)."""
+    note(f"ce far-from-reference rows dtype={dtype} chunk={chunk}")
+    m, d, v = 300, 64, 1000
+    g = gen(21)
+    hid = randn((m, d), g, torch.float32, "cpu")
+    hid[::2] *= 4.0
+    w = randn((v, d), g, torch.float32, "cpu")
+    tgt = torch.randint(0, v, (m,), generator=g)
+    tgt[::7] = -100
+    hid, w, tgt = hid.to(dtype).to(cuda), w.to(dtype).to(cuda), tgt.to(cuda)
+    logits = np64(hid) @ np64(w).T
+    valid = (tgt != -100).cpu().numpy()
+    tcol = np.where(valid, tgt.cpu().numpy(), 0)
+    gap = logits.max(axis=1) - logits[np.arange(m), tcol]
+    assert (gap[valid] > 80).sum() >= 0.3 * valid.sum()  # the recomputation is exercised
+    assert (gap[valid] < 70).sum() >= 0.2 * valid.sum()  # and so is the fast path
+    loss, dh, dw = _run_ce(hid, w, tgt, chunk)
+    tol = 2e-2 if dtype == torch.bfloat16 else 1e-4
+    _check_ce(hid, w, tgt, loss, dh, dw, tol, f"far rows {dtype} chunk {chunk}")
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("m,d,v,chunk", [(17, 36, 333, 7), (300, 40, 1030, 1000), (9, 4, 6, 1),
                                          (130, 264, 129, 64)])
 def test_ce_ragged_shapes(cuda, dtype, m, d, v, chunk):
