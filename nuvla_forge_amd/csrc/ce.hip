@@ -358,20 +358,31 @@ __global__ NF_GEMM_BOUNDS(C) void ce_logits_kernel(
       const int64_t tok = t0 + t, c = v0 + c8;
       eout.st128((tok * ldp + c) * ES, tok < cnt && c < ldp, v);
     }
-    // E^T: a half-wave stores one vocabulary row's 256 tokens (32 vectors of
-    // 8 tokens, each gathered from 8 tile rows); tokens past the chunk's
-    // rows are zero up to cnt8 (the dW product's K padding), none beyond
+    // E^T through transposing LDS reads (ds_read_b64_tr_b16: in each 16-lane
+    // group, lane i receives element i % 4 of the 8-byte chunks addressed by
+    // lanes i / 4 + 4 q, q = 0..3).  Lane j of a group addresses token row
+    // T + 8 (j % 4) + j / 4 (+ 4 for the second read) at tile columns c0 ..
+    // c0 + 3, so lane i gets tokens T + 8 (i / 4) .. + 7 of column c0 + i % 4:
+    // one 16-byte E^T vector.  A wavefront covers 16 columns x 32 tokens per
+    // step, wavefront w columns 32 w .. 32 w + 31; tokens past the chunk's
+    // rows are zero up to cnt8 (the dW product's K padding), none beyond.
+    typedef short v4s __attribute__((ext_vector_type(4)));
+    const int grp = l >> 4, j = l & 15;
 #pragma unroll 2
-    for (int it = 0; it < 16; ++it) {
-      const int idx = it * C::NT + (int)threadIdx.x;
-      const int tv = idx & 31, c = idx >> 5;  // token vector, tile column
-      const int64_t v = v0 + c, tok = t0 + 8 * tv;
+    for (int k = 0; k < 16; ++k) {
+      const int C0 = 32 * w + 16 * (k >> 3), T = 32 * (k & 7);
+      const int c0 = C0 + 4 * grp;
+      const int ra = T + 8 * (j & 3) + (j >> 2), rb = ra + 4;
+      const v4s a = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+          (__attribute__((address_space(3))) v4s *)(smem + ra * 512 + 2 * (c0 ^ e_swz(ra))));
+      const v4s b = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+          (__attribute__((address_space(3))) v4s *)(smem + rb * 512 + 2 * (c0 ^ e_swz(rb))));
+      const int64_t v = v0 + c0 + (j & 3), tok = t0 + T + 8 * (j >> 2);
       uint16_t e[8];
 #pragma unroll
-      for (int q = 0; q < 8; ++q) {
-        const int t = 8 * tv + q;
-        const uint16_t b = *reinterpret_cast<const uint16_t *>(smem + t * 512 + 2 * (c ^ e_swz(t)));
-        e[q] = tok + q < cnt ? b : (uint16_t)0;
+      for (int q = 0; q < 4; ++q) {
+        e[q] = tok + q < cnt ? (uint16_t)a[q] : (uint16_t)0;
+        e[4 + q] = tok + 4 + q < cnt ? (uint16_t)b[q] : (uint16_t)0;
       }
       u32x4 pk;
       __builtin_memcpy(&pk, e, 16);
