@@ -209,9 +209,11 @@ int nf_adaln_bwd_noalloc(const void *dh_up, const void *dout, const void *x,
  * nf_ce_fwd computes the loss and fills `state` (nf_ce_state_bytes, 16-byte
  * aligned), which the caller keeps for nf_ce_bwd; `workspace`
  * (nf_ce_fwd_workspace) is scratch for the call.  The valid rows are taken
- * `chunk_rows` at a time (rounded up to 256): a chunk's logits become
- * (softmax - onehot) * inv in place in the input type, so memory is
- * O(chunk_rows * V), not O(M * V), as the reference's row chunks
+ * `chunk_rows` at a time (rounded up to 256): a chunk's logits are held as
+ * exp(logit - the row's target logit) in the input type, in both layouts the
+ * gradient products read, with the target entry carrying the one-hot term
+ * and a per-row fp32 factor making them (softmax - onehot) * inv, so memory
+ * is O(chunk_rows * V), not O(M * V), as the reference's row chunks
  * (chunk_size) are; results do not depend on chunk_rows beyond fp rounding.
  * The forward also runs the gradient products of every chunk but the last
  * (into fp32 accumulators in `state`).  Replaces _ChunkedCrossEntropy.forward

@@ -9,9 +9,11 @@ ignore_index=-100, force_reference=False)`` (chunked_ce.py:185-208).
 
 The device path is two calls.  ``nf_ce_fwd`` compacts the valid rows on the
 device and, ``chunk_size`` of them at a time, forms their logits once on
-bf16 (or fp32) MFMA, turns them into ``(softmax - onehot) / n`` in place
-(fp32 log-sum-exp from per-tile statistics), and runs the gradient products
-of every chunk but the last; the loss comes out.  ``nf_ce_bwd`` runs the last
+bf16 (or fp32) MFMA and keeps them as ``exp(logit - target logit)`` in both
+layouts the gradient products read, with a per-row factor (from an fp32
+log-sum-exp over per-tile statistics) that makes them ``(softmax - onehot) /
+n``; it runs the gradient products of every chunk but the last, and the loss
+comes out.  ``nf_ce_bwd`` runs the last
 chunk's products with ``grad_output`` known and writes both gradients scaled,
 in each input's dtype.  The reference forms fp32 gradients in the forward
 pass and scales and casts them in the backward; the results are the same.
