@@ -600,8 +600,8 @@ struct Plan {
 // are half those of 512 blocks.  bf16 [8192, 1024]: 18.8 us for RB = 4 with
 // 32 blocks per sample against 19.4 us for RB = 1 with 64.
 constexpr int kBwdBlocksTarget = 256;
-// adaln_reduce_kernel stages at most 1024 partial rows of whole samples per
-// round, so one sample may contribute at most 1024 of them.
+// A cap on the blocks (and so the partial rows) per sample: past it more
+// blocks only add partial rows for the reduction to read.
 constexpr int kMaxBlocksPerSample = 1024;
 constexpr int kFwdGroupsTarget = 2048;
 constexpr int kFwdMaxRowsPerGroup = 8;
