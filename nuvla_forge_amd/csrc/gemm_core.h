@@ -440,8 +440,11 @@ __device__ __forceinline__ void mainloop_dtl_ops(const DtlOperand<C, C::ACW> &op
     // buffer kt % STAGES is refilled with stage kt + STAGES right after the
     // barrier that follows the last read of stage kt.  The operands of the
     // KG k-groups of a stage alternate between two register sets, each read
-    // from LDS while the MFMAs of the other run; the last k-group's MFMAs
-    // cover the wait for the next stage and the read of its k-group 0.
+    // from LDS while the MFMAs of the other run.  The last k-group's MFMAs go
+    // out before the wait for the next stage, so the matrix pipe has work
+    // queued while the wavefront waits at the barrier (measured against
+    // issuing them after the hand-over: +1% on 8192^3 and the cross-entropy
+    // products, cfg4 fwd+bwd 1.456-1.463 against 1.465-1.478 ms).
 #pragma unroll
     for (int s = 0; s < C::STAGES; ++s)
       if (s < nk) {
@@ -468,7 +471,8 @@ __device__ __forceinline__ void mainloop_dtl_ops(const DtlOperand<C, C::ACW> &op
           interleave_hint<C>();
         }
       }
-      // the last k-group (in a1, b1) covers the stage hand-over
+      mfma_block<C>(a1, b1, acc);  // the last k-group, then the hand-over
+      interleave_hint<C>();
       if (kt + 1 < nk) {
         if constexpr (C::STAGES == 2) {
           // stage kt + 1 is the only one in flight: wait for all of it
@@ -485,8 +489,6 @@ __device__ __forceinline__ void mainloop_dtl_ops(const DtlOperand<C, C::ACW> &op
         cur = cur + 1 == C::STAGES ? 0 : cur + 1;
         read_kgroup_dtl<C>(smem + cur * C::STAGE, wm, wn, 0, a0, b0);
       }
-      mfma_block<C>(a1, b1, acc);
-      interleave_hint<C>();
     }
   } else {
     for (int64_t kt = 0; kt < nk; ++kt) {
