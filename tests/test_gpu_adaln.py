@@ -187,6 +187,30 @@ def test_missing_upstream_gradient(cuda, which):
             assert on.rel_err(np64(got), want) < 1e-5, k
 
 
+@pytest.mark.parametrize("want", [("weight",), ("gate", "shift"), ("scale",),
+                                  ("x", "y"), ("gate", "weight", "scale", "shift")])
+@pytest.mark.parametrize("b,t,n", [(8, 64, 1024), (2, 16, 333), (40, 3, 256)])
+def test_only_some_parameter_gradients(cuda, want, b, t, n):
+    """Leaves that do not require grad get no reduction output: the partial
+    reduction runs without its dweight blocks, or without its dgate / dshift /
+    dscale blocks, and the requested sums are unchanged."""
+    note(f"adaln grads {want} b={b} t={t} n={n}")
+    inp = _inputs(b, t, n, torch.float32, cuda, seed=5)
+    leaves = {k: v.detach().requires_grad_(k in want) for k, v in inp.items()}
+    h, out = fused_adaln_residual_rmsnorm(**leaves, tokens_per_sample=t)
+    dh, dout = _upstream(b * t, n, torch.float32, cuda, seed=6)
+    torch.autograd.backward([h, out], [dh, dout])
+    torch.cuda.synchronize()
+    a = {k: np64(v) for k, v in inp.items()}
+    gw = on.adaln_backward(**a, t=t, dh_up=np64(dh), dout=np64(dout))
+    for k in NAMES:
+        got = leaves[k].grad
+        if k not in want:
+            assert got is None, k
+        else:
+            assert on.rel_err(np64(got), gw[k]) < 1e-5, (k, on.rel_err(np64(got), gw[k]))
+
+
 def test_zero_gate_keeps_residual_exact(cuda):
     note("adaln zero gate")
     b, t, n = 2, 16, 1024
