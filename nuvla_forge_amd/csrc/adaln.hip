@@ -35,10 +35,9 @@ struct ReduceArgs {
   int64_t ld_scale;
   int N, J, B;
   int dt_weight, dt_scale, dt_gate, dt_shift;
-  int slices;     // 32-column slices
   int ublocks;    // dgate/dshift/dscale blocks per sample: ceil(3N / 256)
   int gps_w;      // dweight blocks: row groups per sample (a power of two <= 32)
-  int dw_blocks;  // dweight blocks (slices, or 0 without dweight)
+  int dw_blocks;  // dweight blocks: one per 32-column slice, or 0 without dweight
 };
 
 constexpr int kRcLanes = 8;                    // 16-byte lanes per slice row
@@ -377,7 +376,7 @@ extern "C" int nf_adaln_bwd_reduce(void *workspace,
   if (grid > INT32_MAX) return set_error(NF_ERR_ARG, "nf_adaln_bwd_reduce: too many blocks");
   ReduceArgs r{static_cast<const float *>(workspace), weight, scale, dgate, dscale, dshift,
                dweight, ld_scale, (int)N, J, B, dt_weight, dt_scale, dt_gate, dt_shift,
-               slices, ublocks, gps_w, dw_blocks};
+               ublocks, gps_w, dw_blocks};
   hipStream_t s = static_cast<hipStream_t>(stream);
   const bool vec = N % 4 == 0 && (M == 0 || aligned16(workspace));
   if (vec)

@@ -1,0 +1,152 @@
+"""Seeded random shapes and dtypes for every fused op against the oracle (GPU).
+
+Each case draws its shape, element types and data from its seed (the test id
+names the seed, so a failure names its case), sized so that the fp64 oracle
+finishes in well under a second:
+
+* adaLN: B in 1..40, T in 1..300, N in 1..5000 (odd N included), fp32 / bf16 /
+  fp16 activations, conditioning and weight sometimes fp32 beside 16-bit
+  activations (the autocast mix), dh_up and dout both present;
+* SwiGLU: 1..3 dims, up to ~1.5 M elements, fp32 / bf16 / fp16;
+* chunked CE: M in 1..700, D in 1..320, V in 2..3000, chunk_size in 1..800,
+  a random fraction of ignored rows (all of them now and then), weight scale
+  0.02..1, fp32 / bf16;
+* SwiGLU in the gate/up GEMM: M in 1..600, D in 8..320, H in 1..700, bf16.
+
+Tolerances are BASELINE's (fp32 1e-5, 16-bit 2e-2 norm-wise against the
+fp64 oracle on the same rounded inputs), except CE in fp32 at 1e-4 when the
+weight scale makes logits of magnitude ~30 or more possible (an fp32 logit
+that large carries ~1e-5 absolute rounding error, which exp turns into the
+same relative error in every probability).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from nuvla_forge_amd.kernels import (chunked_cross_entropy, fused_adaln_residual_rmsnorm,
+                                     fused_gate_up_swiglu, fused_swiglu)
+from oracle import numerics as on
+from tests.helpers import TOL, gen, note, np64, randn
+
+pytestmark = pytest.mark.gpu
+
+DT = [torch.float32, torch.bfloat16, torch.float16]
+
+
+def _pick(rng, seq):
+    return seq[int(rng.integers(len(seq)))]
+
+
+@pytest.mark.parametrize("seed", range(16))
+def test_adaln_random(cuda, seed):
+    rng = np.random.default_rng(1000 + seed)
+    b = int(rng.integers(1, 41))
+    t = int(rng.integers(1, 301))
+    n = int(rng.integers(1, 5001))
+    while b * t * n > 1_500_000:
+        t = max(1, t // 2)
+        n = max(1, n // 2) if b * t * n > 1_500_000 else n
+    dt = _pick(rng, DT)
+    cdt = torch.float32 if (dt != torch.float32 and rng.random() < 0.4) else dt
+    note(f"adaln random seed={seed} b={b} t={t} n={n} dt={dt} cond={cdt}")
+    g = gen(seed)
+    inp = {"x": randn((b * t, n), g, dt, cuda), "y": randn((b * t, n), g, dt, cuda),
+           "gate": randn((b, n), g, cdt, cuda, std=0.1),
+           "weight": randn((n,), g, cdt, cuda, std=0.02, mean=1.0),
+           "scale": randn((b, n), g, cdt, cuda, std=0.1),
+           "shift": randn((b, n), g, cdt, cuda, std=0.1)}
+    dh, dout = randn((b * t, n), g, dt, cuda), randn((b * t, n), g, dt, cuda)
+    leaves = {k: v.detach().requires_grad_(True) for k, v in inp.items()}
+    h, out = fused_adaln_residual_rmsnorm(**leaves, tokens_per_sample=t)
+    torch.autograd.backward([h, out], [dh, dout])
+    torch.cuda.synchronize()
+    a = {k: np64(v) for k, v in inp.items()}
+    hw, ow, _ = on.adaln_forward(**a, t=t)
+    gw = on.adaln_backward(**a, t=t, dh_up=np64(dh), dout=np64(dout))
+    tol = TOL[dt]
+    errs = {"h": on.rel_err(np64(h), hw), "out": on.rel_err(np64(out), ow)}
+    errs.update({"d" + k: on.rel_err(np64(leaves[k].grad), gw[k]) for k in inp})
+    bad = {k: v for k, v in errs.items() if not v <= tol}
+    assert not bad, bad
+
+
+@pytest.mark.parametrize("seed", range(8))
+def test_swiglu_random(cuda, seed):
+    rng = np.random.default_rng(2000 + seed)
+    ndim = int(rng.integers(1, 4))
+    shape = tuple(int(rng.integers(1, 120 if ndim > 1 else 1_500_000)) for _ in range(ndim))
+    dt = _pick(rng, DT)
+    note(f"swiglu random seed={seed} shape={shape} dt={dt}")
+    g = gen(seed)
+    a, b, dout = (randn(shape, g, dt, cuda) for _ in range(3))
+    la, lb = a.detach().requires_grad_(True), b.detach().requires_grad_(True)
+    out = fused_swiglu(la, lb)
+    out.backward(dout)
+    torch.cuda.synchronize()
+    A, B, G = np64(a), np64(b), np64(dout)
+    da, db = on.swiglu_backward(A, B, G)
+    for name, got, want in (("out", out, on.swiglu_forward(A, B)), ("da", la.grad, da),
+                            ("db", lb.grad, db)):
+        err = on.rel_err(np64(got), want)
+        assert err <= TOL[dt], (name, err)
+
+
+@pytest.mark.parametrize("seed", range(16))
+def test_ce_random(cuda, seed):
+    rng = np.random.default_rng(3000 + seed)
+    m = int(rng.integers(1, 701))
+    d = int(rng.integers(1, 321))
+    v = int(rng.integers(2, 3001))
+    chunk = int(rng.integers(1, 801))
+    frac = 1.0 if rng.random() < 0.1 else float(rng.random()) * 0.5
+    w_std = float(np.exp(rng.uniform(np.log(0.02), 0.0)))
+    dt = _pick(rng, DT[:2])
+    note(f"ce random seed={seed} m={m} d={d} v={v} chunk={chunk} ignore={frac:.2f} "
+         f"w_std={w_std:.3f} dt={dt}")
+    g = gen(seed)
+    hid = randn((m, d), g, dt, cuda)
+    w = randn((v, d), g, dt, cuda, std=w_std)
+    tgt = torch.randint(0, v, (m,), generator=g)
+    tgt[torch.rand(m, generator=g) < frac] = -100
+    tgt = tgt.to(cuda)
+    lh, lw = hid.detach().requires_grad_(True), w.detach().requires_grad_(True)
+    loss = chunked_cross_entropy(lh, lw, tgt, chunk_size=chunk)
+    loss.backward()
+    torch.cuda.synchronize()
+    lo, dho, dwo = on.ce_forward_backward(np64(hid), np64(w), tgt.cpu().numpy())
+    big = float(np.abs(np64(hid) @ np64(w).T).max(initial=0.0)) > 30.0
+    tol = TOL[dt] if dt != torch.float32 or not big else 1e-4
+    errs = {"loss": abs(float(loss) - lo) / max(abs(lo), 1e-30) if lo else abs(float(loss)),
+            "dh": on.rel_err(np64(lh.grad), dho), "dw": on.rel_err(np64(lw.grad), dwo)}
+    bad = {k: e for k, e in errs.items() if not e <= tol}
+    assert not bad, bad
+    if frac == 1.0:
+        assert float(loss) == 0.0 and not lh.grad.any() and not lw.grad.any()
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_gate_up_swiglu_random(cuda, seed):
+    rng = np.random.default_rng(4000 + seed)
+    m = int(rng.integers(1, 601))
+    d = int(rng.integers(8, 321))
+    h = int(rng.integers(1, 701))
+    note(f"gemm swiglu random seed={seed} m={m} d={d} h={h}")
+    g = gen(seed)
+    x = randn((m, d), g, torch.bfloat16, cuda)
+    wg = randn((h, d), g, torch.bfloat16, cuda, std=d ** -0.5)
+    wu = randn((h, d), g, torch.bfloat16, cuda, std=d ** -0.5)
+    dact = randn((m, h), g, torch.bfloat16, cuda)
+    leaves = [t.detach().requires_grad_(True) for t in (x, wg, wu)]
+    act = fused_gate_up_swiglu(*leaves)
+    act.backward(dact)
+    torch.cuda.synchronize()
+    X, WG, WU, DA = np64(x), np64(wg), np64(wu), np64(dact)
+    a, b = X @ WG.T, X @ WU.T
+    da, db = on.swiglu_backward(a, b, DA)
+    want = (on.swiglu_forward(a, b), da @ WG + db @ WU, da.T @ X, db.T @ X)
+    got = (act, leaves[0].grad, leaves[1].grad, leaves[2].grad)
+    errs = {k: on.rel_err(np64(gv), wv) for k, gv, wv in zip(("act", "dx", "dwg", "dwu"), got, want)}
+    assert all(e <= 2e-2 for e in errs.values()), errs
