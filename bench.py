@@ -273,6 +273,9 @@ def bench_adaln(args, dev):
     # per-kernel durations: back-to-back launches of each C-ABI entry point
     kern_ms = adaln_kernel_ms(inp, t, dh, dout, args.steps)
     instep_ms = adaln_in_step_ms(inp, t, dh, dout, args.steps)
+    # the streaming probe on the same bytes, same box, same run: forward
+    # 2 reads + 2 writes, backward 4 + 2 of [8192, 1024] bf16 arrays
+    probe = stream_ceilings(args, dev, (("cfg2", m * n * 2),))
 
     alg = adaln_alg_bytes(b, t, n)
     bwd_alg = (6 * m * n + 2 * b * n + n) * 2
@@ -287,6 +290,7 @@ def bench_adaln(args, dev):
         "bwd_gbs_in_step": bwd_alg / (instep_ms["nf_adaln_bwd"] * 1e-3) / 1e9,
         "gbs": alg / (graph_ms * 1e-3) / 1e9, "gbs_eager": alg / (eager_ms * 1e-3) / 1e9,
         "ref_style_gbs_11MNe": 11 * m * n * 2 / (graph_ms * 1e-3) / 1e9,
+        "stream_probe": probe,
     }
 
 
@@ -342,6 +346,47 @@ def bench_copy(args, dev):
             out[label][name] = {"us": ms * 1e3, "gbs": nbytes / (ms * 1e-3) / 1e9,
                                 "frac_of_8tbs": nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS}
         del a, b, c, d
+    out["stream_probe"] = stream_ceilings(args, dev)
+    return out
+
+
+def stream_ceilings(args, dev, sizes=(("cfg2_16MiB", 16 << 20), ("cfg5_256MiB", 256 << 20))):
+    """`nf_stream_probe` (a grid-stride streaming kernel with no dependency
+    between its accesses, non-temporal stores) on the adaLN step's traffic
+    shapes -- forward 2 reads + 2 writes, backward 4 reads + 2 writes -- with
+    arrays of the cfg2 activation size (16 MiB) and of the cfg5 adaLN size
+    (256 MiB): microseconds per launch back to back on one set of arrays
+    (`same`: inputs partly warm in the L2s) and alternating between two sets
+    (`alt`: each launch finds the other set's data in the L2s, the cache state
+    the row kernels meet inside a step).  Context, never the denominator."""
+    import torch
+
+    from nuvla_forge_amd import _lib
+
+    L = _lib.lib()
+    out = {}
+    for label, nbytes in sizes:
+        for r, w in ((2, 2), (4, 2)):
+            sets = [[torch.empty(nbytes, dtype=torch.uint8, device=dev) for _ in range(r + w)]
+                    for _ in range(2)]
+            for t in sets[0] + sets[1]:
+                t.random_(0, 256)
+
+            def launch(k):
+                ins, outs = sets[k][:r], sets[k][r:]
+                ptrs = [t.data_ptr() for t in ins] + [None] * (4 - r)
+                ptrs += [t.data_ptr() for t in outs] + [None] * (2 - w)
+                _lib.check(L.nf_stream_probe(r, w, *ptrs, nbytes // 16, _lib.stream_of(ins[0])),
+                           "nf_stream_probe")
+
+            steps = max(5, args.steps // 5)
+            same = per_launch_ms(lambda: launch(0), steps)
+            alt = per_launch_ms(lambda: (launch(0), launch(1)), steps, 10) / 2
+            moved = (r + w) * nbytes
+            out[f"{label}_{r}r{w}w"] = {
+                "bytes": moved, "same_us": same * 1e3, "same_gbs": moved / (same * 1e-3) / 1e9,
+                "alt_us": alt * 1e3, "alt_gbs": moved / (alt * 1e-3) / 1e9}
+            del sets
     return out
 
 
@@ -734,6 +779,24 @@ def main() -> int:
             "in_step_kernel_ms": {k: round(v, 5) for k, v in ad["in_step_ms"].items()},
             "fwd_kernel_gbs": round(ad["fwd_gbs"], 1),
             "ref_style_gbs_11MNe": round(ad["ref_style_gbs_11MNe"], 1),
+            # context, not the roofline: each row kernel against nf_stream_probe
+            # moving the same array shapes with no dependencies, back to back
+            # ('same') and with the L2s holding other data ('alt', as inside
+            # the step); fractions are probe time / kernel time
+            "stream_probe_ms": {
+                "fwd_2r2w": {"same": round(ad["stream_probe"]["cfg2_2r2w"]["same_us"] / 1e3, 5),
+                             "alt": round(ad["stream_probe"]["cfg2_2r2w"]["alt_us"] / 1e3, 5)},
+                "bwd_4r2w": {"same": round(ad["stream_probe"]["cfg2_4r2w"]["same_us"] / 1e3, 5),
+                             "alt": round(ad["stream_probe"]["cfg2_4r2w"]["alt_us"] / 1e3, 5)}},
+            "frac_of_stream_probe": {
+                "fwd_back_to_back": round(ad["stream_probe"]["cfg2_2r2w"]["same_us"] / 1e3
+                                          / ad["kernel_ms"]["nf_adaln_fwd"], 3),
+                "fwd_in_step": round(ad["stream_probe"]["cfg2_2r2w"]["alt_us"] / 1e3
+                                     / ad["in_step_ms"]["nf_adaln_fwd"], 3),
+                "bwd_back_to_back": round(ad["stream_probe"]["cfg2_4r2w"]["same_us"] / 1e3
+                                          / ad["kernel_ms"]["nf_adaln_bwd"], 3),
+                "bwd_in_step": round(ad["stream_probe"]["cfg2_4r2w"]["alt_us"] / 1e3
+                                     / ad["in_step_ms"]["nf_adaln_bwd"], 3)},
         },
         "roofline": {
             "kernel": "adaln_bwd_kernel (nf_adaln_bwd)",

@@ -263,6 +263,18 @@ int nf_gemm_nt(const void *A, int64_t lda, const void *B, int64_t ldb,
                float *C, int64_t ldc, int64_t M, int64_t N, int64_t K,
                int dtype, void *stream);
 
+/* ------------------------------------------------------------------------
+ * Measurement aid with no counterpart in the reference: the streaming
+ * ceiling bench.py sets the row kernels against.  Reads `reads` arrays
+ * (in0..in3) and writes `writes` arrays (out0, out1) of n16 16-byte vectors
+ * each, (reads, writes) one of (1, 1), (2, 2), (4, 2); out_w[i] = (in0[i]
+ * xor ... xor in_{reads-1}[i]) + w in every 32-bit lane.  Pointers unused by
+ * the (reads, writes) pair may be null; the others must be 16-byte aligned.
+ * ---------------------------------------------------------------------- */
+int nf_stream_probe(int reads, int writes, const void *in0, const void *in1,
+                    const void *in2, const void *in3, void *out0, void *out1,
+                    int64_t n16, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

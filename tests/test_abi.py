@@ -259,6 +259,21 @@ def test_ce_argument_validation():
     assert L.nf_gemm_nt(FAKE, 4, FAKE, 4, FAKE, 2, 2, 2, 8, 1, None) == NF_ERR_ARG  # lda < K
 
 
+def test_stream_probe_argument_validation():
+    """The streaming-ceiling entry point refuses what it cannot run before
+    any launch (no GPU needed); n16 = 0 is a no-op."""
+    L = _lib.lib()
+    ptrs = [FAKE] * 6
+    assert L.nf_stream_probe(3, 1, *ptrs, 16, None) == NF_ERR_ARG and "(3, 1)" in _err()
+    assert L.nf_stream_probe(4, 1, *ptrs, 16, None) == NF_ERR_ARG
+    assert L.nf_stream_probe(2, 2, *ptrs, -1, None) == NF_ERR_ARG and "< 0" in _err()
+    assert L.nf_stream_probe(2, 2, FAKE, None, None, None, FAKE, FAKE, 16, None) == NF_ERR_ARG
+    assert "input 1" in _err()
+    assert L.nf_stream_probe(1, 1, FAKE + 8, None, None, None, FAKE, None, 16,
+                             None) == NF_ERR_ARG and "aligned" in _err()
+    assert L.nf_stream_probe(2, 2, *ptrs, 0, None) == NF_OK
+
+
 def test_chunk_rows_argument():
     assert chunked_ce.chunk_rows_for(1024) == 1024
     assert chunked_ce.chunk_rows_for(7) == 7
