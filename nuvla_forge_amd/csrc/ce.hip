@@ -9,31 +9,36 @@
 // Forward (nf_ce_fwd):
 //   1. ce_compact: the valid rows in order -> rows[], their target columns,
 //      pos[m] (compacted index or -1), n_valid, inv = 1 / max(n_valid, 1).
-//   2. gather: Hc = H[rows] ([M, D], zero past n_valid).  Its transpose Hct
-//      [D, M] and Wt = W^T [D, V] (zero-padded), which make every gradient
-//      operand K-contiguous, are formed by the first logits launch's last
-//      blocks (16-bit inputs) or by transpose launches here (fp32).
+//   2. ce_gather: Hc = H[rows] ([M, D], zero past n_valid) and each valid
+//      row's target logit mref = Hc[r] . W[target], the row's reference.
+//      Wt = W^T [D, V] (zero-padded; the dH product's K-contiguous B
+//      operand) is formed by the first logits launch's last blocks (16-bit
+//      inputs) or by a transpose launch here (fp32).
 //   3. per chunk of `crows` compacted rows:
 //      ce_logits: S = Hc_c W^T tile by tile (formed transposed, W Hc_c^T, so a
 //                 lane holds each token's logits along the vocabulary); per
 //                 (vocabulary tile of WTM rows, token) the max and the sum of
-//                 exp(S - max), the target logit, and E = exp(S - max) in the
-//                 input type, written row-major [crows, ldp];
-//      ce_lse:    lse per row from the tile statistics (fixed order), and the
-//                 row's loss lse - S[target];
-//      ce_fix:    P = inv * (E * exp(max - lse) - onehot) in place, and its
-//                 transpose PT [V, crows]; in the last chunk's launch, also
-//                 the mean loss over the valid rows;
+//                 exp(S - max), the target logit, and E = exp(S - mref) in
+//                 the input type, row-major [crows, ldp] and transposed
+//                 [V, crows];
+//      ce_lse:    lse per row from the tile statistics (fixed order), the
+//                 row's loss lse - S[target], the row factor cfac =
+//                 exp(mref - lse) / n, and the one-hot term folded into E's
+//                 target entry, so cfac * E = (softmax - onehot) / n; rows
+//                 whose maximum lies far above mref are recomputed exactly;
+//      ce_scale_hct: Hct = (cfac * Hc_c)^T, the dW product's B operand; in
+//                 the last chunk's launch, also the mean loss;
 //      gradient products of every chunk but the last (one launch):
-//                 dW_acc (+)= PT_c Hc_c      (fp32 [V, D], K = the chunk's rows)
-//                 dHc_c   = P_c Wt^T         (fp32, K = V, split along K)
+//                 dW_acc (+)= E^T_c Hct_c^T  (fp32 [V, D], K = the chunk's rows)
+//                 dHc_c   = cfac * (E_c Wt^T) (fp32, K = V, split along K)
 // Backward (nf_ce_bwd, with the loss's grad_output g): the last chunk's
-// products, dW = g * (dW_acc + PT H_c) written in dweight's type, and the
+// products, dW = g * (dW_acc + E^T Hct^T) written in dweight's type, and the
 // scatter of dHc back to the hidden rows as g * dH (0 for ignored rows).
 //
-// Memory: the state kept between the calls holds one chunk's P and PT, W^T,
-// Hc^T and the fp32 dH rows, plus the fp32 dW accumulator when there is more
-// than one chunk; the [M, V] logits never exist (unless one chunk covers M).
+// Memory: the state kept between the calls holds one chunk's E in both
+// layouts, W^T, the scaled Hc^T and the fp32 dH rows, plus the fp32 dW
+// accumulator when there is more than one chunk; the [M, V] logits never
+// exist (unless one chunk covers M).
 #include <type_traits>
 
 #include "gemm_store.h"
@@ -199,8 +204,8 @@ __global__ __launch_bounds__(kGatherThreads) void ce_gather_kernel(
 // sum of exp over its WTM vocabulary rows are reductions in registers plus
 // one exchange between the lane halves.  Statistics tile t covers vocabulary
 // rows [t * WTM, (t + 1) * WTM): stats[t * crows + token] = (max, sum
-// exp(S - max)), exact in fp32 whatever mref is.  The target logit comes from
-// the one lane holding it.  E = exp(S - max) * exp(max - mref) goes out
+// exp(S - max)), taken from the sum of E (see the epilogue).  The target
+// logit comes from the one lane holding it.  E = exp(S - mref) goes out
 // row-major [token, ldp] (columns V..ldp zero) and transposed [V, ldet]
 // (tokens past the chunk's rows zero up to a multiple of 8): with 16-bit
 // 256 x 256 tiles through LDS (free once the K loop ends) -- element (t, c)
@@ -211,6 +216,8 @@ __global__ __launch_bounds__(kGatherThreads) void ce_gather_kernel(
 // factor P = inv * exp(mref - lse) (ce_lse_kernel), P * E is the softmax.
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ int e_swz(int t) { return 8 * (((t >> 3) ^ (t & 7)) & 31); }
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kStatsGap = 64.f;  // exp(-64) of a row maximum is below fp32 resolution
 
 // Blocks past the vtiles x ttiles logits tiles run the transpose regions of
 // `tp` (16-bit inputs only): dispatched last, they fill the CUs that the
@@ -273,6 +280,7 @@ __global__ NF_GEMM_BOUNDS(C) void ce_logits_kernel(
   for (int j = 0; j < C::TN; ++j) {
     const int tl = wn * C::WTN + j * 32 + (l & 31);  // token within the tile
     const int64_t tok = t0 + tl;                     // token within the chunk
+    const float mr = tok < cnt ? mref[j0 + tok] : 0.f;  // the row's reference
     float mx = -INFINITY;
 #pragma unroll
     for (int i = 0; i < C::TM; ++i)
@@ -293,22 +301,29 @@ __global__ NF_GEMM_BOUNDS(C) void ce_logits_kernel(
         tgt[tok] = z;
       }
     }
-    // a wavefront with no row inside the vocabulary keeps (-inf, 0) and E = 0
-    const float mt = mx == -INFINITY ? 0.f : mx;
+    // E = exp(S - mref) relative to the row's reference, one FMA and one exp2
+    // per element (rows past V are -inf and give 0).  The tile's statistics
+    // follow from its sum: s = sum exp(S - mx) = exp(mref - mx) * sum E.  A
+    // tile more than kStatsGap below mref keeps s = 1: its share of the row
+    // total, below exp(-kStatsGap) of the row maximum's, is under fp32
+    // resolution.  A row whose maximum lies more than kRefGap above mref
+    // (its E leaves the exponent range, its sums overflow) is recomputed
+    // exactly by the statistics pass; a wavefront with no row inside the
+    // vocabulary keeps (-inf, 0).
+    const float nb = -mr * kLog2e;
 #pragma unroll
     for (int i = 0; i < C::TM; ++i)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) acc[i][j][r] = exp_f32(acc[i][j][r] - mt);
-    float s = 0.f;
+      for (int r = 0; r < 16; ++r)
+        acc[i][j][r] = __builtin_amdgcn_exp2f(__builtin_fmaf(acc[i][j][r], kLog2e, nb));
+    float se = 0.f;
 #pragma unroll
     for (int i = 0; i < C::TM; ++i)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) s += acc[i][j][r];
-    s += __shfl_xor(s, 32);
+      for (int r = 0; r < 16; ++r) se += acc[i][j][r];
+    se += __shfl_xor(se, 32);
+    const float s = mx == -INFINITY ? 0.f : (mr - mx > kStatsGap ? 1.f : se * exp_f32(mr - mx));
     if (half == 0 && tok < cnt) stats[(int64_t)stile * crows + tok] = make_float2(mx, s);
-    // E relative to the row's reference: exp(S - mt) * exp(mt - mref); a
-    // factor that overflows marks a row the statistics pass recomputes
-    const float k = mx == -INFINITY ? 0.f : exp_f32(mx - (tok < cnt ? mref[j0 + tok] : 0.f));
 
 #pragma unroll
     for (int i = 0; i < C::TM; ++i)
@@ -317,7 +332,7 @@ __global__ NF_GEMM_BOUNDS(C) void ce_logits_kernel(
         const int o = i * 32 + 8 * g;  // offset of r = 4g from crow0
         TI ev[4];
 #pragma unroll
-        for (int q = 0; q < 4; ++q) ev[q] = static_cast<TI>(acc[i][j][4 * g + q] * k);
+        for (int q = 0; q < 4; ++q) ev[q] = static_cast<TI>(acc[i][j][4 * g + q]);
         if constexpr (kStaged) {
           const int cl = wm * C::WTM + 4 * half + o;  // tile column (vocabulary)
           u32x2 packed;
@@ -403,9 +418,10 @@ __global__ NF_GEMM_BOUNDS(C) void ce_logits_kernel(
 // the target entry becomes exp(z - mref) - exp(lse - mref), so cfac * E is
 // (softmax - onehot) / n, the gradient of the mean loss by the logits.  A row
 // whose largest logit lies more than kRefGap above mref (its E entries would
-// leave the exponent range) is recomputed exactly by its block: fp32 dot
-// products in a fixed order, E relative to the recomputed row max, written to
-// both layouts.  (The target logit is within kRefGap of the row max for any
+// leave the exponent range and its tile sums overflow) is recomputed exactly
+// by its block: fp32 dot products in a fixed order, the row's max and sum of
+// exponentials (so its lse and loss) from them, E relative to the row max,
+// written to both layouts.  (The target logit is within kRefGap of the row max for any
 // row whose loss is under kRefGap nats.)
 constexpr float kRefGap = 75.f;
 constexpr int kLseRows = 16, kLseParts = 16, kLseThreads = kLseRows * kLseParts;
@@ -418,9 +434,8 @@ __global__ __launch_bounds__(kLseThreads) void ce_lse_kernel(
     TI *PT, int64_t ldet, const TI *__restrict__ W, const TI *__restrict__ Hc, int64_t D,
     int64_t V) {
   __shared__ float2 part[kLseParts][kLseRows];
-  __shared__ float lse_s[kLseRows];
   __shared__ int redo[kLseRows];
-  __shared__ float red[kLseThreads / 64];
+  __shared__ float2 red[kLseThreads / 64];
   const int64_t cnt = chunk_count(n_ptr, j0, crows);
   const int rl = threadIdx.x % kLseRows, q = threadIdx.x / kLseRows;
   const int64_t row = (int64_t)blockIdx.x * kLseRows + rl;
@@ -449,8 +464,7 @@ __global__ __launch_bounds__(kLseThreads) void ce_lse_kernel(
       for (int k = 1; k < kLseParts; ++k) a = combine_stats(a, part[k][rl]);
       const float ls = a.x + log_f32(a.y);
       const float z = tgt[row];
-      loss_row[j0 + row] = ls - z;
-      lse_s[rl] = ls;
+      loss_row[j0 + row] = ls - z;  // rewritten below for a recomputed row
       const float m = mref[j0 + row];
       again = !(a.x - m <= kRefGap);  // also for a NaN / inf row
       if (!again) {
@@ -476,15 +490,31 @@ __global__ __launch_bounds__(kLseThreads) void ce_lse_kernel(
       for (int64_t d = 0; d < D; ++d) s += static_cast<float>(h[d]) * static_cast<float>(w[d]);
       return s;
     };
-    float mx = -INFINITY;
-    for (int64_t v = threadIdx.x; v < V; v += kLseThreads) mx = fmaxf(mx, logit(v));
-    mx = wave_max(mx);
-    if (lane == 0) red[wv] = mx;
+    // the row's maximum and sum of exponentials: each thread keeps a running
+    // (max, sum) over its logits, a fixed butterfly combines the wavefront's
+    // lanes (every lane ends with the same pair) and the wavefronts are
+    // combined in order (the tile statistics of such a row overflowed)
+    float2 st = make_float2(-INFINITY, 0.f);
+    for (int64_t v = threadIdx.x; v < V; v += kLseThreads) {
+      const float x = logit(v);
+      if (x > st.x) {
+        st.y = st.y * exp_f32(st.x - x) + 1.f;
+        st.x = x;
+      } else {
+        st.y += exp_f32(x - st.x);
+      }
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1)
+      st = combine_stats(st, make_float2(__shfl_xor(st.x, off), __shfl_xor(st.y, off)));
+    if (lane == 0) red[wv] = st;
     __syncthreads();
-    mx = red[0];
-    for (int u = 1; u < kLseThreads / 64; ++u) mx = fmaxf(mx, red[u]);
+    st = red[0];
+    for (int u = 1; u < kLseThreads / 64; ++u) st = combine_stats(st, red[u]);
     __syncthreads();
-    const float ls = lse_s[k];
+    const float mx = st.x;
+    const float ls = st.x + log_f32(st.y);
+    if (threadIdx.x == 0) loss_row[j0 + r] = ls - tgt[r];
     const int64_t tc = tcol[j0 + r];
     for (int64_t v = threadIdx.x; v < ldp; v += kLseThreads) {
       float e = 0.f;
