@@ -772,9 +772,10 @@ struct StateView {
         dWacc(reinterpret_cast<float *>(s + L.s_dwacc)) {}
 };
 
-// The gradient products of chunk c in one launch: dW (+)= PT_c Hct_c^T (Hct
-// holding the chunk's rows already times their factor cfac) and dHc_c =
-// cfac_c * (P_c Wt^T) (the factor per output row, split along K).  dW goes
+// The gradient products of chunk c in one launch: dW (+)= E^T_c Hct_c^T (E^T
+// in the PT buffer; Hct holding the chunk's rows already times their factor
+// cfac) and dHc_c = cfac_c * (E_c Wt^T) (E in the P buffer; the factor per
+// output row, split along K).  dW goes
 // to `dw_out` (type dt_w, scaled by g when given) on top of `dw_in` when
 // given.
 template <typename TI>
