@@ -346,7 +346,8 @@ extern "C" int nf_adaln_bwd_reduce(void *workspace,
                                    void *stream) {
   if (int e = check_shape("nf_adaln_bwd_reduce", M, N, T)) return e;
   if (!dgate && !dscale && !dshift && !dweight) return NF_OK;
-  if (!weight || !scale)
+  // with no rows there is no sample: nothing is read, dweight becomes 0
+  if (M > 0 && (!weight || !scale))
     return set_error(NF_ERR_ARG, "nf_adaln_bwd_reduce: null pointer");
   if (ld_scale < 0) return set_error(NF_ERR_ARG, "nf_adaln_bwd_reduce: bad row stride");
   if (!is_dtype(dt_gate) || !is_dtype(dt_weight) || !is_dtype(dt_scale) ||

@@ -216,7 +216,6 @@ __global__ __launch_bounds__(kGatherThreads) void ce_gather_kernel(
 // factor P = inv * exp(mref - lse) (ce_lse_kernel), P * E is the softmax.
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ int e_swz(int t) { return 8 * (((t >> 3) ^ (t & 7)) & 31); }
-constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kStatsGap = 64.f;  // exp(-64) of a row maximum is below fp32 resolution
 
 // Blocks past the vtiles x ttiles logits tiles run the transpose regions of
@@ -301,8 +300,9 @@ __global__ NF_GEMM_BOUNDS(C) void ce_logits_kernel(
         tgt[tok] = z;
       }
     }
-    // E = exp(S - mref) relative to the row's reference, one FMA and one exp2
-    // per element (rows past V are -inf and give 0).  The tile's statistics
+    // E = exp(S - mref) relative to the row's reference (rows past V are -inf
+    // and give 0; S - mref is exact where S is near mref, so the target's own
+    // entry is exactly 1).  The tile's statistics
     // follow from its sum: s = sum exp(S - mx) = exp(mref - mx) * sum E.  A
     // tile more than kStatsGap below mref keeps s = 1: its share of the row
     // total, below exp(-kStatsGap) of the row maximum's, is under fp32
@@ -310,12 +310,10 @@ __global__ NF_GEMM_BOUNDS(C) void ce_logits_kernel(
     // (its E leaves the exponent range, its sums overflow) is recomputed
     // exactly by the statistics pass; a wavefront with no row inside the
     // vocabulary keeps (-inf, 0).
-    const float nb = -mr * kLog2e;
 #pragma unroll
     for (int i = 0; i < C::TM; ++i)
 #pragma unroll
-      for (int r = 0; r < 16; ++r)
-        acc[i][j][r] = __builtin_amdgcn_exp2f(__builtin_fmaf(acc[i][j][r], kLog2e, nb));
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = exp_f32(acc[i][j][r] - mr);
     float se = 0.f;
 #pragma unroll
     for (int i = 0; i < C::TM; ++i)
