@@ -1,7 +1,8 @@
 """Degenerate sizes through the public ops on the device (GPU): empty
-inputs, one-element rows, a one-word vocabulary, one-wide hidden states;
-every result checked against the oracle (or the closed form where the
-oracle's answer is trivially 0)."""
+inputs, one-element rows, a one-word vocabulary, one-wide hidden states, and
+an ignore_index other than -100 (inside the vocabulary, or -1); every result
+checked against the oracle (or the closed form where the oracle's answer is
+trivially 0)."""
 
 from __future__ import annotations
 
@@ -98,3 +99,31 @@ def test_swiglu_empty_and_single(cuda, shape):
         da, db = on.swiglu_backward(A, B, G)
         assert on.rel_err(np64(out), on.swiglu_forward(A, B)) <= 1e-5
         assert on.rel_err(np64(la.grad), da) <= 1e-5 and on.rel_err(np64(lb.grad), db) <= 1e-5
+
+
+@pytest.mark.parametrize("ignore_index", [3, -1, 0])
+def test_ce_custom_ignore_index(cuda, ignore_index):
+    """An ignore_index inside the vocabulary (3, 0) ignores the rows whose
+    target is that class; -1 ignores rows marked -1; against the oracle with
+    the same rows dropped."""
+    note(f"ce ignore_index={ignore_index}")
+    m, d, v = 64, 16, 10
+    g = gen(40 + ignore_index)
+    hid = randn((m, d), g, torch.float32, cuda)
+    w = randn((v, d), g, torch.float32, cuda)
+    tgt = torch.randint(0, v, (m,), generator=g)
+    if ignore_index < 0:
+        tgt[::5] = ignore_index
+    tgt = tgt.to(cuda)
+    lh, lw = hid.detach().requires_grad_(True), w.detach().requires_grad_(True)
+    loss = chunked_cross_entropy(lh, lw, tgt, chunk_size=16, ignore_index=ignore_index)
+    loss.backward()
+    torch.cuda.synchronize()
+    t = tgt.cpu().numpy().copy()
+    dropped = t == ignore_index
+    assert dropped.any()
+    t[dropped] = -100  # the oracle's own ignore marker
+    lo, dho, dwo = on.ce_forward_backward(np64(hid), np64(w), t)
+    assert abs(float(loss) - lo) <= 1e-5 * max(1.0, abs(lo))
+    assert on.rel_err(np64(lh.grad), dho) <= 1e-5 and on.rel_err(np64(lw.grad), dwo) <= 1e-5
+    assert not lh.grad[torch.from_numpy(dropped).to(cuda)].any()
