@@ -30,7 +30,9 @@ Timing:
     the two callers at the reference's model shape: the DiT seam (B8 T6 N384,
     autocast dtypes, chunk(6) views) and the reasoning-head CE (M512 D384
     V32000, bf16 hidden, fp32 lm_head), each beside its eager formulation;
-    SwiGLU in the gate/up GEMM epilogue at the encoder MLP shape.
+    SwiGLU in the gate/up GEMM epilogue at the encoder MLP shape;
+    nf_mfma_probe's MFMA rate with no memory traffic (random and zero bf16
+    operands, with the shader clock), the CE's rate as a fraction of it.
 """
 
 from __future__ import annotations
@@ -59,7 +61,7 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--no-extra", action="store_true", help="headline workload only")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baselines")
     ap.add_argument("--only", choices=("swiglu", "ce", "stress", "traffic", "dit", "head",
-                                       "gateup", "copy", "adaln", "ce_gemm_ceiling"),
+                                       "gateup", "copy", "adaln", "ce_gemm_ceiling", "mfma"),
                     default=None,
                     help="run one secondary workload alone (for profiling) and print its "
                          "record instead of the headline line")
@@ -322,6 +324,43 @@ def bench_ce_gemm_ceiling(args, dev):
     out["sum_us"] = total * 1e3
     out["tflops_6MvVD"] = 6 * mv * v * d / (total * 1e-3) / 1e12
     return out
+
+
+def bench_mfma_ceiling(args, dev, blocks=2048, iters=300):
+    """`nf_mfma_probe` for context (never the roofline denominator): bf16
+    v_mfma_f32_32x32x16 products on operands held in registers, with no
+    memory access in the loop -- 2048 blocks of 256 threads (one block per CU
+    at a time: a block holds the register file of its CU's four SIMDs), each
+    300 rounds of 128 products per wavefront -- timed as 20 back-to-back
+    launches in a HIP graph, on random N(0,1) bf16 operands and on zeros.
+    The shader clock comes from the stamps of the graph's last launch (shader
+    cycles over the 100 MHz real-time counter, summed over blocks).  On
+    random data the chip's power limit lowers the clock (a real product's
+    operands toggle the multipliers; zeros do not), so the random-operand
+    rate is the most any bf16 product of this build's data can reach."""
+    import torch
+
+    from nuvla_forge_amd import _lib
+
+    L = _lib.lib()
+    g = torch.Generator().manual_seed(60)
+    ops = torch.randn(16, 256, 8, generator=g).to(torch.bfloat16).to(dev)
+    out = torch.empty(blocks, 256, device=dev)
+    stamps = torch.zeros(blocks, 4, dtype=torch.int64, device=dev)
+    flops = blocks * 4 * iters * 32 * (2 * 32 * 32 * 16)
+    res = {"blocks": blocks, "iters": iters, "flops_per_launch": flops}
+    for name, ptr in (("random", ops.data_ptr()), ("zero", None)):
+        def launch(ptr=ptr):
+            _lib.check(L.nf_mfma_probe(ptr, iters, blocks, out.data_ptr(), stamps.data_ptr(),
+                                       _lib.stream_of(out)), "nf_mfma_probe")
+
+        ms = per_launch_ms(launch, max(5, args.steps // 5))
+        st = stamps.cpu().double()
+        ghz = float((st[:, 1] - st[:, 0]).sum() / ((st[:, 3] - st[:, 2]).sum() / 100e6) / 1e9)
+        tflops = flops / (ms * 1e-3) / 1e12
+        res[name] = {"us": ms * 1e3, "tflops": tflops,
+                     "frac_of_spec": tflops / MFMA_BF16_PEAK_TFLOPS, "clock_ghz": ghz}
+    return res
 
 
 def bench_copy(args, dev):
@@ -714,7 +753,8 @@ def main() -> int:
         fn = {"swiglu": bench_swiglu, "ce": bench_ce, "stress": bench_stress,
               "traffic": bench_traffic, "dit": bench_dit_seam,
               "head": bench_ce_reasoning_head, "gateup": bench_gate_up, "copy": bench_copy,
-              "adaln": bench_adaln, "ce_gemm_ceiling": bench_ce_gemm_ceiling}[args.only]
+              "adaln": bench_adaln, "ce_gemm_ceiling": bench_ce_gemm_ceiling,
+              "mfma": bench_mfma_ceiling}[args.only]
         print(json.dumps({"workload": args.only, **fn(args, dev)}), flush=True)
         return 0
 
@@ -730,6 +770,13 @@ def main() -> int:
         log("chunked CE cfg4 ...")
         extra["ce_cfg4"] = bench_ce(args, dev)
         log(f"  {extra['ce_cfg4']}")
+        log("MFMA ceiling probe ...")
+        mp = bench_mfma_ceiling(args, dev)
+        extra["mfma_probe"] = mp
+        # context, not the roofline: the CE's rate on 6 n V D against what the
+        # MFMA pipes reach with no memory traffic on random bf16 operands
+        extra["ce_cfg4"]["frac_of_mfma_probe"] = extra["ce_cfg4"]["tflops"] / mp["random"]["tflops"]
+        log(f"  {mp}")
         log("stress chain cfg5 ...")
         extra["stress_cfg5"] = bench_stress(args, dev)
         log(f"  {extra['stress_cfg5']}")

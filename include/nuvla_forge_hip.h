@@ -275,6 +275,21 @@ int nf_stream_probe(int reads, int writes, const void *in0, const void *in1,
                     const void *in2, const void *in3, void *out0, void *out1,
                     int64_t n16, void *stream);
 
+/* ------------------------------------------------------------------------
+ * Measurement aid with no counterpart in the reference: the MFMA ceiling
+ * bench.py sets the cross entropy's products against.  `blocks` blocks of
+ * 256 threads each issue iters * 128 bf16 v_mfma_f32_32x32x16 products
+ * (2 * 32 * 32 * 16 flops each) on operands held in registers, with no
+ * memory access in the loop.  ops: 16 * 256 16-byte vectors (vector v of
+ * thread t at index v * 256 + t; every block reads the same ones), or NULL
+ * for zero operands.  out[b * 256 + t] = the sum of thread t's accumulators
+ * in block b (blocks * 256 floats).  stamps (NULL or blocks * 4 values):
+ * per block, the shader clock counter at start and end, then the 100 MHz
+ * real-time counter at start and end.
+ * ---------------------------------------------------------------------- */
+int nf_mfma_probe(const void *ops, int64_t iters, int64_t blocks, float *out,
+                  uint64_t *stamps, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -274,6 +274,19 @@ def test_stream_probe_argument_validation():
     assert L.nf_stream_probe(2, 2, *ptrs, 0, None) == NF_OK
 
 
+def test_mfma_probe_argument_validation():
+    """The MFMA-ceiling entry point refuses bad sizes and pointers before any
+    launch (no GPU needed)."""
+    L = _lib.lib()
+    assert L.nf_mfma_probe(FAKE, -1, 1, FAKE, None, None) == NF_ERR_ARG and "iters" in _err()
+    assert L.nf_mfma_probe(FAKE, 2**30 + 1, 1, FAKE, None, None) == NF_ERR_ARG
+    assert L.nf_mfma_probe(FAKE, 1, 0, FAKE, None, None) == NF_ERR_ARG and "blocks" in _err()
+    assert L.nf_mfma_probe(FAKE, 1, 2**20 + 1, FAKE, None, None) == NF_ERR_ARG
+    assert L.nf_mfma_probe(FAKE, 1, 1, None, None, None) == NF_ERR_ARG and "out" in _err()
+    assert L.nf_mfma_probe(FAKE + 8, 1, 1, FAKE, None, None) == NF_ERR_ARG
+    assert "aligned" in _err()
+
+
 def test_chunk_rows_argument():
     assert chunked_ce.chunk_rows_for(1024) == 1024
     assert chunked_ce.chunk_rows_for(7) == 7

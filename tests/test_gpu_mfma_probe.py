@@ -1,0 +1,39 @@
+"""nf_mfma_probe, the MFMA ceiling bench.py sets the cross entropy's products
+against (GPU): with every A operand a and every B operand b (bf16), each of a
+thread's 256 accumulators receives 2 * iters products of 16-term dot products,
+so its sum is 256 * 32 * iters * a * b, exact in fp32 at these sizes; zero
+operands (a null `ops`) give 0; the stamps count forward."""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from nuvla_forge_amd import _lib
+from tests.helpers import note
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("a,b,iters,blocks", [(1.0, 1.0, 10, 3), (0.5, 0.25, 7, 300),
+                                              (0.0, 3.0, 5, 1), (None, None, 4, 2)])
+def test_mfma_probe_values(cuda, a, b, iters, blocks):
+    note(f"mfma probe a={a} b={b} iters={iters} blocks={blocks}")
+    L = _lib.lib()
+    ops = None
+    if a is not None:
+        ops = torch.empty(16, 256, 8, dtype=torch.bfloat16, device=cuda)
+        ops[0:4].fill_(a)
+        ops[8:12].fill_(a)
+        ops[4:8].fill_(b)
+        ops[12:16].fill_(b)
+    out = torch.full((blocks, 256), -1.0, device=cuda)
+    stamps = torch.zeros(blocks, 4, dtype=torch.int64, device=cuda)
+    _lib.check(L.nf_mfma_probe(None if ops is None else ops.data_ptr(), iters, blocks,
+                               out.data_ptr(), stamps.data_ptr(), _lib.stream_of(out)),
+               "nf_mfma_probe")
+    torch.cuda.synchronize()
+    want = 0.0 if a is None else 256 * 32 * iters * a * b
+    assert torch.equal(out, torch.full_like(out, want))
+    st = stamps.cpu()
+    assert bool((st[:, 1] >= st[:, 0]).all()) and bool((st[:, 3] >= st[:, 2]).all())
