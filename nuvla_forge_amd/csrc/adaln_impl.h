@@ -591,8 +591,10 @@ struct Plan {
 // (bf16 [8,1024,1024] and [32,2048,2048]).  More wavefronts in flight beat
 // deeper per-thread buffering for these streaming kernels, so rows of
 // N >= 1024 are split over >= 2 wavefronts in the forward and the backward
-// keeps one 8-element chunk per thread (up to 16 wavefronts per row).
-// Forward: each row group walks clamp(M / 2048, 1, 8) consecutive rows.
+// keeps one 8-element chunk per thread up to N = 4096 (8 wavefronts), two
+// beyond (8 wavefronts up to N = 8192, 16 up to 16384).
+// Forward: each row group walks clamp(M / 2048, 1, 8) consecutive rows
+// (clamp(M / 256, 1, 8) for rows of 8 or more wavefronts).
 // Backward: ~256 blocks of 512 threads (1 per CU), each a run of one
 // sample's rows; with 16-bit rows every row group keeps 4 rows in flight
 // (adaln_bwd_kernel RB = 4), which hides the latency the 2-per-CU launch
@@ -604,6 +606,12 @@ constexpr int kBwdBlocksTarget = 256;
 // blocks only add partial rows for the reduction to read.
 constexpr int kMaxBlocksPerSample = 1024;
 constexpr int kFwdGroupsTarget = 2048;
+// Rows of 8 or more wavefronts (N > 4096 with two chunks per lane) fill a
+// block each; for them ~256 row groups (one per CU, 2-4 rows each, taken in
+// batches) beat one row per block: bf16 [1024, 8192] forward 14.5 us with 4
+// rows per group against 23.3 us with 1, [512, 16384] 14.4 us with 2 against
+// 22.0 us with 1 (and 16.8 us with 4).
+constexpr int kFwdWideGroupsTarget = 256;
 constexpr int kFwdMaxRowsPerGroup = 8;
 
 inline int pick_wpr(int64_t N, int max_k) {
@@ -623,12 +631,17 @@ inline Plan make_plan(int64_t M, int64_t N, int64_t T, int fwd_groups = kFwdGrou
   pl.fwd_wpr = pick_wpr(N, 2);
   if (N >= 1024 && pl.fwd_wpr < 2) pl.fwd_wpr = 2;
   pl.fwd_k = pick_k(N, pl.fwd_wpr);
+  if (pl.fwd_wpr >= 8 && fwd_groups == kFwdGroupsTarget) fwd_groups = kFwdWideGroupsTarget;
   {
     int64_t rpg = M / fwd_groups;
     if (rpg > kFwdMaxRowsPerGroup) rpg = kFwdMaxRowsPerGroup;
     pl.fwd_rpg = (int)(rpg < 1 ? 1 : rpg);
   }
-  pl.bwd_wpr = pick_wpr(N, 1);
+  // One chunk per lane up to N = 4096 (8 wavefronts); wider rows take two
+  // chunks per lane, so rows up to 8192 stay on 512-thread blocks (256
+  // VGPRs, no spills: bf16 [1024, 8192] backward 24.5 us) instead of
+  // 1024-thread blocks whose 128-VGPR budget spills the row (134 us).
+  pl.bwd_wpr = pick_wpr(N, N > 4096 ? 2 : 1);
   if (pl.bwd_wpr > 16) pl.bwd_wpr = 16;
   pl.bwd_k = pick_k(N, pl.bwd_wpr);
   pl.B = M / T;
@@ -697,10 +710,14 @@ int launch_bwd_t(const BwdArgs &a, int64_t B, hipStream_t s) {
   using S = BwdShape<WPR>;
   const unsigned grid = (unsigned)(B * a.J);
   constexpr int RB = VEC ? bwd_batch_rows<TX, TY, K>() : 1;
+  // The next-row prefetch needs a second row of registers; 1024-thread
+  // blocks (16 wavefronts per row, N > 8192) have 128 VGPRs and spill less
+  // without it (bf16 [512, 16384]: 66 us against 116 us).
+  constexpr bool PF = K > 1 && S::BLK <= 512;
   if constexpr (RB > 1)
     adaln_bwd_kernel<TX, TY, K, WPR, VEC, kBwdNT, false, 512, RB><<<grid, S::BLK, 0, s>>>(a);
   else
-    adaln_bwd_kernel<TX, TY, K, WPR, VEC, kBwdNT, (K > 1)><<<grid, S::BLK, 0, s>>>(a);
+    adaln_bwd_kernel<TX, TY, K, WPR, VEC, kBwdNT, PF><<<grid, S::BLK, 0, s>>>(a);
   return check_launch("nf_adaln_bwd");
 }
 

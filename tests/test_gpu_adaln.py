@@ -89,6 +89,28 @@ def test_adaln_matches_oracle(cuda, dtype, b, t, n):
     _check(inp, t, dh, dout, h, out, grads, TOL[dtype], f"{dtype} ({b},{t},{n})")
 
 
+@pytest.mark.parametrize("dtype,b,t,n", [
+    (torch.bfloat16, 8, 128, 8192),   # 4 rows per forward group, 8 wavefronts x 2 chunks back
+    (torch.bfloat16, 2, 256, 16384),  # 2 rows per forward group, 16 wavefronts, no prefetch
+    (torch.bfloat16, 4, 64, 6000),    # 8 wavefronts x 2 chunks with a partial last chunk
+    (torch.float16, 3, 100, 5000),    # wide rows whose groups cross samples
+    (torch.float32, 2, 256, 8192),
+    (torch.float32, 1, 64, 16384),
+])
+def test_adaln_wide_rows(cuda, dtype, b, t, n):
+    """Rows of 5000-16384 elements with enough rows for the wide-row launch
+    plans (several rows per forward row group, two chunks per lane in the
+    backward), against the oracle, and a second backward bit-identical."""
+    note(f"adaln wide rows dtype={dtype} b={b} t={t} n={n}")
+    inp = _inputs(b, t, n, dtype, cuda)
+    dh, dout = _upstream(b * t, n, dtype, cuda)
+    h, out, grads = _run(inp, t, dh, dout)
+    _check(inp, t, dh, dout, h, out, grads, TOL[dtype], f"wide {dtype} ({b},{t},{n})")
+    _, _, again = _run(inp, t, dh, dout)
+    for k in NAMES:
+        assert torch.equal(again[k], grads[k]), f"d{k} differs between runs"
+
+
 def test_cfg2_bf16_and_bitwise_deterministic_backward(cuda):
     note("adaln cfg2 bf16 [8,1024,1024] x10 backward")
     b, t, n = 8, 1024, 1024
