@@ -395,11 +395,18 @@ struct BwdRow {
 // issued before any math, the RB row dot products reduced with one LDS round
 // (PF is then unused).  The per-row arithmetic and the accumulation order are
 // those of RB = 1, so the results are bit-identical.
+// CL: the per-column conditioning factors (weight * (1 + scale), gate) sit in
+// LDS instead of registers, each thread reading back its own columns at the
+// start of every row (no barrier: nothing is shared).  For 1024-thread blocks
+// (16 wavefronts per row, 128 VGPRs per thread), whose registers cannot hold
+// them beside the row and the column partials.
 template <typename TX, typename TY, int K, int WPR, bool VEC, bool NT, bool PF, int MINB = 512,
-          int RB = 1>
+          int RB = 1, bool CL = false>
 __global__ __launch_bounds__((BwdShape<WPR, MINB>::BLK)) void adaln_bwd_kernel(
     BwdArgs p) {
   using S = BwdShape<WPR, MINB>;
+  static_assert(!CL || (RB == 1 && !PF), "LDS conditioning is for the one-row loop");
+  __shared__ __attribute__((aligned(16))) float cond[CL ? 2 * kMaxN : 1];
   __shared__ float red[S::G * WPR * RB];
   // combine buffer for the G row groups: (G - 1) x (R * K * 8) floats
   __shared__ float comb[S::G > 1 ? (S::G - 1) * S::R * K * 8 : 1];
@@ -430,6 +437,16 @@ __global__ __launch_bounds__((BwdShape<WPR, MINB>::BLK)) void adaln_bwd_kernel(
     }
 #pragma unroll
     for (int i = 0; i < 8; ++i) wo[k][i] = wv[i] * (1.f + sv[i]);
+    if constexpr (CL) {
+      float *cw = cond + (k * S::R + rt) * 8, *cg = cw + kMaxN;
+#pragma unroll
+      for (int i = 0; i < 8; i += 4) {
+        *reinterpret_cast<float4 *>(cw + i) = make_float4(wo[k][i], wo[k][i + 1], wo[k][i + 2],
+                                                          wo[k][i + 3]);
+        *reinterpret_cast<float4 *>(cg + i) = make_float4(gv[k][i], gv[k][i + 1], gv[k][i + 2],
+                                                          gv[k][i + 3]);
+      }
+    }
   }
 
   float accA[K][8], accS[K][8], accG[K][8];
@@ -530,16 +547,42 @@ __global__ __launch_bounds__((BwdShape<WPR, MINB>::BLK)) void adaln_bwd_kernel(
     }
     const float rstd = active ? p.rstd[row] : 0.f;
 
-    // xhat = (x + gate * y) * rstd (h recomputed in fp32, never re-read)
+    // chunk k's conditioning factors: from registers, or (CL) read back from
+    // LDS where they are used, so they are never all live at once
+    auto cond_of = [&](int k, float (&w8)[8], float (&g8)[8]) {
+      if constexpr (CL) {
+        const float *cw = cond + (k * S::R + rt) * 8, *cg = cw + kMaxN;
+#pragma unroll
+        for (int i = 0; i < 8; i += 4) {
+          const float4 a = *reinterpret_cast<const float4 *>(cw + i);
+          const float4 e = *reinterpret_cast<const float4 *>(cg + i);
+          w8[i] = a.x; w8[i + 1] = a.y; w8[i + 2] = a.z; w8[i + 3] = a.w;
+          g8[i] = e.x; g8[i + 1] = e.y; g8[i + 2] = e.z; g8[i + 3] = e.w;
+        }
+      } else {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          w8[i] = wo[k][i];
+          g8[i] = gv[k][i];
+        }
+      }
+    };
+    // xhat = (x + gate * y) * rstd (h recomputed in fp32, never re-read);
+    // with CL formed again after the exchange (same operations, same
+    // values) instead of held across it
     float xh[K][8];
     float dot = 0.f;
 #pragma unroll
-    for (int k = 0; k < K; ++k)
+    for (int k = 0; k < K; ++k) {
+      float w8[8], g8[8];
+      cond_of(k, w8, g8);
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
-        xh[k][i] = (cur.x[k][i] + gv[k][i] * cur.y[k][i]) * rstd;
-        dot += (cur.dout[k][i] * wo[k][i]) * xh[k][i];
+        const float xv = (cur.x[k][i] + g8[i] * cur.y[k][i]) * rstd;
+        if constexpr (!CL) xh[k][i] = xv;
+        dot += (cur.dout[k][i] * w8[i]) * xv;
       }
+    }
     dot = row_sum<WPR>(dot, red, g, rt);
     const float c = dot / (float)p.N;
 
@@ -548,13 +591,16 @@ __global__ __launch_bounds__((BwdShape<WPR, MINB>::BLK)) void adaln_bwd_kernel(
       const int col = (k * S::R + rt) * 8;
       const int valid = active ? chunk_valid(p.N, col) : 0;
       if (valid > 0) {
+        float w8[8], g8[8];
+        cond_of(k, w8, g8);
         float dh[8], dyv[8];
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
           const float d = cur.dout[k][i];
-          dh[i] = cur.dh[k][i] + rstd * (d * wo[k][i] - xh[k][i] * c);
-          dyv[i] = dh[i] * gv[k][i];
-          accA[k][i] += d * xh[k][i];
+          const float xv = CL ? (cur.x[k][i] + g8[i] * cur.y[k][i]) * rstd : xh[k][i];
+          dh[i] = cur.dh[k][i] + rstd * (d * w8[i] - xv * c);
+          dyv[i] = dh[i] * g8[i];
+          accA[k][i] += d * xv;
           accS[k][i] += d;
           accG[k][i] += dh[i] * cur.y[k][i];
         }
@@ -714,10 +760,11 @@ int launch_bwd_t(const BwdArgs &a, int64_t B, hipStream_t s) {
   // blocks (16 wavefronts per row, N > 8192) have 128 VGPRs and spill less
   // without it (bf16 [512, 16384]: 66 us against 116 us).
   constexpr bool PF = K > 1 && S::BLK <= 512;
+  constexpr bool CL = S::BLK > 512 && RB == 1;
   if constexpr (RB > 1)
     adaln_bwd_kernel<TX, TY, K, WPR, VEC, kBwdNT, false, 512, RB><<<grid, S::BLK, 0, s>>>(a);
   else
-    adaln_bwd_kernel<TX, TY, K, WPR, VEC, kBwdNT, PF><<<grid, S::BLK, 0, s>>>(a);
+    adaln_bwd_kernel<TX, TY, K, WPR, VEC, kBwdNT, PF, 512, 1, CL><<<grid, S::BLK, 0, s>>>(a);
   return check_launch("nf_adaln_bwd");
 }
 
