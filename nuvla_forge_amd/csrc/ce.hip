@@ -615,21 +615,63 @@ __global__ __launch_bounds__(kPrepThreads) void ce_scale_hct_kernel(
 // 6. dH[m, :] = g * dHc[pos[m], :] in dH's type, 0 where pos[m] < 0.
 // ---------------------------------------------------------------------------
 // VE elements per thread step (4 when D is a multiple of 4: one 16-byte load).
+// With sp.S > 1 the last chunk's dH product was left in S fp32 slices
+// (`part`, [S, crows, D]): for its rows (compacted index >= sp.j0) the kernel
+// forms (sum of the slices in order 0 .. S-1) * (cfac * 1) as
+// splitk_reduce_kernel would have written to dHc, then scales by g: the same
+// operations in the same order, so the same bits, with one launch and one
+// fp32 pass over the rows fewer.
+struct SplitRows {
+  const float *part;
+  int S;
+  int64_t j0, crows;
+  const float *cfac;
+};
 template <int VE>
 __global__ __launch_bounds__(256) void ce_scatter_dh_kernel(const float *__restrict__ dHc,
                                                             int64_t D,
                                                             const int *__restrict__ pos,
                                                             int64_t M, const float *g_ptr,
-                                                            void *dH, int dt) {
+                                                            void *dH, int dt, SplitRows sp) {
   const float g = g_ptr ? *g_ptr : 1.f;
   const int64_t dv = D / VE;
   const int64_t total = M * dv;
+  const int64_t slice = sp.crows * D;
   for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total;
        i += (int64_t)gridDim.x * 256) {
     const int64_t m = i / dv, c = (i - m * dv) * VE;
     const int p = pos[m];
     float v[VE];
-    if constexpr (VE == 4) {
+    if (sp.S > 1 && p >= sp.j0) {
+      const float *src = sp.part + (p - sp.j0) * D + c;
+      float a[VE];
+#pragma unroll
+      for (int k = 0; k < VE; ++k) a[k] = 0.f;
+      // slices added in order, 8 loads in flight per batch
+      constexpr int kBatch = 8;
+      for (int q0 = 0; q0 < sp.S; q0 += kBatch) {
+        float t[kBatch][VE];
+#pragma unroll
+        for (int u = 0; u < kBatch; ++u) {
+          if (q0 + u < sp.S) {
+            if constexpr (VE == 4) {
+              const float4 w = *reinterpret_cast<const float4 *>(src + (q0 + u) * slice);
+              t[u][0] = w.x; t[u][1] = w.y; t[u][2] = w.z; t[u][3] = w.w;
+            } else {
+              t[u][0] = src[(q0 + u) * slice];
+            }
+          }
+        }
+#pragma unroll
+        for (int u = 0; u < kBatch; ++u)
+          if (q0 + u < sp.S)
+#pragma unroll
+            for (int k = 0; k < VE; ++k) a[k] += t[u][k];
+      }
+      const float f = sp.cfac[p] * 1.f;
+#pragma unroll
+      for (int k = 0; k < VE; ++k) v[k] = a[k] * f;
+    } else if constexpr (VE == 4) {
       const float4 q = p >= 0 ? *reinterpret_cast<const float4 *>(dHc + (int64_t)p * D + c)
                               : make_float4(0.f, 0.f, 0.f, 0.f);
       v[0] = q.x; v[1] = q.y; v[2] = q.z; v[3] = q.w;
@@ -776,10 +818,12 @@ struct StateView {
 // output row, split along K).  dW goes
 // to `dw_out` (type dt_w, scaled by g when given) on top of `dw_in` when
 // given.
+// reduce_dh = false leaves a split dH's fp32 slices in `part` for the
+// caller (the backward's scatter adds them).
 template <typename TI>
 int launch_grads(const Plan &L, const StateView<TI> &S, int64_t c, int64_t D, int64_t V,
                  const float *dw_in, void *dw_out, int dt_w, const float *g, float *part,
-                 hipStream_t s) {
+                 hipStream_t s, bool reduce_dh = true) {
   using C = MainCfg<TI>;
   const int64_t j0 = c * L.crows;
   auto jw = make_job<C>(S.PT, L.crows, S.Hct + j0, L.ldht, dw_in, dw_out, dt_w, g, D, V, D,
@@ -799,9 +843,9 @@ int launch_grads(const Plan &L, const StateView<TI> &S, int64_t c, int64_t D, in
     jh.part = part;
     jh.tiles *= L.split.S;
   }
-  // the longest blocks go first
-  return L.split.kslice > L.crows ? launch_gemm_store<C>(jh, jw, s)
-                                  : launch_gemm_store<C>(jw, jh, s);
+  // the longest blocks go first (the dW job is never split)
+  return L.split.kslice > L.crows ? launch_gemm_store<C>(jh, jw, s, reduce_dh)
+                                  : launch_gemm_store<C>(jw, jh, s, reduce_dh);
 }
 
 template <typename TI>
@@ -908,16 +952,20 @@ int ce_bwd_run(int64_t M, int64_t D, int64_t V, int64_t chunk_rows, char *state,
   const StateView<TI> S(L, state);
   float *part = reinterpret_cast<float *>(ws + L.b_part);
   int e;
+  // the last chunk's split dH slices are added by the scatter below
   if ((e = launch_grads<TI>(L, S, L.nch - 1, D, V, L.nch > 1 ? S.dWacc : nullptr, dW, dt_w, g,
-                            part, s)))
+                            part, s, /*reduce_dh=*/false)))
     return e;
-  const bool vec = D % 4 == 0;  // dHc rows are then 16-byte aligned
+  const SplitRows sp{part, L.split.S, (L.nch - 1) * L.crows, L.crows, S.cfac};
+  const bool vec = D % 4 == 0;  // dHc rows and slices are then 16-byte aligned
   int64_t blocks = (M * (vec ? D / 4 : D) + 255) / 256;
   if (blocks > 4096) blocks = 4096;
   if (vec)
-    ce_scatter_dh_kernel<4><<<(unsigned)blocks, 256, 0, s>>>(S.dHc, D, S.pos, M, g, dH, dt_h);
+    ce_scatter_dh_kernel<4><<<(unsigned)blocks, 256, 0, s>>>(S.dHc, D, S.pos, M, g, dH, dt_h,
+                                                             sp);
   else
-    ce_scatter_dh_kernel<1><<<(unsigned)blocks, 256, 0, s>>>(S.dHc, D, S.pos, M, g, dH, dt_h);
+    ce_scatter_dh_kernel<1><<<(unsigned)blocks, 256, 0, s>>>(S.dHc, D, S.pos, M, g, dH, dt_h,
+                                                             sp);
   return check_launch("ce_scatter_dh");
 }
 

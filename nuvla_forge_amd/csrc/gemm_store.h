@@ -488,10 +488,11 @@ bool job_sb_ok(const GemmJob<TI> &j) {
 }
 
 // Both jobs in one grid (j1 may be empty: tiles == 0), then the split-K
-// reductions of a split job.
+// reductions of a split job (unless `reduce` is false: the caller then adds
+// the slices itself, as splitk_reduce_kernel would).
 template <class C>
 int launch_gemm_store(const GemmJob<typename C::TI> &j0, const GemmJob<typename C::TI> &j1,
-                      hipStream_t s) {
+                      hipStream_t s, bool reduce = true) {
   const int64_t total = (int64_t)j0.tiles + j1.tiles;
   if (total == 0) return NF_OK;
   if (total > 0x7fffffffLL) return set_error(NF_ERR_ARG, "gemm: too many tiles");
@@ -505,6 +506,7 @@ int launch_gemm_store(const GemmJob<typename C::TI> &j0, const GemmJob<typename 
   else
     gemm_store_kernel<C, false, false><<<grid, C::NT, 0, s>>>(j0, j1);
   if (int e = check_launch("gemm_store")) return e;
+  if (!reduce) return NF_OK;
   for (const auto *jp : {&j0, &j1}) {
     if (jp->tiles == 0 || jp->ksplit <= 1) continue;
     int64_t blocks = (jp->M * jp->N + 255) / 256;
