@@ -407,7 +407,8 @@ __global__ NF_GEMM_BOUNDS(C) void ce_logits_kernel(
 // ---------------------------------------------------------------------------
 // 4. lse per row of a chunk: a block takes 16 rows and 16 parts; part q
 // combines statistics tiles q, q + 16, q + 32, ... of its row in that order
-// (four tiles' loads issued before their combines), then the first part
+// (sixteen tiles' loads issued before their combines: one round of loads for
+// vocabularies up to 32768), then the first part
 // combines the 16 partial results in order.  A row of 16 tokens is 128
 // contiguous bytes of the [ntiles][crows] statistics.
 // ---------------------------------------------------------------------------
@@ -440,7 +441,7 @@ __global__ __launch_bounds__(kLseThreads) void ce_lse_kernel(
   if ((int64_t)blockIdx.x * kLseRows >= cnt) return;  // the whole block is past the chunk
   float2 a = make_float2(-INFINITY, 0.f);
   if (row < cnt) {
-    constexpr int kBatch = 4;
+    constexpr int kBatch = 16;
     for (int t0 = q; t0 < ntiles; t0 += kLseParts * kBatch) {
       float2 v[kBatch];
 #pragma unroll
