@@ -96,6 +96,8 @@ def test_adaln_matches_oracle(cuda, dtype, b, t, n):
     (torch.float16, 3, 100, 5000),    # wide rows whose groups cross samples
     (torch.float32, 2, 256, 8192),
     (torch.float32, 1, 64, 16384),
+    (torch.bfloat16, 2, 40, 10001),   # odd N: element-wise path, 16 wavefronts, LDS factors
+    (torch.float32, 3, 30, 5001),     # odd N: element-wise path, 8 wavefronts x 2 chunks
 ])
 def test_adaln_wide_rows(cuda, dtype, b, t, n):
     """Rows of 5000-16384 elements with enough rows for the wide-row launch
