@@ -166,6 +166,20 @@ def test_ce_rows_far_from_their_reference(cuda, dtype, chunk):
     _check_ce(hid, w, tgt, loss, dh, dw, tol, f"far rows {dtype} chunk {chunk}")
 
 
+@pytest.mark.parametrize("dtype,chunk", [(torch.bfloat16, 128), (torch.bfloat16, 4096),
+                                         (torch.float32, 128)])
+def test_ce_large_vocabulary(cuda, dtype, chunk):
+    """A Llama-3-sized vocabulary (V = 128256: 1002 statistics tiles per row,
+    several load rounds in the lse pass, 501 vocabulary tiles per logits
+    launch) with several row chunks and with one, against the oracle."""
+    m, d, v = 300, 256, 128256
+    note(f"ce large vocabulary dtype={dtype} m={m} d={d} v={v} chunk={chunk}")
+    hid, w, tgt = _ce_inputs(m, d, v, dtype, cuda, seed=9, w_std=0.05,
+                             ignore=slice(None, None, 7))
+    loss, dh, dw = _run_ce(hid, w, tgt, chunk)
+    _check_ce(hid, w, tgt, loss, dh, dw, TOL[dtype], f"large vocab {dtype} chunk {chunk}")
+
+
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("m,d,v,chunk", [(17, 36, 333, 7), (300, 40, 1030, 1000), (9, 4, 6, 1),
                                          (130, 264, 129, 64)])
