@@ -151,6 +151,11 @@ template <typename TX, typename TY, int K, int WPR, bool VEC, bool NT,
 __global__ __launch_bounds__((FwdShape<WPR, MINB>::BLK)) void adaln_fwd_kernel(
     FwdArgs p) {
   using S = FwdShape<WPR, MINB>;
+  // 1024-thread blocks (16 wavefronts per row, 128 VGPRs per thread) hold
+  // neither the weight nor the next row nor h: the weight is read again when
+  // the sample changes, each row is loaded at the top of its iteration, and h
+  // is formed again for the output (same operations, same values)
+  constexpr bool LEAN = S::BLK > 512;
   __shared__ float red[S::G * WPR];
   const int g = threadIdx.x / S::R;
   const int rt = threadIdx.x % S::R;
@@ -160,11 +165,13 @@ __global__ __launch_bounds__((FwdShape<WPR, MINB>::BLK)) void adaln_fwd_kernel(
   const TY *const yp = static_cast<const TY *>(p.y);
 
   float wv[K][8];
+  if constexpr (!LEAN) {
 #pragma unroll
-  for (int k = 0; k < K; ++k) {
-    const int col = (k * S::R + rt) * 8;
-    const int valid = chunk_valid(p.N, col);
-    if (valid > 0) load8_dyn<VEC>(p.weight, p.dt_weight, col, valid, wv[k]);
+    for (int k = 0; k < K; ++k) {
+      const int col = (k * S::R + rt) * 8;
+      const int valid = chunk_valid(p.N, col);
+      if (valid > 0) load8_dyn<VEC>(p.weight, p.dt_weight, col, valid, wv[k]);
+    }
   }
 
   Raw8<TX> xc[K], xn[K];
@@ -183,14 +190,18 @@ __global__ __launch_bounds__((FwdShape<WPR, MINB>::BLK)) void adaln_fwd_kernel(
       }
     }
   };
-  if (first < last) load_row(first, xc, yc);
+  if (!LEAN && first < last) load_row(first, xc, yc);
 
   float gv[K][8], wo[K][8], shv[K][8];
   int64_t cur_b = -1;
   for (int r = 0; r < p.rows_per_group; ++r) {
     const int64_t row = first + r;
     const bool active = row < last;
-    if (row + 1 < last) load_row(row + 1, xn, yn);
+    if constexpr (LEAN) {
+      if (active) load_row(row, xc, yc);
+    } else {
+      if (row + 1 < last) load_row(row + 1, xn, yn);
+    }
     if (active) {
       const int64_t b = row / p.T;
       if (b != cur_b) {  // uniform across the row group
@@ -201,6 +212,7 @@ __global__ __launch_bounds__((FwdShape<WPR, MINB>::BLK)) void adaln_fwd_kernel(
           const int valid = chunk_valid(p.N, col);
           float sv[8];
           if (valid > 0) {
+            if constexpr (LEAN) load8_dyn<VEC>(p.weight, p.dt_weight, col, valid, wv[k]);
             load8_dyn<VEC>(p.gate, p.dt_gate, b * p.ld_gate + col, valid, gv[k]);
             load8_dyn<VEC>(p.scale, p.dt_scale, b * p.ld_scale + col, valid, sv);
             load8_dyn<VEC>(p.shift, p.dt_shift, b * p.ld_shift + col, valid, shv[k]);
@@ -236,15 +248,20 @@ __global__ __launch_bounds__((FwdShape<WPR, MINB>::BLK)) void adaln_fwd_kernel(
       if (valid > 0) {
         float o[8];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) o[i] = (hv[k][i] * rstd) * wo[k][i] + shv[k][i];
+        for (int i = 0; i < 8; ++i) {
+          const float hh = LEAN ? xc[k][i] + gv[k][i] * yc[k][i] : hv[k][i];
+          o[i] = (hh * rstd) * wo[k][i] + shv[k][i];
+        }
         store8_hint<TX, VEC, NT>(static_cast<TX *>(p.out) + row * (int64_t)p.N + col, valid,
                                  o);
       }
     }
+    if constexpr (!LEAN) {
 #pragma unroll
-    for (int k = 0; k < K; ++k) {
-      xc[k] = xn[k];
-      yc[k] = yn[k];
+      for (int k = 0; k < K; ++k) {
+        xc[k] = xn[k];
+        yc[k] = yn[k];
+      }
     }
   }
 }
@@ -768,13 +785,34 @@ int launch_bwd_t(const BwdArgs &a, int64_t B, hipStream_t s) {
   return check_launch("nf_adaln_bwd");
 }
 
+// (wavefronts per row, chunks per lane) pairs make_plan gives on the vector
+// path, so only those are compiled: forward one chunk up to 2 wavefronts (N <=
+// 1024), two chunks otherwise; backward one chunk up to 8 wavefronts (N <=
+// 4096), two chunks from 8 (N > 4096).  The element-wise path always takes two.
+template <int WPR, int K>
+constexpr bool fwd_planned() {
+  return K == 2 || WPR <= 2;
+}
+template <int WPR, int K>
+constexpr bool bwd_planned() {
+  return K == 1 ? WPR <= 8 : WPR >= 8;
+}
+inline int unplanned(const char *who, int wpr, int k) {
+  return set_error(NF_ERR_ARG, "%s: no kernel for %d wavefronts x %d chunks per row", who, wpr,
+                   k);
+}
+
 template <typename TX, typename TY, bool VEC, int WPR>
 int fwd_k(const FwdArgs &a, const Plan &pl, hipStream_t s) {
   if constexpr (!VEC) {
     return launch_fwd_t<TX, TY, false, WPR, 2>(a, pl, s);
   } else {
-    if (pl.fwd_k == 1) return launch_fwd_t<TX, TY, true, WPR, 1>(a, pl, s);
-    return launch_fwd_t<TX, TY, true, WPR, 2>(a, pl, s);
+    if (pl.fwd_k == 1) {
+      if constexpr (fwd_planned<WPR, 1>()) return launch_fwd_t<TX, TY, true, WPR, 1>(a, pl, s);
+      return unplanned("nf_adaln_fwd", WPR, 1);
+    }
+    if constexpr (fwd_planned<WPR, 2>()) return launch_fwd_t<TX, TY, true, WPR, 2>(a, pl, s);
+    return unplanned("nf_adaln_fwd", WPR, 2);
   }
 }
 template <typename TX, typename TY, bool VEC, int WPR>
@@ -782,8 +820,12 @@ int bwd_k(const BwdArgs &a, const Plan &pl, hipStream_t s) {
   if constexpr (!VEC) {
     return launch_bwd_t<TX, TY, false, WPR, 2>(a, pl.B, s);
   } else {
-    if (pl.bwd_k == 1) return launch_bwd_t<TX, TY, true, WPR, 1>(a, pl.B, s);
-    return launch_bwd_t<TX, TY, true, WPR, 2>(a, pl.B, s);
+    if (pl.bwd_k == 1) {
+      if constexpr (bwd_planned<WPR, 1>()) return launch_bwd_t<TX, TY, true, WPR, 1>(a, pl.B, s);
+      return unplanned("nf_adaln_bwd", WPR, 1);
+    }
+    if constexpr (bwd_planned<WPR, 2>()) return launch_bwd_t<TX, TY, true, WPR, 2>(a, pl.B, s);
+    return unplanned("nf_adaln_bwd", WPR, 2);
   }
 }
 

@@ -98,6 +98,8 @@ def test_adaln_matches_oracle(cuda, dtype, b, t, n):
     (torch.float32, 1, 64, 16384),
     (torch.bfloat16, 2, 40, 10001),   # odd N: element-wise path, 16 wavefronts, LDS factors
     (torch.float32, 3, 30, 5001),     # odd N: element-wise path, 8 wavefronts x 2 chunks
+    (torch.bfloat16, 4, 129, 12000),  # odd T: the one-row forward on 1024-thread blocks
+    (torch.float16, 3, 75, 16384),    # fewer than 2 rows per forward group
 ])
 def test_adaln_wide_rows(cuda, dtype, b, t, n):
     """Rows of 5000-16384 elements with enough rows for the wide-row launch
