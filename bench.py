@@ -270,7 +270,10 @@ def bench_adaln(args, dev):
     _sync()
     graph_ok = graph_ok and same(ref, outs)
     del graph, outs
-    graph1_ms, _, _ = time_graph(make, args.steps, args.warmup, 1)
+    graph1_ms, _, graph1 = time_graph(make, args.steps, args.warmup, 1)
+    cold_ms = cold_replay_ms(graph1, dev, max(5, args.steps // 2))
+    cold_dirty_ms = cold_replay_ms(graph1, dev, max(5, args.steps // 2), dirty=True)
+    del graph1
 
     # per-kernel durations: back-to-back launches of each C-ABI entry point
     kern_ms = adaln_kernel_ms(inp, t, dh, dout, args.steps)
@@ -286,7 +289,7 @@ def bench_adaln(args, dev):
     fwd_gbs = fwd_alg / (kern_ms["nf_adaln_fwd"] * 1e-3) / 1e9
     return {
         "b": b, "t": t, "n": n, "alg_bytes": alg, "graph_ms": graph_ms, "eager_ms": eager_ms,
-        "graph1_ms": graph1_ms,
+        "graph1_ms": graph1_ms, "cold_ms": cold_ms, "cold_dirty_ms": cold_dirty_ms,
         "graph_matches_eager": graph_ok, "kernel_ms": kern_ms, "in_step_ms": instep_ms,
         "bwd_alg_bytes": bwd_alg, "bwd_gbs": bwd_gbs, "fwd_alg_bytes": fwd_alg, "fwd_gbs": fwd_gbs,
         "bwd_gbs_in_step": bwd_alg / (instep_ms["nf_adaln_bwd"] * 1e-3) / 1e9,
@@ -427,6 +430,31 @@ def stream_ceilings(args, dev, sizes=(("cfg2_16MiB", 16 << 20), ("cfg5_256MiB", 
                 "alt_us": alt * 1e3, "alt_gbs": moved / (alt * 1e-3) / 1e9}
             del sets
     return out
+
+
+def cold_replay_ms(graph, dev, reps, dirty=False, flush_bytes=1 << 30):
+    """Milliseconds per replay of a one-step graph with the caches cold: before
+    each replay a read pass over `flush_bytes` (4x the 256 MB Infinity Cache)
+    evicts the step's operands from the L2s and the Infinity Cache, so they
+    come from HBM (with `dirty`, a read-modify-write pass, whose dirty lines
+    the step then has to write back as well); only the replay lies between
+    the events."""
+    import torch
+
+    flush = torch.ones(flush_bytes // 4, dtype=torch.int32, device=dev)
+    pairs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+             for _ in range(reps)]
+    for e0, e1 in pairs:
+        if dirty:
+            flush.add_(1)
+        else:
+            flush.sum(dtype=torch.int64)
+        e0.record()
+        graph.replay()
+        e1.record()
+    _sync()
+    del flush
+    return statistics.median(e0.elapsed_time(e1) for e0, e1 in pairs)
 
 
 def adaln_in_step_ms(inp, t, dh, dout, steps, reps=10):
@@ -821,6 +849,14 @@ def main() -> int:
             "hbm_frac_whole_step": round(ad["gbs"] / HBM_PEAK_GBS, 4),
             "eager_ms_per_step": round(ad["eager_ms"], 5),
             "graph1_ms_per_step": round(ad["graph1_ms"], 5),
+            # one-step replays after a 1 GiB read pass has evicted the
+            # operands from the L2s and the Infinity Cache (HBM-resident
+            # inputs; compare graph1_ms_per_step), and after a 1 GiB
+            # read-modify-write pass whose dirty lines the step writes back
+            "cold_ms_per_step": round(ad["cold_ms"], 5),
+            "cold_dirty_ms_per_step": round(ad["cold_dirty_ms"], 5),
+            "hbm_frac_cold_step": round(ad["alg_bytes"] / (ad["cold_ms"] * 1e-3) / 1e9
+                                        / HBM_PEAK_GBS, 4),
             "graph_matches_eager": ad["graph_matches_eager"],
             "kernel_ms": {k: round(v, 5) for k, v in ad["kernel_ms"].items()},
             "in_step_kernel_ms": {k: round(v, 5) for k, v in ad["in_step_ms"].items()},
