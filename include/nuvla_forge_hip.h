@@ -188,7 +188,9 @@ int nf_adaln_bwd_noalloc(const void *dh_up, const void *dout, const void *x,
 
 /* ------------------------------------------------------------------------
  * Chunked cross entropy.
- *   logits = hidden @ weight^T          ([M, V], never materialised)
+ *   logits = hidden @ weight^T          ([M, V]; chunk_rows rows of it at a
+ *                                        time, all of it when one chunk
+ *                                        covers every valid row)
  *   lse    = logsumexp_v logits         (fp32)
  *   n      = #(targets != ignore_index);  inv = 1 / max(n, 1)
  *   loss   = inv * sum_{valid m} (lse[m] - logits[m, t_m])   (fp32 scalar)
@@ -253,42 +255,6 @@ int nf_ce_fwd_bwd(const void *hidden, const void *weight,
                   float *loss, float *dhidden, float *dweight,
                   int32_t *bad_targets, void *workspace,
                   size_t workspace_bytes, void *stream);
-
-/* ------------------------------------------------------------------------
- * Test hook with no counterpart in the reference: C[M, N] (fp32, row stride
- * ldc) = A[M, K] @ B[N, K]^T with the MFMA core the cross entropy uses.
- * A and B are row-major with unit-stride K, type `dtype` (bf16 or f32).
- * ---------------------------------------------------------------------- */
-int nf_gemm_nt(const void *A, int64_t lda, const void *B, int64_t ldb,
-               float *C, int64_t ldc, int64_t M, int64_t N, int64_t K,
-               int dtype, void *stream);
-
-/* ------------------------------------------------------------------------
- * Measurement aid with no counterpart in the reference: the streaming
- * ceiling bench.py sets the row kernels against.  Reads `reads` arrays
- * (in0..in3) and writes `writes` arrays (out0, out1) of n16 16-byte vectors
- * each, (reads, writes) one of (1, 1), (2, 2), (4, 2); out_w[i] = (in0[i]
- * xor ... xor in_{reads-1}[i]) + w in every 32-bit lane.  Pointers unused by
- * the (reads, writes) pair may be null; the others must be 16-byte aligned.
- * ---------------------------------------------------------------------- */
-int nf_stream_probe(int reads, int writes, const void *in0, const void *in1,
-                    const void *in2, const void *in3, void *out0, void *out1,
-                    int64_t n16, void *stream);
-
-/* ------------------------------------------------------------------------
- * Measurement aid with no counterpart in the reference: the MFMA ceiling
- * bench.py sets the cross entropy's products against.  `blocks` blocks of
- * 256 threads each issue iters * 128 bf16 v_mfma_f32_32x32x16 products
- * (2 * 32 * 32 * 16 flops each) on operands held in registers, with no
- * memory access in the loop.  ops: 16 * 256 16-byte vectors (vector v of
- * thread t at index v * 256 + t; every block reads the same ones), or NULL
- * for zero operands.  out[b * 256 + t] = the sum of thread t's accumulators
- * in block b (blocks * 256 floats).  stamps (NULL or blocks * 4 values):
- * per block, the shader clock counter at start and end, then the 100 MHz
- * real-time counter at start and end.
- * ---------------------------------------------------------------------- */
-int nf_mfma_probe(const void *ops, int64_t iters, int64_t blocks, float *out,
-                  uint64_t *stamps, void *stream);
 
 #ifdef __cplusplus
 }

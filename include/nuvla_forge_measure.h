@@ -1,0 +1,63 @@
+/*
+ * nuvla_forge_measure.h -- measurement aids and a test hook, built into
+ * nuvla_forge_amd/libnf_measure.so beside the product library
+ * (libnf_hip.so, include/nuvla_forge_hip.h).  None of these has a
+ * counterpart in the reference, and no op of the product calls them: the
+ * benchmark sets the product kernels against the two probes, and the tests
+ * drive the MFMA GEMM core through nf_gemm_nt.
+ *
+ * Same conventions as the product ABI: device pointers, int64_t sizes, a
+ * hipStream_t as `void *`, NF_OK or a negative status, and the failure text
+ * in the product library's nf_last_error() (this library reports through
+ * it; libnf_measure.so links libnf_hip.so).
+ */
+#ifndef NUVLA_FORGE_MEASURE_H
+#define NUVLA_FORGE_MEASURE_H
+
+#include "nuvla_forge_hip.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ------------------------------------------------------------------------
+ * Test hook with no counterpart in the reference: C[M, N] (fp32, row stride
+ * ldc) = A[M, K] @ B[N, K]^T with the MFMA core the cross entropy uses.
+ * A and B are row-major with unit-stride K, type `dtype` (bf16 or f32).
+ * ---------------------------------------------------------------------- */
+int nf_gemm_nt(const void *A, int64_t lda, const void *B, int64_t ldb,
+               float *C, int64_t ldc, int64_t M, int64_t N, int64_t K,
+               int dtype, void *stream);
+
+/* ------------------------------------------------------------------------
+ * Measurement aid with no counterpart in the reference: the streaming
+ * ceiling bench.py sets the row kernels against.  Reads `reads` arrays
+ * (in0..in3) and writes `writes` arrays (out0, out1) of n16 16-byte vectors
+ * each, (reads, writes) one of (1, 1), (2, 2), (4, 2); out_w[i] = (in0[i]
+ * xor ... xor in_{reads-1}[i]) + w in every 32-bit lane.  Pointers unused by
+ * the (reads, writes) pair may be null; the others must be 16-byte aligned.
+ * ---------------------------------------------------------------------- */
+int nf_stream_probe(int reads, int writes, const void *in0, const void *in1,
+                    const void *in2, const void *in3, void *out0, void *out1,
+                    int64_t n16, void *stream);
+
+/* ------------------------------------------------------------------------
+ * Measurement aid with no counterpart in the reference: the MFMA ceiling
+ * bench.py sets the cross entropy's products against.  `blocks` blocks of
+ * 256 threads each issue iters * 128 bf16 v_mfma_f32_32x32x16 products
+ * (2 * 32 * 32 * 16 flops each) on operands held in registers, with no
+ * memory access in the loop.  ops: 16 * 256 16-byte vectors (vector v of
+ * thread t at index v * 256 + t; every block reads the same ones), or NULL
+ * for zero operands.  out[b * 256 + t] = the sum of thread t's accumulators
+ * in block b (blocks * 256 floats).  stamps (NULL or blocks * 4 values):
+ * per block, the shader clock counter at start and end, then the 100 MHz
+ * real-time counter at start and end.
+ * ---------------------------------------------------------------------- */
+int nf_mfma_probe(const void *ops, int64_t iters, int64_t blocks, float *out,
+                  uint64_t *stamps, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* NUVLA_FORGE_MEASURE_H */

@@ -2,10 +2,14 @@
 
 Usage: ``python -m nuvla_forge_amd.build [-v]``.  Every ``csrc/*.hip`` file is
 compiled to an object in ``_build/`` (in parallel), then linked into
-``nuvla_forge_amd/libnf_hip.so``.  The library links ``libamdhip64.so.7`` by
-soname, so inside a process that imported torch first it binds to the HIP
-runtime torch already loaded.  Last, ``tests/c/abi_smoke`` (a C program using
-the library through its C ABI alone) is compiled with gcc.
+``nuvla_forge_amd/libnf_hip.so`` (the product: include/nuvla_forge_hip.h).
+The measurement aids and the GEMM test hook (``csrc/measure/*.hip``,
+include/nuvla_forge_measure.h) go into ``nuvla_forge_amd/libnf_measure.so``,
+which links the product library for its error reporting; only the benchmark
+and the tests load it.  Both link ``libamdhip64.so.7`` by soname, so inside a
+process that imported torch first they bind to the HIP runtime torch already
+loaded.  Last, ``tests/c/abi_smoke`` (a C program using the product library
+through its C ABI alone) is compiled with gcc.
 """
 
 from __future__ import annotations
@@ -21,6 +25,7 @@ PKG = Path(__file__).resolve().parent
 CSRC = PKG / "csrc"
 BUILD = PKG.parent / "_build"
 LIB = PKG / "libnf_hip.so"
+MEASURE_LIB = PKG / "libnf_measure.so"
 INCLUDE = PKG.parent / "include"
 
 ARCH = "gfx950"
@@ -51,7 +56,7 @@ def _hipcc() -> str:
 
 
 def _compile(src: Path, verbose: bool) -> Path:
-    obj = BUILD / (src.stem + ".o")
+    obj = BUILD / (("measure_" if src.parent.name == "measure" else "") + src.stem + ".o")
     cmd = [_hipcc(), *CFLAGS, "-c", str(src), "-o", str(obj)]
     if verbose:
         print(" ".join(cmd), flush=True)
@@ -66,24 +71,32 @@ def _compile(src: Path, verbose: bool) -> Path:
     return obj
 
 
-def build(verbose: bool = False, jobs: int | None = None) -> Path:
-    """Compile every csrc/*.hip for gfx950 and link libnf_hip.so.  Always rebuilds."""
-    BUILD.mkdir(exist_ok=True)
-    sources = sorted(CSRC.glob("*.hip"))
-    if not sources:
-        raise RuntimeError(f"no sources under {CSRC}")
-    jobs = jobs or min(len(sources), max(1, (os.cpu_count() or 2)))
-    with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
-        objs = list(ex.map(lambda s: _compile(s, verbose), sources))
-    tmp = LIB.with_suffix(".so.tmp")
+def _link(objs: list[Path], out: Path, extra: list[str], verbose: bool) -> None:
+    tmp = out.with_suffix(".so.tmp")
     cmd = [_hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp),
-           *map(str, objs)]
+           *map(str, objs), *extra]
     if verbose:
         print(" ".join(cmd), flush=True)
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
-        raise RuntimeError(f"link failed:\n{res.stdout}{res.stderr}")
-    os.replace(tmp, LIB)
+        raise RuntimeError(f"link of {out.name} failed:\n{res.stdout}{res.stderr}")
+    os.replace(tmp, out)
+
+
+def build(verbose: bool = False, jobs: int | None = None) -> Path:
+    """Compile every csrc/*.hip and csrc/measure/*.hip for gfx950 and link
+    libnf_hip.so and libnf_measure.so.  Always rebuilds."""
+    BUILD.mkdir(exist_ok=True)
+    sources = sorted(CSRC.glob("*.hip"))
+    measure = sorted((CSRC / "measure").glob("*.hip"))
+    if not sources:
+        raise RuntimeError(f"no sources under {CSRC}")
+    jobs = jobs or min(len(sources) + len(measure), max(1, (os.cpu_count() or 2)))
+    with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
+        objs = list(ex.map(lambda s: _compile(s, verbose), sources + measure))
+    _link(objs[:len(sources)], LIB, ["-Wl,-soname,libnf_hip.so"], verbose)
+    _link(objs[len(sources):], MEASURE_LIB,
+          [f"-L{PKG}", "-lnf_hip", "-Wl,-rpath,$ORIGIN"], verbose)
     build_c_smoke(verbose)
     return LIB
 

@@ -48,19 +48,6 @@ namespace ce {
 
 using namespace gemm;
 
-// bf16: 256x256 block tiles, 8 wavefronts of 128x64 (two per SIMD, so one
-// wavefront's LDS waits and epilogue overlap the other's MFMAs), operands
-// copied global -> LDS directly in 64-wide K-stages, two stage buffers; f32
-// (correctness path): 128x128 tiles staged through registers.
-template <typename TI>
-struct MainCfgT;
-template <>
-struct MainCfgT<bf16> { using type = gemm::DCfg<256, 256, 2, 4, 2, 64>; };
-template <>
-struct MainCfgT<float> { using type = Cfg<float, 128, 128, 2, 2>; };
-template <typename TI>
-using MainCfg = typename MainCfgT<TI>::type;
-
 __device__ __forceinline__ float log_f32(float x) {
   constexpr float kLn2 = 0.6931471805599453f;  // ln(2)
   return __builtin_amdgcn_logf(x) * kLn2;       // log2 on the hardware
@@ -151,7 +138,7 @@ __global__ __launch_bounds__(kCompactThreads) void ce_compact_kernel(
 // fixed-order sum; 0 past n_valid).  One wavefront per row.  E is stored
 // relative to mref (exp(S - mref)), so mref needs only to lie within the
 // exponent range of the row's largest logit; the target logit does for every
-// row whose loss is below ~75 nats, and the statistics pass sends any other
+// row whose loss is below ~50 nats, and the statistics pass sends any other
 // row through an exact recomputation (ce_lse_kernel).  VEC: 16-byte vectors
 // (D a multiple of the vector width, aligned rows).
 // ---------------------------------------------------------------------------
@@ -306,9 +293,9 @@ __global__ NF_GEMM_BOUNDS(C) void ce_logits_kernel(
     // follow from its sum: s = sum exp(S - mx) = exp(mref - mx) * sum E.  A
     // tile more than kStatsGap below mref keeps s = 1: its share of the row
     // total, below exp(-kStatsGap) of the row maximum's, is under fp32
-    // resolution.  A row whose maximum lies more than kRefGap above mref
-    // (its E leaves the exponent range, its sums overflow) is recomputed
-    // exactly by the statistics pass; a wavefront with no row inside the
+    // resolution.  A row whose maximum lies far above mref (its E leaves
+    // the exponent range, its sums overflow) is recomputed exactly by the
+    // statistics pass (kFactorGap); a wavefront with no row inside the
     // vocabulary keeps (-inf, 0).
 #pragma unroll
     for (int i = 0; i < C::TM; ++i)
@@ -415,14 +402,18 @@ __global__ NF_GEMM_BOUNDS(C) void ce_logits_kernel(
 // The row factor cfac = inv * exp(mref - lse), so that cfac * E is the
 // softmax over the row scaled by 1 / n.  The one-hot term goes into E itself:
 // the target entry becomes exp(z - mref) - exp(lse - mref), so cfac * E is
-// (softmax - onehot) / n, the gradient of the mean loss by the logits.  A row
-// whose largest logit lies more than kRefGap above mref (its E entries would
-// leave the exponent range and its tile sums overflow) is recomputed exactly
-// by its block: fp32 dot products in a fixed order, the row's max and sum of
-// exponentials (so its lse and loss) from them, E relative to the row max,
-// written to both layouts.  (The target logit is within kRefGap of the row max for any
-// row whose loss is under kRefGap nats.)
-constexpr float kRefGap = 75.f;
+// (softmax - onehot) / n, the gradient of the mean loss by the logits.
+// The fast path holds while (lse - mref) + ln n <= kFactorGap: cfac (which
+// multiplies Hc into the dW product's operand, rounded to the input type)
+// then stays above exp(-kFactorGap), far inside the normal range of bf16 and
+// fp32, and every E entry below exp(kFactorGap), far from overflow in the
+// products' sums (lse is at least the row's largest logit).  Any other row
+// (a loss above kFactorGap - ln n nats, ~52 at n = 4096; also a row whose
+// tile sums overflowed, or a NaN / inf row) is recomputed exactly by its
+// block: fp32 dot products in a fixed order, the row's max and sum of
+// exponentials (so its lse and loss) from them, E relative to the row max
+// (cfac is then at least 1 / (n V)), written to both layouts.
+constexpr float kFactorGap = 60.f;
 constexpr int kLseRows = 16, kLseParts = 16, kLseThreads = kLseRows * kLseParts;
 
 template <typename TI>
@@ -465,7 +456,7 @@ __global__ __launch_bounds__(kLseThreads) void ce_lse_kernel(
       const float z = tgt[row];
       loss_row[j0 + row] = ls - z;  // rewritten below for a recomputed row
       const float m = mref[j0 + row];
-      again = !(a.x - m <= kRefGap);  // also for a NaN / inf row
+      again = !(ls - m - log_f32(inv) <= kFactorGap);  // also for a NaN / inf row
       if (!again) {
         cfac[j0 + row] = inv * exp_f32(m - ls);
         const int64_t tc = tcol[j0 + row];
@@ -1108,36 +1099,4 @@ extern "C" int nf_ce_fwd_bwd(const void *hidden, const void *weight, const int64
     return e;
   return nf_ce_bwd(M, D, V, chunk_rows, dtype, ws, sb, nullptr, dhidden, NF_DTYPE_F32, dweight,
                    NF_DTYPE_F32, ws + sb, workspace_bytes - sb, stream);
-}
-
-extern "C" int nf_gemm_nt(const void *A, int64_t lda, const void *B, int64_t ldb, float *C,
-                          int64_t ldc, int64_t M, int64_t N, int64_t K, int dtype,
-                          void *stream) {
-  if (M < 0 || N < 0 || K < 0) return set_error(NF_ERR_ARG, "nf_gemm_nt: negative size");
-  if (M > 0x7fffffffLL || N > 0x7fffffffLL || K > 0x7fffffffLL)
-    return set_error(NF_ERR_ARG, "nf_gemm_nt: a size exceeds int32");
-  if (M == 0 || N == 0) return NF_OK;
-  if (!A || !B || !C) return set_error(NF_ERR_ARG, "nf_gemm_nt: null pointer");
-  if (lda < K || ldb < K || ldc < N) return set_error(NF_ERR_ARG, "nf_gemm_nt: bad leading dim");
-  // tiles are at least 128 x 128; the grid is one-dimensional
-  if (((M + 127) / 128) * ((N + 127) / 128) > 0x7fffffffLL)
-    return set_error(NF_ERR_ARG, "nf_gemm_nt: grid too large");
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  if (dtype == NF_DTYPE_BF16) {
-    using C16 = MainCfg<bf16>;
-    const GemmJob<bf16> none{};
-    return launch_gemm_store<C16>(
-        make_job<C16>((const bf16 *)A, lda, (const bf16 *)B, ldb, nullptr, C, NF_DTYPE_F32,
-                      nullptr, ldc, M, N, K),
-        none, s);
-  }
-  if (dtype == NF_DTYPE_F32) {
-    using C32 = MainCfg<float>;
-    const GemmJob<float> none{};
-    return launch_gemm_store<C32>(
-        make_job<C32>((const float *)A, lda, (const float *)B, ldb, nullptr, C, NF_DTYPE_F32,
-                      nullptr, ldc, M, N, K),
-        none, s);
-  }
-  return set_error(NF_ERR_DTYPE, "nf_gemm_nt: dtype %d unsupported", dtype);
 }

@@ -451,6 +451,19 @@ inline int launch_zero16(void *p, int64_t ld, int64_t rows, int64_t cols, hipStr
   return check_launch("zero16");
 }
 
+// bf16: 256x256 block tiles, 8 wavefronts of 128x64 (two per SIMD, so one
+// wavefront's LDS waits and epilogue overlap the other's MFMAs), operands
+// copied global -> LDS directly in 64-wide K-stages, two stage buffers; f32
+// (correctness path): 128x128 tiles staged through registers.
+template <typename TI>
+struct MainCfgT;
+template <>
+struct MainCfgT<bf16> { using type = gemm::DCfg<256, 256, 2, 4, 2, 64>; };
+template <>
+struct MainCfgT<float> { using type = Cfg<float, 128, 128, 2, 2>; };
+template <typename TI>
+using MainCfg = typename MainCfgT<TI>::type;
+
 inline int64_t round_up(int64_t x, int64_t m) { return (x + m - 1) / m * m; }
 inline size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 

@@ -9,7 +9,8 @@
 // reads each block's shader clock from its stamps, so that the GEMM kernels
 // can be set against what the MFMA pipes reach on this box.  A measurement
 // aid only; no op of the library calls it.
-#include "gemm_core.h"
+#include "../gemm_core.h"
+#include "../../../include/nuvla_forge_measure.h"
 
 namespace nf {
 namespace {

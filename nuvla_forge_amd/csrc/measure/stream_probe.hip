@@ -9,7 +9,8 @@
 // each row kernel can be set against what plain streaming reaches on the
 // same box, the same bytes and the same cache state.  A measurement aid
 // only; no op of the library calls it.
-#include "nf_device.h"
+#include "../nf_device.h"
+#include "../../../include/nuvla_forge_measure.h"
 
 namespace nf {
 namespace {

@@ -16,37 +16,60 @@ import numpy as np
 import pytest
 import torch
 
-from nuvla_forge_amd import _lib
+from nuvla_forge_amd import _lib, _measure
 from nuvla_forge_amd import kernels as K
 from nuvla_forge_amd.kernels import chunked_ce, reference
 from oracle import numerics as on
 
 ROOT = Path(__file__).resolve().parents[1]
-HEADERS = sorted((ROOT / "include").glob("*.h"))
+PRODUCT_HEADER = ROOT / "include" / "nuvla_forge_hip.h"
+MEASURE_HEADER = ROOT / "include" / "nuvla_forge_measure.h"
 
 NF_OK, NF_ERR_ARG, NF_ERR_DTYPE, NF_ERR_WORKSPACE = 0, -1, -2, -3
 FAKE = 4096  # a non-null pointer value; every call below returns before using it
 
 
-def _declared() -> set[str]:
-    names: set[str] = set()
-    for h in HEADERS:
-        text = re.sub(r"/\*.*?\*/", "", h.read_text(), flags=re.S)
-        names |= set(re.findall(r"\b(nf_\w+)\s*\(", text))
-    return names
+def _declared(header: Path) -> set[str]:
+    text = re.sub(r"/\*.*?\*/", "", header.read_text(), flags=re.S)
+    return set(re.findall(r"\b(nf_\w+)\s*\(", text))
 
 
 def _err() -> str:
     return _lib.lib().nf_last_error().decode()
 
 
+def _exported(path: Path) -> set[str]:
+    """Dynamic symbols a shared library defines (nm -D --defined-only)."""
+    import shutil
+    import subprocess
+
+    nm = shutil.which("nm")
+    if nm is None:
+        pytest.skip("no nm")
+    out = subprocess.run([nm, "-D", "--defined-only", str(path)], capture_output=True,
+                         text=True, check=True).stdout
+    return {ln.split()[-1] for ln in out.splitlines() if ln.split()}
+
+
 def test_library_exports_every_declared_symbol():
-    declared = _declared()
-    assert len(declared) >= 10, declared
-    raw = ctypes.CDLL(str(_lib.LIB_PATH))
-    missing = [n for n in sorted(declared) if not hasattr(raw, n)]
-    assert not missing, f"not exported: {missing}"
-    assert declared == set(_lib.SIGNATURES), "ctypes signature table out of sync with the header"
+    """Every include/*.h header belongs to one library: the product header to
+    libnf_hip.so, the measurement header to libnf_measure.so; each library
+    exports what its header declares, each ctypes table matches its header,
+    and the product library exports no nf_ entry point beyond its header."""
+    headers = sorted((ROOT / "include").glob("*.h"))
+    assert headers == sorted([PRODUCT_HEADER, MEASURE_HEADER]), headers
+    for header, path, table in ((PRODUCT_HEADER, _lib.LIB_PATH, _lib.SIGNATURES),
+                                (MEASURE_HEADER, _measure.LIB_PATH, _measure.SIGNATURES)):
+        declared = _declared(header)
+        assert declared, header
+        raw = ctypes.CDLL(str(path))
+        missing = [n for n in sorted(declared) if not hasattr(raw, n)]
+        assert not missing, f"{path.name} does not export {missing}"
+        assert declared == set(table), f"ctypes table out of sync with {header.name}"
+    product = {n for n in _exported(_lib.LIB_PATH) if n.startswith("nf_")}
+    assert product == _declared(PRODUCT_HEADER), product ^ _declared(PRODUCT_HEADER)
+    assert not _declared(PRODUCT_HEADER) & _declared(MEASURE_HEADER)
+    assert len(_declared(PRODUCT_HEADER)) >= 10
 
 
 def test_header_is_c_and_the_c_program_links_the_library():
@@ -58,11 +81,13 @@ def test_header_is_c_and_the_c_program_links_the_library():
     gcc = shutil.which("gcc")
     if gcc is None:
         pytest.skip("no gcc")
-    src = '#include "nuvla_forge_hip.h"\nint main(void) { return nf_abi_version() != NF_ABI_VERSION; }\n'
-    res = subprocess.run([gcc, "-std=c99", "-Wall", "-Wextra", "-Werror", "-fsyntax-only",
-                          f"-I{ROOT / 'include'}", "-x", "c", "-"], input=src,
-                         capture_output=True, text=True)
-    assert res.returncode == 0, res.stderr
+    for header in ("nuvla_forge_hip.h", "nuvla_forge_measure.h"):
+        src = (f'#include "{header}"\n'
+               'int main(void) { return nf_abi_version() != NF_ABI_VERSION; }\n')
+        res = subprocess.run([gcc, "-std=c99", "-Wall", "-Wextra", "-Werror", "-fsyntax-only",
+                              f"-I{ROOT / 'include'}", "-x", "c", "-"], input=src,
+                             capture_output=True, text=True)
+        assert res.returncode == 0, (header, res.stderr)
     exe = ROOT / "tests" / "c" / "abi_smoke"
     assert exe.exists(), "tests/c/abi_smoke is built by nuvla_forge_amd.build"
     ldd = subprocess.run(["ldd", str(exe)], capture_output=True, text=True).stdout
@@ -231,8 +256,9 @@ def test_ce_argument_validation():
     assert L.nf_ce_workspace(4096, 1 << 40, 32000, 4096, 1) == 0
     assert L.nf_ce_fwd(FAKE, FAKE, FAKE, 16, 1 << 40, 50, -100, 64, 1, FAKE, None, FAKE, 1 << 20,
                        FAKE, 1 << 20, None) == NF_ERR_ARG and "2^40" in _err()
-    assert L.nf_gemm_nt(FAKE, 1 << 40, FAKE, 1 << 40, FAKE, 16, 16, 16, 1 << 40, 1,
-                        None) == NF_ERR_ARG and "int32" in _err()
+    M_ = _measure.lib()
+    assert M_.nf_gemm_nt(FAKE, 1 << 40, FAKE, 1 << 40, FAKE, 16, 16, 16, 1 << 40, 1,
+                         None) == NF_ERR_ARG and "int32" in _err()
     ws = L.nf_ce_workspace(16, 8, 50, 64, 1)
     base = [FAKE, FAKE, FAKE]
     out = [FAKE, FAKE, FAKE, None, FAKE]
@@ -256,13 +282,13 @@ def test_ce_argument_validation():
     assert L.nf_ce_bwd(*bwd[:9], 7, *bwd[10:]) == NF_ERR_DTYPE  # gradient dtype
     assert L.nf_ce_bwd(*bwd[:6], sb - 1, *bwd[7:]) == NF_ERR_WORKSPACE
     assert L.nf_ce_bwd(*bwd[:13], bws - 1, None) == NF_ERR_WORKSPACE
-    assert L.nf_gemm_nt(FAKE, 4, FAKE, 4, FAKE, 2, 2, 2, 8, 1, None) == NF_ERR_ARG  # lda < K
+    assert M_.nf_gemm_nt(FAKE, 4, FAKE, 4, FAKE, 2, 2, 2, 8, 1, None) == NF_ERR_ARG  # lda < K
 
 
 def test_stream_probe_argument_validation():
     """The streaming-ceiling entry point refuses what it cannot run before
     any launch (no GPU needed); n16 = 0 is a no-op."""
-    L = _lib.lib()
+    L = _measure.lib()
     ptrs = [FAKE] * 6
     assert L.nf_stream_probe(3, 1, *ptrs, 16, None) == NF_ERR_ARG and "(3, 1)" in _err()
     assert L.nf_stream_probe(4, 1, *ptrs, 16, None) == NF_ERR_ARG
@@ -277,7 +303,7 @@ def test_stream_probe_argument_validation():
 def test_mfma_probe_argument_validation():
     """The MFMA-ceiling entry point refuses bad sizes and pointers before any
     launch (no GPU needed)."""
-    L = _lib.lib()
+    L = _measure.lib()
     assert L.nf_mfma_probe(FAKE, -1, 1, FAKE, None, None) == NF_ERR_ARG and "iters" in _err()
     assert L.nf_mfma_probe(FAKE, 2**30 + 1, 1, FAKE, None, None) == NF_ERR_ARG
     assert L.nf_mfma_probe(FAKE, 1, 0, FAKE, None, None) == NF_ERR_ARG and "blocks" in _err()

@@ -16,7 +16,7 @@ import numpy as np
 import pytest
 import torch
 
-from nuvla_forge_amd import _lib
+from nuvla_forge_amd import _lib, _measure
 from nuvla_forge_amd.kernels import chunked_cross_entropy
 from oracle import numerics as on
 from tests.helpers import TOL, gen, note, np64, randn
@@ -33,7 +33,7 @@ def test_gemm_nt_matches_numpy(cuda, dtype, m, n, k):
     a = randn((m, k), g, dtype, cuda)
     b = randn((n, k), g, dtype, cuda)
     c = torch.full((m, n), float("nan"), device=cuda)
-    L = _lib.lib()
+    L = _measure.lib()
     _lib.check(L.nf_gemm_nt(a.data_ptr(), k, b.data_ptr(), k, c.data_ptr(), n, m, n, k,
                             _lib.dtype_code(dtype), _lib.stream_of(a)), "nf_gemm_nt")
     torch.cuda.synchronize()
@@ -47,7 +47,7 @@ def test_gemm_nt_leading_dimensions(cuda):
     base_a = randn((100, 96), g, torch.bfloat16, cuda)
     base_b = randn((70, 80), g, torch.bfloat16, cuda)
     c = torch.zeros(100, 90, device=cuda)
-    L = _lib.lib()
+    L = _measure.lib()
     # A = base_a[:, 8:72] (lda 96), B = base_b[:, 16:80] (ldb 80), C = c[:, :70] (ldc 90)
     _lib.check(L.nf_gemm_nt(base_a[:, 8:].data_ptr(), 96, base_b[:, 16:].data_ptr(), 80,
                             c.data_ptr(), 90, 100, 70, 64, 1, _lib.stream_of(c)), "nf_gemm_nt")
@@ -68,7 +68,7 @@ def test_gemm_nt_output_over_2gib(cuda):
     b = randn((n, k), g, torch.bfloat16, cuda)
     c = torch.full((m, n), float("nan"), device=cuda)
     assert c.numel() * 4 >= 2 ** 31
-    L = _lib.lib()
+    L = _measure.lib()
     _lib.check(L.nf_gemm_nt(a.data_ptr(), k, b.data_ptr(), k, c.data_ptr(), n, m, n, k,
                             _lib.dtype_code(torch.bfloat16), _lib.stream_of(a)), "nf_gemm_nt")
     want = a.float() @ b.float().T
@@ -138,10 +138,11 @@ def test_ce_all_ignored_is_zero(cuda):
 @pytest.mark.parametrize("chunk", [64, 4096])
 def test_ce_rows_far_from_their_reference(cuda, dtype, chunk):
     """Logits of standard deviation ~32 in every other row (hidden rows
-    N(0, 1) x 4, weights N(0, 1)), so that in about a third of the rows the
-    largest logit lies more than 75 above the target logit: E is stored relative to
-    the target logit, and those rows leave its exponent range and go through
-    the exact recomputation; the others keep the fast path.  Against the fp64
+    N(0, 1) x 4, weights N(0, 1)), so that in about half of the rows the loss
+    plus ln n exceeds 65 nats: E is stored relative to the target logit and
+    scaled by a per-row factor exp(mref - lse) / n, and those rows would
+    leave the exponent range, so they go through the exact recomputation;
+    the others (loss + ln n under 55) keep the fast path.  Against the fp64
     oracle on the same rounded inputs.  Tolerances: bf16 2e-2; fp32 1e-4,
     because an fp32 logit of magnitude ~100 carries an absolute rounding
     error of ~1e-5, which exp turns into a relative error of the same size in
@@ -158,12 +159,53 @@ def test_ce_rows_far_from_their_reference(cuda, dtype, chunk):
     logits = np64(hid) @ np64(w).T
     valid = (tgt != -100).cpu().numpy()
     tcol = np.where(valid, tgt.cpu().numpy(), 0)
-    gap = logits.max(axis=1) - logits[np.arange(m), tcol]
-    assert (gap[valid] > 80).sum() >= 0.3 * valid.sum()  # the recomputation is exercised
-    assert (gap[valid] < 70).sum() >= 0.2 * valid.sum()  # and so is the fast path
+    mx = logits.max(axis=1)
+    lse = mx + np.log(np.exp(logits - mx[:, None]).sum(axis=1))
+    crit = (lse - logits[np.arange(m), tcol] + np.log(valid.sum()))[valid]
+    assert (crit > 65).sum() >= 0.3 * valid.sum()  # the recomputation is exercised
+    assert (crit < 55).sum() >= 0.3 * valid.sum()  # and so is the fast path
     loss, dh, dw = _run_ce(hid, w, tgt, chunk)
     tol = 2e-2 if dtype == torch.bfloat16 else 1e-4
     _check_ce(hid, w, tgt, loss, dh, dw, tol, f"far rows {dtype} chunk {chunk}")
+
+
+@pytest.mark.parametrize("chunk", [1024, 4096])
+def test_ce_tiny_row_factor_keeps_its_weight_gradient(cuda, chunk):
+    """bf16, n = 4096 valid rows, and 32 rows whose largest logit lies only
+    74.5 above the target's but whose loss is ~82.8 nats (4080 logits share
+    that maximum).  On the fast path such a row's factor exp(mref - lse) / n
+    is ~3e-40, below bf16's normal range, and its share of the dW operand
+    (factor x hidden row, rounded to bf16) would vanish while its dH stayed
+    right; the criterion (loss + ln n above 60 nats: recompute) keeps it.
+    The 32 rows are the only ones with a nonzero hidden column 0, so dW[:, 0]
+    is their contribution alone, checked on its own besides dH row by row."""
+    note(f"ce tiny row factor bf16 m=4096 d=64 v=4096 chunk={chunk}")
+    m, d, v, nspec, nlow = 4096, 64, 4096, 32, 16
+    g = gen(41)
+    hid = torch.randn(m, d, generator=g)
+    hid[:, 0] = 0.0
+    spec = torch.randperm(m, generator=g)[:nspec]
+    hid[spec] = 0.0
+    hid[spec, 0] = 1.0
+    w = torch.randn(v, d, generator=g) * 0.05
+    w[:, 0] = 74.5  # bf16-exact
+    low = torch.randperm(v, generator=g)[:nlow]
+    w[low, 0] = 0.0
+    tgt = torch.randint(0, v, (m,), generator=g)
+    tgt[spec] = low[torch.randint(0, nlow, (nspec,), generator=g)]
+    hid, w = hid.to(torch.bfloat16).to(cuda), w.to(torch.bfloat16).to(cuda)
+    tgt = tgt.to(cuda)
+    loss, dh, dw = _run_ce(hid, w, tgt, chunk)
+    lo, dho, dwo = on.ce_forward_backward(np64(hid), np64(w), tgt.cpu().numpy())
+    rows = spec.numpy()
+    logits = np64(hid)[rows] @ np64(w).T
+    row_loss = np.log(np.exp(logits - logits.max(1, keepdims=True)).sum(1)) + logits.max(1)
+    assert np.all(row_loss > 82) and np.all(row_loss < 84)  # fast path before the criterion
+    assert abs(float(loss) - lo) / lo < 2e-2
+    assert on.rel_err(np64(dw)[:, 0], dwo[:, 0]) < 2e-2, "the 32 rows' dW share"
+    for r in rows:
+        assert on.rel_err(np64(dh)[r], dho[r]) < 2e-2, f"dH row {r}"
+    assert on.rel_err(np64(dh), dho) < 2e-2 and on.rel_err(np64(dw), dwo) < 2e-2
 
 
 @pytest.mark.parametrize("dtype,chunk", [(torch.bfloat16, 128), (torch.bfloat16, 4096),
@@ -318,9 +360,18 @@ def test_ce_fp32_hidden_and_lm_head_under_autocast_compute_in_bf16(cuda):
     assert abs(float(loss.detach()) - lo) < abs(float(loss.detach()) - lo32)
 
 
-def test_ce_cfg4_bf16_full_size_and_deterministic(cuda):
-    """BASELINE cfg4: bf16 M4096 D2048 V32000, 409 rows ignored (M_valid 3687)."""
-    note("ce cfg4 bf16 M4096 D2048 V32000")
+_CFG4_ORACLE: dict = {}
+
+
+@pytest.mark.parametrize("chunk", [1024, 4096])
+def test_ce_cfg4_bf16_full_size_and_deterministic(cuda, chunk):
+    """BASELINE cfg4: bf16 M4096 D2048 V32000, 409 rows ignored (M_valid 3687).
+
+    chunk_size 1024 is the reference's default (four row chunks here, the
+    fp32 dW accumulator between them); 4096 is one chunk over all valid rows,
+    the plan the benchmark also reports (the whole gradient product in the
+    backward launch, E and E^T of every valid row held)."""
+    note(f"ce cfg4 bf16 M4096 D2048 V32000 chunk={chunk}")
     m, d, v = 4096, 2048, 32000
     g = gen(2)
     hid = randn((m, d), gen(0), torch.bfloat16, cuda)
@@ -328,16 +379,46 @@ def test_ce_cfg4_bf16_full_size_and_deterministic(cuda):
     tgt = torch.randint(0, v, (m,), generator=g)
     tgt[torch.randperm(m, generator=g)[:409]] = -100
     tgt = tgt.to(cuda)
-    loss, dh, dw = _run_ce(hid, w, tgt, 1024)  # the default: 1024-row chunks, four here
-    loss2, dh2, dw2 = _run_ce(hid, w, tgt, 1024)
+    loss, dh, dw = _run_ce(hid, w, tgt, chunk)
+    loss2, dh2, dw2 = _run_ce(hid, w, tgt, chunk)
     assert torch.equal(loss, loss2) and torch.equal(dh, dh2) and torch.equal(dw, dw2)
-    H = hid.float().cpu().numpy()
-    W = w.float().cpu().numpy()
-    lo, dho, dwo = on.ce_forward_backward(H, W, tgt.cpu().numpy())
+    if "ref" not in _CFG4_ORACLE:  # the same inputs for both chunk sizes
+        H = hid.float().cpu().numpy()
+        W = w.float().cpu().numpy()
+        _CFG4_ORACLE["ref"] = on.ce_forward_backward(H, W, tgt.cpu().numpy())
+    lo, dho, dwo = _CFG4_ORACLE["ref"]
     assert abs(float(loss.detach()) - lo) / lo < 2e-2
     assert on.rel_err(dh.float().cpu().numpy(), dho) < 2e-2
     assert on.rel_err(dw.float().cpu().numpy(), dwo) < 2e-2
     assert np.all(dh.float().cpu().numpy()[(tgt == -100).cpu().numpy()] == 0)
+
+
+def test_ce_state_is_released_after_backward(cuda):
+    """The state nf_ce_fwd leaves for nf_ce_bwd (E in both layouts, W^T, the
+    scaled Hc^T, fp32 dH rows, the fp32 dW accumulator) is saved through
+    save_for_backward, so autograd frees it once the backward has run, while
+    the caller still holds ``loss`` (a training loop keeping the previous
+    step's loss for logging must not carry two states)."""
+    note("ce state released after backward")
+    m, d, v = 1024, 256, 8192
+    g = gen(31)
+    hid = randn((m, d), g, torch.bfloat16, cuda).requires_grad_(True)
+    w = randn((v, d), g, torch.bfloat16, cuda, std=0.05).requires_grad_(True)
+    tgt = torch.randint(0, v, (m,), generator=g).to(cuda)
+    L = _lib.lib()
+    state_bytes = L.nf_ce_state_bytes(m, d, v, 256, _lib.dtype_code(torch.bfloat16))
+    assert state_bytes > 4 * 256 * v  # bf16 E and E^T of one 256-row chunk at least
+    loss = chunked_cross_entropy(hid, w, tgt, chunk_size=256)
+    torch.cuda.synchronize()
+    held = torch.cuda.memory_allocated()
+    loss.backward()
+    torch.cuda.synchronize()
+    grads = hid.grad.numel() * 2 + w.grad.numel() * 2
+    after = torch.cuda.memory_allocated()
+    assert after <= held + grads - state_bytes, (held, after, grads, state_bytes)
+    assert loss.grad_fn is not None  # loss still referenced
+    with pytest.raises(RuntimeError):
+        loss.backward()  # the saved state is gone: a second backward is refused
 
 
 def _reasoning_head_inputs(dev, seed=8):

@@ -9,7 +9,7 @@ from __future__ import annotations
 import pytest
 import torch
 
-from nuvla_forge_amd import _lib
+from nuvla_forge_amd import _lib, _measure
 from tests.helpers import note
 
 pytestmark = pytest.mark.gpu
@@ -19,7 +19,7 @@ pytestmark = pytest.mark.gpu
                                               (0.0, 3.0, 5, 1), (None, None, 4, 2)])
 def test_mfma_probe_values(cuda, a, b, iters, blocks):
     note(f"mfma probe a={a} b={b} iters={iters} blocks={blocks}")
-    L = _lib.lib()
+    L = _measure.lib()
     ops = None
     if a is not None:
         ops = torch.empty(16, 256, 8, dtype=torch.bfloat16, device=cuda)

@@ -9,7 +9,7 @@ from __future__ import annotations
 import pytest
 import torch
 
-from nuvla_forge_amd import _lib
+from nuvla_forge_amd import _lib, _measure
 from tests.helpers import note
 
 pytestmark = pytest.mark.gpu
@@ -25,7 +25,7 @@ def test_stream_probe_values(cuda, reads, writes, n16):
     outs = [torch.full((n16, 4), -1, dtype=torch.int32, device=cuda) for _ in range(writes)]
     ptrs = [t.data_ptr() for t in ins] + [None] * (4 - reads)
     ptrs += [t.data_ptr() for t in outs] + [None] * (2 - writes)
-    L = _lib.lib()
+    L = _measure.lib()
     _lib.check(L.nf_stream_probe(reads, writes, *ptrs, n16, _lib.stream_of(ins[0])),
                "nf_stream_probe")
     torch.cuda.synchronize()
