@@ -343,9 +343,9 @@ def bench_mfma_ceiling(args, dev, blocks=2048, iters=300):
     rate is the most any bf16 product of this build's data can reach."""
     import torch
 
-    from nuvla_forge_amd import _lib
+    from nuvla_forge_amd import _lib, _measure
 
-    L = _lib.lib()
+    L = _measure.lib()
     g = torch.Generator().manual_seed(60)
     ops = torch.randn(16, 256, 8, generator=g).to(torch.bfloat16).to(dev)
     out = torch.empty(blocks, 256, device=dev)
@@ -403,9 +403,9 @@ def stream_ceilings(args, dev, sizes=(("cfg2_16MiB", 16 << 20), ("cfg5_256MiB", 
     the row kernels meet inside a step).  Context, never the denominator."""
     import torch
 
-    from nuvla_forge_amd import _lib
+    from nuvla_forge_amd import _lib, _measure
 
-    L = _lib.lib()
+    L = _measure.lib()
     out = {}
     for label, nbytes in sizes:
         for r, w in ((2, 2), (4, 2)):
@@ -551,14 +551,18 @@ def bench_ce(args, dev):
                 "graph_matches_eager": same(ref, outs), "tokens_per_s": m / (ms * 1e-3),
                 "tflops": tflops, "mfma_frac": tflops / MFMA_BF16_PEAK_TFLOPS}
 
-    # BASELINE cfg4's "chunk 4096" as chunk_size (rows per chunk: one chunk
-    # of the 3687 valid rows here, holding what the reference's own
-    # [4096, V] fp32 logits tile holds at that setting) is the figure; the
-    # reference's default 1024 and 2048 (four and two chunks, each extra
-    # chunk one more fp32 pass over dW) beside it
-    main = run(4096)
+    # The figure of record is the reference's default chunk_size 1024 (rows
+    # per chunk, chunked_ce.py:189: four chunks of the 3687 valid rows here,
+    # one [1024, V] tile's worth of E and E^T at a time, the fp32 dW
+    # accumulator between chunks).  Beside it 2048 and 4096; 4096 is one
+    # chunk over every valid row, so it holds E and E^T of all 3687 rows
+    # (2 x 236 MB in bf16, what the reference's [4096, V] fp32 logits tile
+    # would hold at that setting): faster, but not the reference's memory
+    # bound at its default.
+    main = run(1024)
     return {"m": m, "d": d, "v": v, "m_valid": m_valid, "alg_flops": flops, **main,
-            "chunk_1024": run(1024), "chunk_2048": run(2048)}
+            "chunk_2048": run(2048),
+            "chunk_4096_one_chunk": {**run(4096), "holds": "E and E^T of every valid row"}}
 
 
 def bench_stress(args, dev):

@@ -31,7 +31,7 @@ import torch
 
 from .. import _lib
 from .reference import adaln_residual_rmsnorm_ref
-from .utils import device_of, use_fused
+from .utils import check_devices, device_of, use_fused
 
 MAX_N = 16384  # widest row the kernels take (the reference's own limit, :262)
 
@@ -58,6 +58,8 @@ class _FusedAdaLNResidualRMSNorm(torch.autograd.Function):
             raise ValueError(f"M={m} is not a multiple of tokens_per_sample={t}")
         if n > MAX_N:
             raise ValueError(f"N={n} exceeds {MAX_N}")
+        check_devices("fused_adaln_residual_rmsnorm", "x",
+                      dict(x=x, y=y, gate=gate, weight=weight, scale=scale, shift=shift))
         b = m // t
         x = _rows(x)
         y = _rows(y)
@@ -101,6 +103,8 @@ class _FusedAdaLNResidualRMSNorm(torch.autograd.Function):
         need = ctx.needs_input_grad
         if dh_up is None and dout is None:
             return (None,) * 8
+        check_devices("fused_adaln_residual_rmsnorm backward", "x",
+                      dict(x=x, dh_up=dh_up, dout=dout))
         dh_up = None if dh_up is None else dh_up.to(x.dtype).contiguous()
         dout = None if dout is None else dout.to(x.dtype).contiguous()
 

@@ -46,7 +46,7 @@ from __future__ import annotations
 import torch
 
 from .. import _lib
-from .utils import device_of, use_fused
+from .utils import check_devices, device_of, use_fused
 
 # Opt-in: raise ValueError for targets outside [0, V) that are not
 # ignore_index.  The check reads one device int back to the host (a
@@ -114,17 +114,19 @@ def _forward_eager(hidden, lm_weight, targets, chunk_size, ignore_index):
 
 
 class _DeviceCall:
-    """What the two device calls share: the shape, the compute type and the
-    state nf_ce_fwd leaves for nf_ce_bwd."""
+    """What the two device calls share besides the state tensor: the shape
+    and the compute type.  The state (nf_ce_fwd's output, nf_ce_bwd's input)
+    travels through ``ctx.save_for_backward``, so autograd frees it once the
+    backward has run."""
 
     def __init__(self, m, d, v, chunk_rows, cdt):
         self.m, self.d, self.v, self.chunk_rows, self.cdt = m, d, v, chunk_rows, cdt
         self.code = _lib.dtype_code(cdt)
-        self.state = None
 
 
 def _forward_hip(hidden, lm_weight, targets, chunk_size, ignore_index):
-    """Loss and the call record for ``_backward_hip``."""
+    """(loss, call record, state) for ``_backward_hip``; state is None when
+    there are no rows."""
     m, d = hidden.shape
     v = lm_weight.shape[0]
     cdt = _compute_dtype(hidden, lm_weight)
@@ -132,7 +134,7 @@ def _forward_hip(hidden, lm_weight, targets, chunk_size, ignore_index):
     dev = hidden.device
     loss = torch.empty((), dtype=torch.float32, device=dev)
     if m == 0:
-        return loss.zero_(), call
+        return loss.zero_(), call, None
     h = hidden.to(cdt).contiguous()
     w = lm_weight.to(cdt).contiguous()
     tg = targets.to(torch.int64).contiguous()
@@ -144,13 +146,13 @@ def _forward_hip(hidden, lm_weight, targets, chunk_size, ignore_index):
     ws_bytes = L.nf_ce_fwd_workspace(*shape)
     if not st_bytes or not ws_bytes:
         raise ValueError(f"chunked_cross_entropy: shape M={m} D={d} V={v} is beyond the kernels")
-    call.state = torch.empty(st_bytes, dtype=torch.uint8, device=dev)
+    state = torch.empty(st_bytes, dtype=torch.uint8, device=dev)
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
     with device_of(hidden):
         _lib.check(
             L.nf_ce_fwd(h.data_ptr(), w.data_ptr(), tg.data_ptr(), m, d, v, int(ignore_index),
                         call.chunk_rows, call.code, loss.data_ptr(), _lib.ptr(bad),
-                        call.state.data_ptr(), st_bytes, ws.data_ptr(), ws_bytes,
+                        state.data_ptr(), st_bytes, ws.data_ptr(), ws_bytes,
                         _lib.stream_of(hidden)),
             "nf_ce_fwd",
         )
@@ -159,11 +161,13 @@ def _forward_hip(hidden, lm_weight, targets, chunk_size, ignore_index):
         if nbad:
             raise ValueError(f"chunked_cross_entropy: {nbad} target(s) outside [0, {v}) "
                              f"and not ignore_index={ignore_index}")
-    return loss, call
+    return loss, call, state
 
 
-def _backward_hip(call, grad_output, hidden_dtype, weight_dtype, dev):
+def _backward_hip(call, state, grad_output, hidden_dtype, weight_dtype, dev):
     """(grad_output * dL/dhidden, grad_output * dL/dweight) in the inputs' dtypes."""
+    check_devices("chunked_cross_entropy backward", "the forward's hidden",
+                  {"grad_output": grad_output}, device=dev)
     m, d, v = call.m, call.d, call.v
     dh = torch.empty((m, d), dtype=hidden_dtype, device=dev)
     dw = torch.empty((v, d), dtype=weight_dtype, device=dev)
@@ -175,8 +179,8 @@ def _backward_hip(call, grad_output, hidden_dtype, weight_dtype, dev):
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
     with device_of(dh):
         _lib.check(
-            L.nf_ce_bwd(m, d, v, call.chunk_rows, call.code, call.state.data_ptr(),
-                        call.state.numel(), g.data_ptr(), dh.data_ptr(), _lib.dtype_code(dh),
+            L.nf_ce_bwd(m, d, v, call.chunk_rows, call.code, state.data_ptr(),
+                        state.numel(), g.data_ptr(), dh.data_ptr(), _lib.dtype_code(dh),
                         dw.data_ptr(), _lib.dtype_code(dw), ws.data_ptr(), ws_bytes,
                         _lib.stream_of(dh)),
             "nf_ce_bwd",
@@ -192,6 +196,8 @@ class _ChunkedCrossEntropy(torch.autograd.Function):
                              f"{tuple(hidden.shape)} and {tuple(lm_weight.shape)}")
         if targets.shape != (hidden.shape[0],):
             raise ValueError(f"targets must be [M={hidden.shape[0]}], got {tuple(targets.shape)}")
+        check_devices("chunked_cross_entropy", "hidden",
+                      dict(hidden=hidden, lm_weight=lm_weight, targets=targets))
         ctx.hidden_dtype = hidden.dtype
         ctx.weight_dtype = lm_weight.dtype
         # the reference's rule (chunked_ce.py:133): the eager chunk loop for
@@ -202,7 +208,11 @@ class _ChunkedCrossEntropy(torch.autograd.Function):
                                                       ignore_index)
             ctx.save_for_backward(d_hidden, d_weight)
             return loss
-        loss, ctx.call = _forward_hip(hidden, lm_weight, targets, chunk_size, ignore_index)
+        loss, ctx.call, state = _forward_hip(hidden, lm_weight, targets, chunk_size,
+                                             ignore_index)
+        # through save_for_backward, not a ctx attribute: autograd releases
+        # the state (hundreds of MB at the BASELINE shape) after the backward
+        ctx.save_for_backward(state)
         ctx.device = hidden.device
         return loss
 
@@ -213,8 +223,9 @@ class _ChunkedCrossEntropy(torch.autograd.Function):
             g = grad_output
             return ((d_hidden * g).to(ctx.hidden_dtype), (d_weight * g).to(ctx.weight_dtype),
                     None, None, None, None)
-        dh, dw = _backward_hip(ctx.call, grad_output, ctx.hidden_dtype, ctx.weight_dtype,
-                               ctx.device)
+        (state,) = ctx.saved_tensors
+        dh, dw = _backward_hip(ctx.call, state, grad_output, ctx.hidden_dtype,
+                               ctx.weight_dtype, ctx.device)
         return dh, dw, None, None, None, None
 
 

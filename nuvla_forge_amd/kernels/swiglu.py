@@ -19,7 +19,7 @@ import torch.nn.functional as F
 
 from .. import _lib
 from .reference import swiglu_ref
-from .utils import device_of, use_fused
+from .utils import check_devices, device_of, use_fused
 
 
 def _check(a: torch.Tensor, b: torch.Tensor) -> None:
@@ -27,8 +27,7 @@ def _check(a: torch.Tensor, b: torch.Tensor) -> None:
         raise ValueError(f"fused_swiglu: shape mismatch {tuple(a.shape)} vs {tuple(b.shape)}")
     if a.dtype != b.dtype:
         raise TypeError(f"fused_swiglu: dtype mismatch {a.dtype} vs {b.dtype}")
-    if a.device != b.device:
-        raise ValueError("fused_swiglu: a and b are on different devices")
+    check_devices("fused_swiglu", "a", dict(a=a, b=b))
     _lib.dtype_code(a)
 
 
@@ -52,6 +51,7 @@ class _FusedSwiGLU(torch.autograd.Function):
     @staticmethod
     def backward(ctx, dout):
         a, b = ctx.saved_tensors
+        check_devices("fused_swiglu backward", "a", dict(a=a, dout=dout))
         dout = dout.contiguous()
         if dout.dtype != a.dtype:
             dout = dout.to(a.dtype)
@@ -79,6 +79,7 @@ class _FusedGateUpSwiGLU(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, x, w_gate, w_up):
+        check_devices("fused_gate_up_swiglu", "x", dict(x=x, w_gate=w_gate, w_up=w_up))
         m, d = x.shape
         h = w_gate.shape[0]
         a = torch.empty((m, h), dtype=torch.bfloat16, device=x.device)
@@ -99,6 +100,7 @@ class _FusedGateUpSwiGLU(torch.autograd.Function):
     @staticmethod
     def backward(ctx, dact):
         x, w_gate, w_up, a, b = ctx.saved_tensors
+        check_devices("fused_gate_up_swiglu backward", "x", dict(x=x, dact=dact))
         dact = dact.to(torch.bfloat16).contiguous()
         da, db = torch.empty_like(a), torch.empty_like(b)
         L = _lib.lib()

@@ -2,7 +2,8 @@
 outputs and gradients for the three ops, computed by torch fp64 autograd of
 the reference's eager formulation (oracle/torch_cpu.py).  The fixtures pin the
 NumPy oracle (tests/test_oracle.py::test_golden_fixtures) and double as
-seeded GPU parity cases.
+seeded GPU parity cases (tests/test_gpu_golden.py runs them through the
+fused ops in fp32).
 
     python tests/golden/make_golden.py
 """
