@@ -271,9 +271,11 @@ def bench_adaln(args, dev):
     graph_ok = graph_ok and same(ref, outs)
     del graph, outs
     graph1_ms, _, graph1 = time_graph(make, args.steps, args.warmup, 1)
-    cold_ms = cold_replay_ms(graph1, dev, max(5, args.steps // 2))
+    cold_1r_ms = cold_replay_ms(graph1, dev, max(5, args.steps // 2))
     cold_dirty_ms = cold_replay_ms(graph1, dev, max(5, args.steps // 2), dirty=True)
     del graph1
+    floor_ms = single_replay_floor_ms(dev, max(5, args.steps // 2))
+    cold_ms, flush_ms = cold_graph_ms(make, dev)
 
     # per-kernel durations: back-to-back launches of each C-ABI entry point
     kern_ms = adaln_kernel_ms(inp, t, dh, dout, args.steps)
@@ -289,7 +291,8 @@ def bench_adaln(args, dev):
     fwd_gbs = fwd_alg / (kern_ms["nf_adaln_fwd"] * 1e-3) / 1e9
     return {
         "b": b, "t": t, "n": n, "alg_bytes": alg, "graph_ms": graph_ms, "eager_ms": eager_ms,
-        "graph1_ms": graph1_ms, "cold_ms": cold_ms, "cold_dirty_ms": cold_dirty_ms,
+        "graph1_ms": graph1_ms, "cold_ms": cold_ms, "cold_1r_ms": cold_1r_ms,
+        "cold_dirty_ms": cold_dirty_ms, "single_replay_floor_ms": floor_ms, "flush_ms": flush_ms,
         "graph_matches_eager": graph_ok, "kernel_ms": kern_ms, "in_step_ms": instep_ms,
         "bwd_alg_bytes": bwd_alg, "bwd_gbs": bwd_gbs, "fwd_alg_bytes": fwd_alg, "fwd_gbs": fwd_gbs,
         "bwd_gbs_in_step": bwd_alg / (instep_ms["nf_adaln_bwd"] * 1e-3) / 1e9,
@@ -455,6 +458,56 @@ def cold_replay_ms(graph, dev, reps, dirty=False, flush_bytes=1 << 30):
     _sync()
     del flush
     return statistics.median(e0.elapsed_time(e1) for e0, e1 in pairs)
+
+
+def cold_graph_ms(make_step, dev, per_graph=5, replays=6, flush_bytes=1 << 30):
+    """Milliseconds per step with the caches cold, timed inside HIP graphs:
+    one graph holds `per_graph` x [a read-only pass over `flush_bytes` (4x the
+    256 MB Infinity Cache; nf_stream_probe's (1, 0) form), one step], a
+    second graph the same passes alone, and the difference per step is the
+    step after its operands left the L2s and the Infinity Cache.  Unlike
+    events around a one-step replay (cold_replay_ms) it carries no per-replay
+    launch or event cost; the step's own launches are in it, as in the
+    headline."""
+    import torch
+
+    from nuvla_forge_amd import _lib, _measure
+
+    M = _measure.lib()
+    buf = torch.ones(flush_bytes // 4, dtype=torch.int32, device=dev)
+    sink = torch.zeros(4, dtype=torch.int32, device=dev)
+
+    def flush():
+        _lib.check(M.nf_stream_probe(1, 0, buf.data_ptr(), None, None, None, sink.data_ptr(),
+                                     None, flush_bytes // 16, _lib.stream_of(buf)),
+                   "nf_stream_probe")
+
+    def make_with():
+        step = make_step()
+
+        def run():
+            flush()
+            return step()
+        return run
+
+    total = per_graph * replays
+    with_ms, _, g1 = time_graph(make_with, total, 2, per_graph)
+    del g1
+    flush_ms, _, g2 = time_graph(lambda: flush, total, 2, per_graph)
+    del g2, buf
+    return with_ms - flush_ms, flush_ms
+
+
+def single_replay_floor_ms(dev, reps):
+    """What cold_replay_ms reads for a one-kernel graph that moves nothing (a
+    64-element fill): the method's own cost of events around one replay."""
+    import torch
+
+    tiny = torch.zeros(64, device=dev)
+    _, _, graph = time_graph(lambda: (lambda: tiny.fill_(1.0)), 2, 2, 1)
+    ms = cold_replay_ms(graph, dev, reps)
+    del graph
+    return ms
 
 
 def adaln_in_step_ms(inp, t, dh, dout, steps, reps=10):
@@ -853,14 +906,19 @@ def main() -> int:
             "hbm_frac_whole_step": round(ad["gbs"] / HBM_PEAK_GBS, 4),
             "eager_ms_per_step": round(ad["eager_ms"], 5),
             "graph1_ms_per_step": round(ad["graph1_ms"], 5),
-            # one-step replays after a 1 GiB read pass has evicted the
-            # operands from the L2s and the Infinity Cache (HBM-resident
-            # inputs; compare graph1_ms_per_step), and after a 1 GiB
-            # read-modify-write pass whose dirty lines the step writes back
+            # the step with HBM-resident operands: inside HIP graphs, each
+            # step after a 1 GiB read-only pass that evicts its operands
+            # from the L2s and the Infinity Cache, minus the passes alone
             "cold_ms_per_step": round(ad["cold_ms"], 5),
-            "cold_dirty_ms_per_step": round(ad["cold_dirty_ms"], 5),
             "hbm_frac_cold_step": round(ad["alg_bytes"] / (ad["cold_ms"] * 1e-3) / 1e9
                                         / HBM_PEAK_GBS, 4),
+            # the same as events around single one-step replays after the
+            # pass (a 1 GiB read, or read-modify-write whose dirty lines the
+            # step writes back); single_replay_floor_ms is what that method
+            # reads for a 64-element fill kernel, its own fixed cost
+            "cold_single_replay_ms_per_step": round(ad["cold_1r_ms"], 5),
+            "cold_dirty_single_replay_ms_per_step": round(ad["cold_dirty_ms"], 5),
+            "single_replay_floor_ms": round(ad["single_replay_floor_ms"], 5),
             "graph_matches_eager": ad["graph_matches_eager"],
             "kernel_ms": {k: round(v, 5) for k, v in ad["kernel_ms"].items()},
             "in_step_kernel_ms": {k: round(v, 5) for k, v in ad["in_step_ms"].items()},

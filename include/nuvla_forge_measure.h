@@ -34,8 +34,11 @@ int nf_gemm_nt(const void *A, int64_t lda, const void *B, int64_t ldb,
  * ceiling bench.py sets the row kernels against.  Reads `reads` arrays
  * (in0..in3) and writes `writes` arrays (out0, out1) of n16 16-byte vectors
  * each, (reads, writes) one of (1, 1), (2, 2), (4, 2); out_w[i] = (in0[i]
- * xor ... xor in_{reads-1}[i]) + w in every 32-bit lane.  Pointers unused by
- * the (reads, writes) pair may be null; the others must be 16-byte aligned.
+ * xor ... xor in_{reads-1}[i]) + w in every 32-bit lane.  (1, 0) is a
+ * read-only pass over in0 that writes at most one vector, out0[0] (only for
+ * a marker value): a cache-evicting pass for cold-cache measurements.
+ * Pointers unused by the (reads, writes) pair may be null; the others must
+ * be 16-byte aligned.
  * ---------------------------------------------------------------------- */
 int nf_stream_probe(int reads, int writes, const void *in0, const void *in1,
                     const void *in2, const void *in3, void *out0, void *out1,

@@ -19,8 +19,8 @@
 // sample does not change.
 //
 // Backward.  Block (b, j) owns a contiguous run of rows of sample b; its G row
-// groups take every G-th row, again with the next row's four inputs loaded
-// before the current row is processed.  Each thread accumulates three
+// groups take every G-th row, with the next row's (or batch's) four inputs
+// loaded before the current one is processed.  Each thread accumulates three
 // per-column partials over its rows:
 //   A = sum dout * xhat,  S = sum dout,  G = sum dh * y
 // (dscale = weight * A, dshift = S, dgate = G, dweight = sum_b (1+scale_b) A_b);
@@ -408,23 +408,19 @@ struct BwdRow {
   Raw8<TY> y[K];
 };
 
-// RB > 1: rows are taken in batches of RB per row group, all their loads
-// issued before any math, the RB row dot products reduced with one LDS round
-// (PF is then unused).  The per-row arithmetic and the accumulation order are
-// those of RB = 1, so the results are bit-identical.
 // CL: the per-column conditioning factors (weight * (1 + scale), gate) sit in
 // LDS instead of registers, each thread reading back its own columns at the
 // start of every row (no barrier: nothing is shared).  For 1024-thread blocks
 // (16 wavefronts per row, 128 VGPRs per thread), whose registers cannot hold
 // them beside the row and the column partials.
 template <typename TX, typename TY, int K, int WPR, bool VEC, bool NT, bool PF, int MINB = 512,
-          int RB = 1, bool CL = false>
+          bool CL = false>
 __global__ __launch_bounds__((BwdShape<WPR, MINB>::BLK)) void adaln_bwd_kernel(
     BwdArgs p) {
   using S = BwdShape<WPR, MINB>;
-  static_assert(!CL || (RB == 1 && !PF), "LDS conditioning is for the one-row loop");
+  static_assert(!CL || !PF, "LDS conditioning is for the loop without prefetch");
   __shared__ __attribute__((aligned(16))) float cond[CL ? 2 * kMaxN : 1];
-  __shared__ float red[S::G * WPR * RB];
+  __shared__ float red[S::G * WPR];
   // combine buffer for the G row groups: (G - 1) x (R * K * 8) floats
   __shared__ float comb[S::G > 1 ? (S::G - 1) * S::R * K * 8 : 1];
 
@@ -498,62 +494,9 @@ __global__ __launch_bounds__((BwdShape<WPR, MINB>::BLK)) void adaln_bwd_kernel(
 
   const int64_t nrows = t1 > t0 ? t1 - t0 : 0;
   const int64_t iters = (nrows + S::G - 1) / S::G;
-  if constexpr (RB > 1) {
-    for (int64_t it = 0; it < iters; it += RB) {
-      BwdRow<TX, TY, K> rw[RB];
-      float rs[RB], dot[RB];
-#pragma unroll
-      for (int q = 0; q < RB; ++q) load_row(t0 + (it + q) * S::G + g, rw[q]);
-#pragma unroll
-      for (int q = 0; q < RB; ++q) {
-        const int64_t t = t0 + (it + q) * S::G + g;
-        rs[q] = t < t1 ? p.rstd[b * p.T + t] : 0.f;
-      }
-      float xh[RB][K][8];
-#pragma unroll
-      for (int q = 0; q < RB; ++q) {
-        dot[q] = 0.f;
-#pragma unroll
-        for (int k = 0; k < K; ++k)
-#pragma unroll
-          for (int i = 0; i < 8; ++i) {
-            xh[q][k][i] = (rw[q].x[k][i] + gv[k][i] * rw[q].y[k][i]) * rs[q];
-            dot[q] += (rw[q].dout[k][i] * wo[k][i]) * xh[q][k][i];
-          }
-      }
-      row_sum_batch<WPR, RB>(dot, red, g, rt);
-#pragma unroll
-      for (int q = 0; q < RB; ++q) {
-        const int64_t t = t0 + (it + q) * S::G + g;
-        const int64_t row = b * p.T + t;
-        const float c = dot[q] / (float)p.N;
-#pragma unroll
-        for (int k = 0; k < K; ++k) {
-          const int col = (k * S::R + rt) * 8;
-          const int valid = t < t1 ? chunk_valid(p.N, col) : 0;
-          if (valid > 0) {
-            float dh[8], dyv[8];
-#pragma unroll
-            for (int i = 0; i < 8; ++i) {
-              const float d = rw[q].dout[k][i];
-              dh[i] = rw[q].dh[k][i] + rs[q] * (d * wo[k][i] - xh[q][k][i] * c);
-              dyv[i] = dh[i] * gv[k][i];
-              accA[k][i] += d * xh[q][k][i];
-              accS[k][i] += d;
-              accG[k][i] += dh[i] * rw[q].y[k][i];
-            }
-            store8_hint<TX, VEC, NT>(static_cast<TX *>(p.dx) + row * (int64_t)p.N + col, valid,
-                                     dh);
-            store8_hint<TY, VEC, NT>(static_cast<TY *>(p.dy) + row * (int64_t)p.N + col, valid,
-                                     dyv);
-          }
-        }
-      }
-    }
-  }
   BwdRow<TX, TY, K> cur, nxt;
-  if (PF && RB == 1 && iters > 0) load_row(t0 + g, cur);
-  for (int64_t it = 0; RB == 1 && it < iters; ++it) {
+  if (PF && iters > 0) load_row(t0 + g, cur);
+  for (int64_t it = 0; it < iters; ++it) {
     const int64_t t = t0 + it * S::G + g;
     const bool active = t < t1;
     const int64_t row = b * p.T + t;
@@ -637,6 +580,148 @@ __global__ __launch_bounds__((BwdShape<WPR, MINB>::BLK)) void adaln_bwd_kernel(
 }
 
 // ---------------------------------------------------------------------------
+// backward, software-pipelined: the rows of block (b, j) as in
+// adaln_bwd_kernel (row group g takes rows t0 + g, t0 + g + G, ...), in
+// batches of RB per row group, with batch i + 1's loads issued before batch
+// i's math and stores (two register buffers in turn, the loop unrolled by
+// two).  Per-row arithmetic, accumulation order and the final combine are
+// adaln_bwd_kernel's, so the results are bit-identical to it.
+// Host conditions: 16-bit x and y, vector I/O, one 8-element chunk per lane.
+// ---------------------------------------------------------------------------
+template <typename TX, typename TY, int K, int RB>
+struct BwdBatch {
+  BwdRow<TX, TY, K> rw[RB];
+  float rs[RB];
+};
+
+template <typename TX, typename TY, int K, int WPR, bool NT, int RB>
+__global__ __launch_bounds__((BwdShape<WPR>::BLK)) void adaln_bwd_pipe_kernel(BwdArgs p) {
+  using S = BwdShape<WPR>;
+  __shared__ float red[S::G * WPR * RB];
+  __shared__ float comb[S::G > 1 ? (S::G - 1) * S::R * K * 8 : 1];
+
+  const int g = threadIdx.x / S::R;
+  const int rt = threadIdx.x % S::R;
+  const int64_t b = blockIdx.x / p.J;
+  const int j = blockIdx.x % p.J;
+  const int64_t t0 = (int64_t)j * p.rows_per_block;
+  int64_t t1 = t0 + p.rows_per_block;
+  if (t1 > p.T) t1 = p.T;
+
+  float wo[K][8], gv[K][8];
+#pragma unroll
+  for (int k = 0; k < K; ++k) {
+    const int col = (k * S::R + rt) * 8;
+    float wv[8], sv[8];
+    if (col < p.N) {
+      load8_dyn<true>(p.weight, p.dt_weight, col, 8, wv);
+      load8_dyn<true>(p.scale, p.dt_scale, b * p.ld_scale + col, 8, sv);
+      load8_dyn<true>(p.gate, p.dt_gate, b * p.ld_gate + col, 8, gv[k]);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) wv[i] = sv[i] = gv[k][i] = 0.f;
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) wo[k][i] = wv[i] * (1.f + sv[i]);
+  }
+
+  float accA[K][8], accS[K][8], accG[K][8];
+#pragma unroll
+  for (int k = 0; k < K; ++k)
+#pragma unroll
+    for (int i = 0; i < 8; ++i) accA[k][i] = accS[k][i] = accG[k][i] = 0.f;
+
+  const TX *const xp = static_cast<const TX *>(p.x);
+  const TY *const yp = static_cast<const TY *>(p.y);
+  const TX *const dop = static_cast<const TX *>(p.dout);
+  const TX *const dhp = static_cast<const TX *>(p.dh_up);
+  using VX = typename Raw8<TX>::vtype;
+  using VY = typename Raw8<TY>::vtype;
+
+  using Batch = BwdBatch<TX, TY, K, RB>;
+  auto load_batch = [&](int64_t it, Batch &bt) {
+#pragma unroll
+    for (int q = 0; q < RB; ++q) {
+      const int64_t t = t0 + (it + q) * S::G + g;
+      const int64_t row = b * p.T + t;
+      BwdRow<TX, TY, K> &rw = bt.rw[q];
+#pragma unroll
+      for (int k = 0; k < K; ++k) {
+        const int col = (k * S::R + rt) * 8;
+        if (t < t1 && col < p.N) {
+          rw.x[k].v = *reinterpret_cast<const VX *>(xp + row * p.ld_x + col);
+          rw.y[k].v = *reinterpret_cast<const VY *>(yp + row * p.ld_y + col);
+          if (dop) rw.dout[k].v = *reinterpret_cast<const VX *>(dop + row * (int64_t)p.N + col);
+          else rw.dout[k].zero();
+          if (dhp) rw.dh[k].v = *reinterpret_cast<const VX *>(dhp + row * (int64_t)p.N + col);
+          else rw.dh[k].zero();
+        } else {
+          rw.x[k].zero(); rw.y[k].zero(); rw.dout[k].zero(); rw.dh[k].zero();
+        }
+      }
+      bt.rs[q] = t < t1 ? p.rstd[row] : 0.f;
+    }
+  };
+  auto work_batch = [&](int64_t it, const Batch &bt) {
+    float xh[RB][K][8], dot[RB];
+#pragma unroll
+    for (int q = 0; q < RB; ++q) {
+      dot[q] = 0.f;
+#pragma unroll
+      for (int k = 0; k < K; ++k)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          xh[q][k][i] = (bt.rw[q].x[k][i] + gv[k][i] * bt.rw[q].y[k][i]) * bt.rs[q];
+          dot[q] += (bt.rw[q].dout[k][i] * wo[k][i]) * xh[q][k][i];
+        }
+    }
+    row_sum_batch<WPR, RB>(dot, red, g, rt);
+#pragma unroll
+    for (int q = 0; q < RB; ++q) {
+      const int64_t t = t0 + (it + q) * S::G + g;
+      const int64_t row = b * p.T + t;
+      const float c = dot[q] / (float)p.N;
+#pragma unroll
+      for (int k = 0; k < K; ++k) {
+        const int col = (k * S::R + rt) * 8;
+        if (t < t1 && col < p.N) {
+          float dh[8], dyv[8];
+#pragma unroll
+          for (int i = 0; i < 8; ++i) {
+            const float d = bt.rw[q].dout[k][i];
+            dh[i] = bt.rw[q].dh[k][i] + bt.rs[q] * (d * wo[k][i] - xh[q][k][i] * c);
+            dyv[i] = dh[i] * gv[k][i];
+            accA[k][i] += d * xh[q][k][i];
+            accS[k][i] += d;
+            accG[k][i] += dh[i] * bt.rw[q].y[k][i];
+          }
+          store8_hint<TX, true, NT>(static_cast<TX *>(p.dx) + row * (int64_t)p.N + col, 8, dh);
+          store8_hint<TY, true, NT>(static_cast<TY *>(p.dy) + row * (int64_t)p.N + col, 8, dyv);
+        }
+      }
+    }
+  };
+
+  const int64_t nrows = t1 > t0 ? t1 - t0 : 0;
+  const int64_t iters = (nrows + S::G - 1) / S::G;  // the same in every row group
+  Batch A, B;
+  if (iters > 0) load_batch(0, A);
+  for (int64_t it = 0; it < iters; it += 2 * RB) {
+    if (it + RB < iters) load_batch(it + RB, B);
+    work_batch(it, A);
+    if (it + RB < iters) {
+      if (it + 2 * RB < iters) load_batch(it + 2 * RB, A);
+      work_batch(it + RB, B);
+    }
+  }
+
+  float *dst = p.partial + (int64_t)blockIdx.x * 3 * p.N;
+  combine_store<K, S::G, S::R, true>(accA, comb, g, rt, dst, p.N);
+  combine_store<K, S::G, S::R, true>(accS, comb, g, rt, dst + p.N, p.N);
+  combine_store<K, S::G, S::R, true>(accG, comb, g, rt, dst + 2 * (int64_t)p.N, p.N);
+}
+
+// ---------------------------------------------------------------------------
 // planning
 // ---------------------------------------------------------------------------
 struct Plan {
@@ -645,6 +730,7 @@ struct Plan {
   int fwd_rpg;  // forward: contiguous rows per row group
   int bwd_wpr;  // backward: wavefronts per row (1, 2, 4, 8, 16)
   int bwd_k;    // backward: 8-element chunks per thread (1, 2)
+  int bwd_rb;   // pipelined backward (16-bit rows, one chunk per lane): rows per batch
   int J;        // backward blocks per sample
   int rows_per_block;
   int64_t B;
@@ -659,12 +745,17 @@ struct Plan {
 // Forward: each row group walks clamp(M / 2048, 1, 8) consecutive rows
 // (clamp(M / 256, 1, 8) for rows of 8 or more wavefronts).
 // Backward: ~256 blocks of 512 threads (1 per CU), each a run of one
-// sample's rows; with 16-bit rows every row group keeps 4 rows in flight
-// (adaln_bwd_kernel RB = 4), which hides the latency the 2-per-CU launch
-// hid, and the partial rows (B * J * 3 * N floats written, then reduced)
-// are half those of 512 blocks.  bf16 [8192, 1024]: 18.8 us for RB = 4 with
-// 32 blocks per sample against 19.4 us for RB = 1 with 64.
+// sample's rows, so the partial rows (B * J * 3 * N floats written, then
+// reduced) are half those of 512 blocks.  16-bit rows of one chunk per lane
+// take the pipelined kernel (adaln_bwd_pipe_kernel): batches of 2 rows per
+// row group when a row group has at most 16 rows, of 1 row beyond (A/B on
+// one box, fwd -> bwd -> reduce step, bit-identical): bf16 [8192, 1024]
+// (8 rows per row group) 35.4 us with 2-row batches, 36.1 with 1-row, 36.3
+// for the one-round kernel with 4-row batches it replaces; bf16 [65536,
+// 2048] (128 rows per row group) 489 us with 1-row batches, 516 with
+// 2-row, 503 one-round.  512 blocks lost at both shapes (38.4-39.7 us).
 constexpr int kBwdBlocksTarget = 256;
+constexpr int kBwdRb2MaxRows = 16;
 // A cap on the blocks (and so the partial rows) per sample: past it more
 // blocks only add partial rows for the reduction to read.
 constexpr int kMaxBlocksPerSample = 1024;
@@ -688,9 +779,19 @@ inline int pick_k(int64_t N, int wpr) {
   return k <= 1 ? 1 : (k <= 2 ? 2 : 4);
 }
 
-inline Plan make_plan(int64_t M, int64_t N, int64_t T, int fwd_groups = kFwdGroupsTarget,
-                      int bwd_blocks = kBwdBlocksTarget) {
+// Launch choices make_plan takes from its caller; the defaults are the
+// shipped plan (a measurement build sweeps them).
+struct Knobs {
+  int fwd_groups = kFwdGroupsTarget;  // forward row groups aimed at
+  int bwd_blocks = kBwdBlocksTarget;  // backward blocks aimed at
+  int fwd_rpg = 0;  // rows per forward row group (0: M / fwd_groups, capped)
+  int bwd_rb = 0;   // pipelined backward rows per batch, 1 or 2 (0: planned)
+};
+
+inline Plan make_plan(int64_t M, int64_t N, int64_t T, const Knobs &kn = Knobs()) {
   Plan pl{};
+  int fwd_groups = kn.fwd_groups;
+  const int bwd_blocks = kn.bwd_blocks;
   pl.fwd_wpr = pick_wpr(N, 2);
   if (N >= 1024 && pl.fwd_wpr < 2) pl.fwd_wpr = 2;
   pl.fwd_k = pick_k(N, pl.fwd_wpr);
@@ -700,6 +801,7 @@ inline Plan make_plan(int64_t M, int64_t N, int64_t T, int fwd_groups = kFwdGrou
     if (rpg > kFwdMaxRowsPerGroup) rpg = kFwdMaxRowsPerGroup;
     pl.fwd_rpg = (int)(rpg < 1 ? 1 : rpg);
   }
+  if (kn.fwd_rpg > 0) pl.fwd_rpg = kn.fwd_rpg;
   // One chunk per lane up to N = 4096 (8 wavefronts); wider rows take two
   // chunks per lane, so rows up to 8192 stay on 512-thread blocks (256
   // VGPRs, no spills: bf16 [1024, 8192] backward 24.5 us) instead of
@@ -717,6 +819,8 @@ inline Plan make_plan(int64_t M, int64_t N, int64_t T, int fwd_groups = kFwdGrou
   if (J < 1) J = 1;
   pl.rows_per_block = (int)((T + J - 1) / J);
   pl.J = (int)((T + pl.rows_per_block - 1) / pl.rows_per_block);
+  const int64_t group_rows = (pl.rows_per_block + G - 1) / G;
+  pl.bwd_rb = kn.bwd_rb > 0 ? (kn.bwd_rb >= 2 ? 2 : 1) : (group_rows <= kBwdRb2MaxRows ? 2 : 1);
   return pl;
 }
 
@@ -761,27 +865,30 @@ int launch_fwd_t(const FwdArgs &a, const Plan &pl, hipStream_t s) {
   adaln_fwd_kernel<TX, TY, K, WPR, VEC, kFwdNT><<<fwd_grid<S>(pl, a.M), S::BLK, 0, s>>>(a);
   return check_launch("nf_adaln_fwd");
 }
-// Backward rows in flight per row group: 4 for 16-bit rows of one 8-element
-// chunk per thread, else 1 (with the next-row prefetch when a thread holds
-// two chunks per row).
+// The pipelined backward takes 16-bit rows of one 8-element chunk per lane
+// on the vector path; the others run adaln_bwd_kernel one row at a time
+// (with the next-row prefetch when a thread holds two chunks per row).
 template <typename TX, typename TY, int K>
-constexpr int bwd_batch_rows() {
-  return (sizeof(TX) == 2 && sizeof(TY) == 2 && K == 1) ? 4 : 1;
+constexpr bool bwd_pipelined() {
+  return sizeof(TX) == 2 && sizeof(TY) == 2 && K == 1;
 }
 template <typename TX, typename TY, bool VEC, int WPR, int K>
-int launch_bwd_t(const BwdArgs &a, int64_t B, hipStream_t s) {
+int launch_bwd_t(const BwdArgs &a, const Plan &pl, hipStream_t s) {
   using S = BwdShape<WPR>;
-  const unsigned grid = (unsigned)(B * a.J);
-  constexpr int RB = VEC ? bwd_batch_rows<TX, TY, K>() : 1;
-  // The next-row prefetch needs a second row of registers; 1024-thread
-  // blocks (16 wavefronts per row, N > 8192) have 128 VGPRs and spill less
-  // without it (bf16 [512, 16384]: 66 us against 116 us).
-  constexpr bool PF = K > 1 && S::BLK <= 512;
-  constexpr bool CL = S::BLK > 512 && RB == 1;
-  if constexpr (RB > 1)
-    adaln_bwd_kernel<TX, TY, K, WPR, VEC, kBwdNT, false, 512, RB><<<grid, S::BLK, 0, s>>>(a);
-  else
-    adaln_bwd_kernel<TX, TY, K, WPR, VEC, kBwdNT, PF, 512, 1, CL><<<grid, S::BLK, 0, s>>>(a);
+  const unsigned grid = (unsigned)(pl.B * a.J);
+  if constexpr (VEC && bwd_pipelined<TX, TY, K>()) {
+    if (pl.bwd_rb == 2)
+      adaln_bwd_pipe_kernel<TX, TY, K, WPR, kBwdNT, 2><<<grid, S::BLK, 0, s>>>(a);
+    else
+      adaln_bwd_pipe_kernel<TX, TY, K, WPR, kBwdNT, 1><<<grid, S::BLK, 0, s>>>(a);
+  } else {
+    // The next-row prefetch needs a second row of registers; 1024-thread
+    // blocks (16 wavefronts per row, N > 8192) have 128 VGPRs and spill less
+    // without it (bf16 [512, 16384]: 66 us against 116 us).
+    constexpr bool PF = K > 1 && S::BLK <= 512;
+    constexpr bool CL = S::BLK > 512;
+    adaln_bwd_kernel<TX, TY, K, WPR, VEC, kBwdNT, PF, 512, CL><<<grid, S::BLK, 0, s>>>(a);
+  }
   return check_launch("nf_adaln_bwd");
 }
 
@@ -818,13 +925,13 @@ int fwd_k(const FwdArgs &a, const Plan &pl, hipStream_t s) {
 template <typename TX, typename TY, bool VEC, int WPR>
 int bwd_k(const BwdArgs &a, const Plan &pl, hipStream_t s) {
   if constexpr (!VEC) {
-    return launch_bwd_t<TX, TY, false, WPR, 2>(a, pl.B, s);
+    return launch_bwd_t<TX, TY, false, WPR, 2>(a, pl, s);
   } else {
     if (pl.bwd_k == 1) {
-      if constexpr (bwd_planned<WPR, 1>()) return launch_bwd_t<TX, TY, true, WPR, 1>(a, pl.B, s);
+      if constexpr (bwd_planned<WPR, 1>()) return launch_bwd_t<TX, TY, true, WPR, 1>(a, pl, s);
       return unplanned("nf_adaln_bwd", WPR, 1);
     }
-    if constexpr (bwd_planned<WPR, 2>()) return launch_bwd_t<TX, TY, true, WPR, 2>(a, pl.B, s);
+    if constexpr (bwd_planned<WPR, 2>()) return launch_bwd_t<TX, TY, true, WPR, 2>(a, pl, s);
     return unplanned("nf_adaln_bwd", WPR, 2);
   }
 }

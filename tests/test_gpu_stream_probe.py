@@ -35,3 +35,19 @@ def test_stream_probe_values(cuda, reads, writes, n16):
     for w, t in enumerate(outs):
         # unsigned 32-bit lanes: +w wraps modulo 2^32, as int32 addition does
         assert torch.equal(t, want + w), w
+
+
+@pytest.mark.parametrize("n16", [1000, 4_500_001])
+def test_stream_probe_read_only_pass(cuda, n16):
+    """The (1, 0) form reads in0 and writes nothing for data without the
+    marker value (its one possible store goes to out0[0] only)."""
+    note(f"stream probe read-only n16={n16}")
+    g = torch.Generator().manual_seed(7)
+    src = torch.randint(-2**31, 2**31 - 1, (n16, 4), generator=g, dtype=torch.int64)
+    src = src.to(torch.int32).to(cuda)
+    sink = torch.full((2, 4), -1, dtype=torch.int32, device=cuda)
+    L = _measure.lib()
+    _lib.check(L.nf_stream_probe(1, 0, src.data_ptr(), None, None, None, sink.data_ptr(), None,
+                                 n16, _lib.stream_of(src)), "nf_stream_probe")
+    torch.cuda.synchronize()
+    assert torch.all(sink == -1)
