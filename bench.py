@@ -944,7 +944,7 @@ def main() -> int:
                                      / ad["in_step_ms"]["nf_adaln_bwd"], 3)},
         },
         "roofline": {
-            "kernel": "adaln_bwd_kernel (nf_adaln_bwd)",
+            "kernel": "adaln_bwd_pipe_kernel (nf_adaln_bwd)",
             "bound": "hbm",
             "achieved": round(ad["bwd_gbs"], 1),
             "peak": HBM_PEAK_GBS,
