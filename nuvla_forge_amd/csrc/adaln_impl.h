@@ -271,7 +271,7 @@ __global__ __launch_bounds__((FwdShape<WPR, MINB>::BLK)) void adaln_fwd_kernel(
 // conditioning is loaded once; each batch issues all its x / y loads before
 // any math (2 * RB * K loads in flight per thread) and reduces its RB sums of
 // squares with one LDS round.
-template <typename TX, typename TY, int K, int WPR, bool VEC, bool NT, int RB>
+template <typename TX, typename TY, int K, int WPR, bool VEC, bool NT, int RB, bool NTL>
 __global__ __launch_bounds__((FwdShape<WPR, fwd_min_block<K>()>::BLK)) void adaln_fwd_batch_kernel(
     FwdArgs p) {
   using S = FwdShape<WPR, fwd_min_block<K>()>;
@@ -312,8 +312,8 @@ __global__ __launch_bounds__((FwdShape<WPR, fwd_min_block<K>()>::BLK)) void adal
         const int col = (k * S::R + rt) * 8;
         const int valid = row < last ? chunk_valid(p.N, col) : 0;
         if (valid > 0) {
-          xs[q][k].template load<VEC>(xp + row * p.ld_x + col, valid);
-          ys[q][k].template load<VEC>(yp + row * p.ld_y + col, valid);
+          xs[q][k].template load<VEC, NTL>(xp + row * p.ld_x + col, valid);
+          ys[q][k].template load<VEC, NTL>(yp + row * p.ld_y + col, valid);
         } else {
           xs[q][k].zero();
           ys[q][k].zero();
@@ -594,7 +594,7 @@ struct BwdBatch {
   float rs[RB];
 };
 
-template <typename TX, typename TY, int K, int WPR, bool NT, int RB>
+template <typename TX, typename TY, int K, int WPR, bool NT, int RB, bool NTL>
 __global__ __launch_bounds__((BwdShape<WPR>::BLK)) void adaln_bwd_pipe_kernel(BwdArgs p) {
   using S = BwdShape<WPR>;
   __shared__ float red[S::G * WPR * RB];
@@ -649,11 +649,11 @@ __global__ __launch_bounds__((BwdShape<WPR>::BLK)) void adaln_bwd_pipe_kernel(Bw
       for (int k = 0; k < K; ++k) {
         const int col = (k * S::R + rt) * 8;
         if (t < t1 && col < p.N) {
-          rw.x[k].v = *reinterpret_cast<const VX *>(xp + row * p.ld_x + col);
-          rw.y[k].v = *reinterpret_cast<const VY *>(yp + row * p.ld_y + col);
-          if (dop) rw.dout[k].v = *reinterpret_cast<const VX *>(dop + row * (int64_t)p.N + col);
+          rw.x[k].v = stream_load_vec<VX, NTL>(xp + row * p.ld_x + col);
+          rw.y[k].v = stream_load_vec<VY, NTL>(yp + row * p.ld_y + col);
+          if (dop) rw.dout[k].v = stream_load_vec<VX, NTL>(dop + row * (int64_t)p.N + col);
           else rw.dout[k].zero();
-          if (dhp) rw.dh[k].v = *reinterpret_cast<const VX *>(dhp + row * (int64_t)p.N + col);
+          if (dhp) rw.dh[k].v = stream_load_vec<VX, NTL>(dhp + row * (int64_t)p.N + col);
           else rw.dh[k].zero();
         } else {
           rw.x[k].zero(); rw.y[k].zero(); rw.dout[k].zero(); rw.dh[k].zero();
@@ -744,7 +744,7 @@ struct Plan {
 // beyond (8 wavefronts up to N = 8192, 16 up to 16384).
 // Forward: each row group walks clamp(M / 2048, 1, 8) consecutive rows
 // (clamp(M / 256, 1, 8) for rows of 8 or more wavefronts).
-// Backward: ~256 blocks of 512 threads (1 per CU), each a run of one
+// Backward: at most 256 blocks of 512 threads (1 per CU), each a run of one
 // sample's rows, so the partial rows (B * J * 3 * N floats written, then
 // reduced) are half those of 512 blocks.  16-bit rows of one chunk per lane
 // take the pipelined kernel (adaln_bwd_pipe_kernel): batches of 2 rows per
@@ -812,7 +812,11 @@ inline Plan make_plan(int64_t M, int64_t N, int64_t T, const Knobs &kn = Knobs()
   pl.B = M / T;
   const int R = 64 * pl.bwd_wpr;
   const int G = (R < 512 ? 512 : R) / R;
-  int64_t J = pl.B > 0 ? (bwd_blocks + pl.B - 1) / pl.B : 1;
+  // At most bwd_blocks blocks in all: the backward kernels hold one
+  // 512-thread block per CU (151-251 VGPRs a lane), so blocks past 256 run as
+  // a second, nearly empty round (bf16 [24, 2048, 2048] with 11 blocks per
+  // sample, 264 blocks: 361 us against 235 us with 10).
+  int64_t J = pl.B > 0 ? bwd_blocks / pl.B : 1;
   const int64_t jmax = (T + 2 * G - 1) / (2 * G);  // >= 2 rows per row group
   if (J > jmax) J = jmax;
   if (J > kMaxBlocksPerSample) J = kMaxBlocksPerSample;
@@ -857,8 +861,12 @@ int launch_fwd_t(const FwdArgs &a, const Plan &pl, hipStream_t s) {
   constexpr int RB = fwd_batch_rows<TX, TY, K>();
   if constexpr (VEC && RB > 1) {
     if (a.rows_per_group % RB == 0 && a.T % a.rows_per_group == 0) {
-      adaln_fwd_batch_kernel<TX, TY, K, WPR, VEC, kFwdNT, RB>
-          <<<fwd_grid<S>(pl, a.M), S::BLK, 0, s>>>(a);
+      if (nt_loads_for(a.M * a.N * (int64_t)(sizeof(TX) + sizeof(TY))))
+        adaln_fwd_batch_kernel<TX, TY, K, WPR, VEC, kFwdNT, RB, true>
+            <<<fwd_grid<S>(pl, a.M), S::BLK, 0, s>>>(a);
+      else
+        adaln_fwd_batch_kernel<TX, TY, K, WPR, VEC, kFwdNT, RB, false>
+            <<<fwd_grid<S>(pl, a.M), S::BLK, 0, s>>>(a);
       return check_launch("nf_adaln_fwd");
     }
   }
@@ -877,10 +885,17 @@ int launch_bwd_t(const BwdArgs &a, const Plan &pl, hipStream_t s) {
   using S = BwdShape<WPR>;
   const unsigned grid = (unsigned)(pl.B * a.J);
   if constexpr (VEC && bwd_pipelined<TX, TY, K>()) {
-    if (pl.bwd_rb == 2)
-      adaln_bwd_pipe_kernel<TX, TY, K, WPR, kBwdNT, 2><<<grid, S::BLK, 0, s>>>(a);
+    const int64_t in_row = (int64_t)(sizeof(TX) * (1 + (a.dout ? 1 : 0) + (a.dh_up ? 1 : 0)) +
+                                     sizeof(TY));
+    const bool ntl = nt_loads_for(a.M * a.N * in_row);
+    if (pl.bwd_rb == 2 && ntl)
+      adaln_bwd_pipe_kernel<TX, TY, K, WPR, kBwdNT, 2, true><<<grid, S::BLK, 0, s>>>(a);
+    else if (pl.bwd_rb == 2)
+      adaln_bwd_pipe_kernel<TX, TY, K, WPR, kBwdNT, 2, false><<<grid, S::BLK, 0, s>>>(a);
+    else if (ntl)
+      adaln_bwd_pipe_kernel<TX, TY, K, WPR, kBwdNT, 1, true><<<grid, S::BLK, 0, s>>>(a);
     else
-      adaln_bwd_pipe_kernel<TX, TY, K, WPR, kBwdNT, 1><<<grid, S::BLK, 0, s>>>(a);
+      adaln_bwd_pipe_kernel<TX, TY, K, WPR, kBwdNT, 1, false><<<grid, S::BLK, 0, s>>>(a);
   } else {
     // The next-row prefetch needs a second row of registers; 1024-thread
     // blocks (16 wavefronts per row, N > 8192) have 128 VGPRs and spill less

@@ -36,6 +36,47 @@ __device__ __forceinline__ float bf16_bits_to_f32(uint32_t bits16) {
 }
 
 // ---------------------------------------------------------------------------
+// Streamed loads: activation data that a row / elementwise kernel reads once.
+// NTL adds the non-temporal hint.  The hint pays only when a launch streams
+// more input than the 256 MB Infinity Cache holds; below that it costs.  A/B
+// on one MI355X (bf16, warm back-to-back launches, outputs bit-identical),
+// plain -> hinted, by the launch's streamed input bytes:
+//   adaLN fwd   34 / 134 / 268 / 402 / 537 MB: 10.5 -> 13.0, 45.0 -> 49.7,
+//               89.6 -> 97.7, 148 -> 142, 190 -> 181 us;
+//   adaLN bwd   67 / 268 / 537 / 1074 MB: 18.7 -> 19.7, 76.6 -> 76.7,
+//               161 -> 150, 304 -> 298 us;
+//   SwiGLU fwd  134 / 268 / 370 / 738 / 1476 MB: 29.2 -> 30.7, 56.3 -> 60.1,
+//               90.7 -> 82.7, 183 -> 167, 353 -> 327 us;
+//   SwiGLU bwd  201 / 402 / 555 / 1107 / 2214 MB: 48.1 -> 53.7,
+//               112.6 -> 105.2, 152.4 -> 142.0, 313 -> 292, 599 -> 562 us.
+// So a launch takes the hint when its streamed inputs exceed kNtLoadMinBytes
+// (between the largest size where it lost and the smallest where it won).
+// ---------------------------------------------------------------------------
+constexpr int64_t kNtLoadMinBytes = (int64_t)320 << 20;
+inline bool nt_loads_for(int64_t input_bytes) { return input_bytes > kNtLoadMinBytes; }
+
+template <bool NTL>
+__device__ __forceinline__ u32x4 stream_load16(const void *p) {
+  if constexpr (NTL)
+    return __builtin_nontemporal_load(static_cast<const u32x4 *>(p));
+  else
+    return *static_cast<const u32x4 *>(p);
+}
+
+// A 16- or 32-byte vector type V loaded as whole 16-byte streamed loads.
+template <typename V, bool NTL>
+__device__ __forceinline__ V stream_load_vec(const void *p) {
+  static_assert(sizeof(V) == 16 || sizeof(V) == 32, "16- or 32-byte vectors");
+  if constexpr (sizeof(V) == 16) {
+    return __builtin_bit_cast(V, stream_load16<NTL>(p));
+  } else {
+    const u32x4 a = stream_load16<NTL>(p);
+    const u32x4 b = stream_load16<NTL>(static_cast<const char *>(p) + 16);
+    return __builtin_bit_cast(V, __builtin_shufflevector(a, b, 0, 1, 2, 3, 4, 5, 6, 7));
+  }
+}
+
+// ---------------------------------------------------------------------------
 // 8-element chunk I/O.  `p` must be 16-byte aligned for the vector forms.
 // ---------------------------------------------------------------------------
 template <typename T>
@@ -156,23 +197,30 @@ struct Raw8 {
 #pragma unroll
     for (int i = 0; i < 8; ++i) v[i] = static_cast<T>(0.f);
   }
-  template <bool VEC>
+  template <bool VEC, bool NTL = false>
   __device__ __forceinline__ void load(const T *p, int valid) {
     if (VEC && valid >= 8) {
-      if constexpr (sizeof(T) == 4) {
-        typedef T t4 __attribute__((ext_vector_type(4)));
-        const t4 a = *reinterpret_cast<const t4 *>(p);
-        const t4 b = *reinterpret_cast<const t4 *>(p + 4);
-        v = __builtin_shufflevector(a, b, 0, 1, 2, 3, 4, 5, 6, 7);
-      } else {
-        v = *reinterpret_cast<const vtype *>(p);
-      }
+      v = stream_load_vec<vtype, NTL>(p);
     } else {
 #pragma unroll
       for (int i = 0; i < 8; ++i) v[i] = i < valid ? p[i] : static_cast<T>(0.f);
     }
   }
 };
+
+// load8 for streamed activation data: the vector form goes through
+// stream_load16<NTL>.
+template <typename T, bool VEC, bool NTL>
+__device__ __forceinline__ void load8_stream(const T *p, int valid, float (&v)[8]) {
+  if (VEC && valid >= 8) {
+    Raw8<T> r;
+    r.template load<true, NTL>(p, 8);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = r[i];
+  } else {
+    load8_masked<T>(p, valid, v);
+  }
+}
 
 // Runtime-typed chunk load for the small [B, N] / [N] conditioning tensors
 // (their element type may differ from the activations').  `dt` is uniform

@@ -208,6 +208,21 @@ def test_adaln_argument_validation():
                                  64, 1024, 8, 1, 1, 1, 1, None) == NF_OK  # nothing requested
 
 
+@pytest.mark.parametrize("b", [1, 2, 3, 5, 6, 7, 8, 12, 24, 32, 40, 100, 255, 256, 300])
+@pytest.mark.parametrize("t,n", [(2048, 1024), (2048, 2048), (64, 256)])
+def test_adaln_backward_blocks_fit_one_round(b, t, n):
+    """The backward's B x J blocks (J read back from the workspace size,
+    B * J * 3 * N fp32 partial rows) stay within the 256 CUs that each hold one
+    512-thread backward block, unless every sample already runs one block."""
+    L = _lib.lib()
+    ws = L.nf_adaln_bwd_workspace(b * t, n, t)
+    j, rem = divmod(ws, b * 3 * n * 4)
+    assert rem == 0 and j >= 1
+    assert b * j <= 256 or j == 1, (b, j)
+    if b <= 256 and t >= 2048:
+        assert b * j > 128, (b, j)  # and still at least half the CUs
+
+
 def _ceil(a: int, b: int) -> int:
     return -(-a // b)
 

@@ -77,7 +77,7 @@ def test_cfg1_fp32_all_six_gradients(cuda):
 @pytest.mark.parametrize("b,t,n", [(2, 16, 256), (4, 32, 1024), (3, 7, 768), (1, 64, 1536),
                                    (2, 8, 1000), (2, 3, 333), (1, 5, 8), (2, 4, 4096),
                                    (1, 2, 16384), (300, 1, 64), (1, 1, 1024), (5, 3, 2048),
-                                   (3, 700, 512)])
+                                   (3, 700, 512), (24, 96, 1024)])
 def test_adaln_matches_oracle(cuda, dtype, b, t, n):
     note(f"adaln dtype={dtype} b={b} t={t} n={n}")
     inp = _inputs(b, t, n, dtype, cuda)
