@@ -911,6 +911,9 @@ int launch_bwd_t(const BwdArgs &a, const Plan &pl, hipStream_t s) {
 // path, so only those are compiled: forward one chunk up to 2 wavefronts (N <=
 // 1024), two chunks otherwise; backward one chunk up to 8 wavefronts (N <=
 // 4096), two chunks from 8 (N > 4096).  The element-wise path always takes two.
+// make_plan never asks for more than two chunks per lane (pick_wpr widens the
+// row first); a plan that did is refused rather than run on a kernel that
+// would cover only part of the row.
 template <int WPR, int K>
 constexpr bool fwd_planned() {
   return K == 2 || WPR <= 2;
@@ -933,6 +936,7 @@ int fwd_k(const FwdArgs &a, const Plan &pl, hipStream_t s) {
       if constexpr (fwd_planned<WPR, 1>()) return launch_fwd_t<TX, TY, true, WPR, 1>(a, pl, s);
       return unplanned("nf_adaln_fwd", WPR, 1);
     }
+    if (pl.fwd_k != 2) return unplanned("nf_adaln_fwd", WPR, pl.fwd_k);
     if constexpr (fwd_planned<WPR, 2>()) return launch_fwd_t<TX, TY, true, WPR, 2>(a, pl, s);
     return unplanned("nf_adaln_fwd", WPR, 2);
   }
@@ -946,6 +950,7 @@ int bwd_k(const BwdArgs &a, const Plan &pl, hipStream_t s) {
       if constexpr (bwd_planned<WPR, 1>()) return launch_bwd_t<TX, TY, true, WPR, 1>(a, pl, s);
       return unplanned("nf_adaln_bwd", WPR, 1);
     }
+    if (pl.bwd_k != 2) return unplanned("nf_adaln_bwd", WPR, pl.bwd_k);
     if constexpr (bwd_planned<WPR, 2>()) return launch_bwd_t<TX, TY, true, WPR, 2>(a, pl, s);
     return unplanned("nf_adaln_bwd", WPR, 2);
   }
