@@ -604,17 +604,16 @@ def bench_ce(args, dev):
                 "graph_matches_eager": same(ref, outs), "tokens_per_s": m / (ms * 1e-3),
                 "tflops": tflops, "mfma_frac": tflops / MFMA_BF16_PEAK_TFLOPS}
 
-    # The figure of record is the reference's default chunk_size 1024 (rows
-    # per chunk, chunked_ce.py:189: four chunks of the 3687 valid rows here,
-    # one [1024, V] tile's worth of E and E^T at a time, the fp32 dW
-    # accumulator between chunks).  Beside it 2048 and 4096; 4096 is one
-    # chunk over every valid row, so it holds E and E^T of all 3687 rows
-    # (2 x 236 MB in bf16, what the reference's [4096, V] fp32 logits tile
-    # would hold at that setting): faster, but not the reference's memory
-    # bound at its default.
+    # The figure of record is the reference's default chunk_size 1024
+    # (chunked_ce.py:189): E held once in bf16 for 2048 rows at a time, the
+    # bytes of the reference's [1024, V] fp32 logits tile, so two chunks of
+    # the 3687 valid rows with the fp32 dW accumulator between them.  Beside
+    # it 512 (four chunks of 1024 rows) and 4096 (one chunk over every valid
+    # row in both layouts: E and E^T of all 3687 rows, 2 x 236 MB, what the
+    # reference's [4096, V] fp32 tile holds at that setting).
     main = run(1024)
     return {"m": m, "d": d, "v": v, "m_valid": m_valid, "alg_flops": flops, **main,
-            "chunk_2048": run(2048),
+            "chunk_512": run(512),
             "chunk_4096_one_chunk": {**run(4096), "holds": "E and E^T of every valid row"}}
 
 

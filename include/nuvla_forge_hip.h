@@ -188,7 +188,7 @@ int nf_adaln_bwd_noalloc(const void *dh_up, const void *dout, const void *x,
 
 /* ------------------------------------------------------------------------
  * Chunked cross entropy.
- *   logits = hidden @ weight^T          ([M, V]; chunk_rows rows of it at a
+ *   logits = hidden @ weight^T          ([M, V]; a chunk of its rows at a
  *                                        time, all of it when one chunk
  *                                        covers every valid row)
  *   lse    = logsumexp_v logits         (fp32)
@@ -211,12 +211,17 @@ int nf_adaln_bwd_noalloc(const void *dh_up, const void *dout, const void *x,
  * nf_ce_fwd computes the loss and fills `state` (nf_ce_state_bytes, 16-byte
  * aligned), which the caller keeps for nf_ce_bwd; `workspace`
  * (nf_ce_fwd_workspace) is scratch for the call.  The valid rows are taken
- * `chunk_rows` at a time (rounded up to 256): a chunk's logits are held as
- * exp(logit - the row's target logit) in the input type, in both layouts the
- * gradient products read, with the target entry carrying the one-hot term
- * and a per-row fp32 factor making them (softmax - onehot) * inv, so memory
- * is O(chunk_rows * V), not O(M * V), as the reference's row chunks
- * (chunk_size) are; results do not depend on chunk_rows beyond fp rounding.
+ * a chunk at a time: a chunk's logits are held as exp(logit - the row's
+ * target logit) in the input type, with the target entry carrying the
+ * one-hot term and a per-row fp32 factor making them (softmax - onehot) *
+ * inv, so memory is O(chunk_rows * V), not O(M * V), as the reference's row
+ * chunks (chunk_size) are; results do not depend on chunk_rows beyond fp
+ * rounding.  Where chunk_rows rows (rounded up to 256) do not cover M, bf16
+ * holds a chunk's logits once (row-major; the dweight product reads them
+ * transposed) and so takes 2 * chunk_rows rows per chunk (rounded up to
+ * 256): 4 * chunk_rows * V bytes, the reference's fp32 [chunk_size, V]
+ * logits tile.  Otherwise, and for fp32, they are held in both layouts the
+ * products read, chunk_rows rows per chunk (rounded up to 256).
  * The forward also runs the gradient products of every chunk but the last
  * (into fp32 accumulators in `state`).  Replaces _ChunkedCrossEntropy.forward
  * and the `_ce_fwd_bwd` kernel, nuvla_forge/kernels/chunked_ce.py:49-98 and

@@ -4,7 +4,7 @@
  * (libnf_hip.so, include/nuvla_forge_hip.h).  None of these has a
  * counterpart in the reference, and no op of the product calls them: the
  * benchmark sets the product kernels against the two probes, and the tests
- * drive the MFMA GEMM core through nf_gemm_nt.
+ * drive the MFMA GEMM core through nf_gemm_nt and nf_gemm_nn.
  *
  * Same conventions as the product ABI: device pointers, int64_t sizes, a
  * hipStream_t as `void *`, NF_OK or a negative status, and the failure text
@@ -28,6 +28,18 @@ extern "C" {
 int nf_gemm_nt(const void *A, int64_t lda, const void *B, int64_t ldb,
                float *C, int64_t ldc, int64_t M, int64_t N, int64_t K,
                int dtype, void *stream);
+
+/* ------------------------------------------------------------------------
+ * Test hook with no counterpart in the reference: C = A[M, K] @ B[K, N]
+ * (bf16 A and B, fp32 C) through the MFMA core's N-major-B path: A
+ * row-major with unit-stride K (lda, K multiples of 8), B row-major with
+ * unit-stride N (ldb >= N, a multiple of 8; columns up to ldb are read),
+ * 16-byte aligned.  C[m, n] is stored at C[m * ldc + n], or at
+ * C[n * ldc + m] when c_transposed is nonzero.
+ * ---------------------------------------------------------------------- */
+int nf_gemm_nn(const void *A, int64_t lda, const void *B, int64_t ldb,
+               float *C, int64_t ldc, int64_t M, int64_t N, int64_t K,
+               int c_transposed, void *stream);
 
 /* ------------------------------------------------------------------------
  * Measurement aid with no counterpart in the reference: the streaming

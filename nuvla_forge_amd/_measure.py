@@ -25,6 +25,7 @@ _I32 = ctypes.c_int
 # name -> (restype, argtypes); the order follows the C declarations
 SIGNATURES = {
     "nf_gemm_nt": (_I32, [_P, _I64, _P, _I64, _P, _I64, _I64, _I64, _I64, _I32, _P]),
+    "nf_gemm_nn": (_I32, [_P, _I64, _P, _I64, _P, _I64, _I64, _I64, _I64, _I32, _P]),
     "nf_stream_probe": (_I32, [_I32, _I32, _P, _P, _P, _P, _P, _P, _I64, _P]),
     "nf_mfma_probe": (_I32, [_P, _I64, _I64, _P, _P, _P]),
 }

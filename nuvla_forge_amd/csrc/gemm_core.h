@@ -233,9 +233,8 @@ __device__ __forceinline__ void mfma_block(const u32x4 (&a)[C::TM], const u32x4 
 // after one per read go first (2 for 8 MFMAs and 6 reads): measured against
 // putting them last, CE cfg4 2.04-2.05 ms against 2.05-2.07 ms and the
 // gate/up fwd+bwd 187-190 us against 191-193 us.
-template <class C>
+template <class C, int kReads = C::TM + C::TN>
 __device__ __forceinline__ void interleave_hint() {
-  constexpr int kReads = C::TM + C::TN;
   constexpr int kMfma = C::TM * C::TN * (sizeof(typename C::TI) == 2 ? 1 : 4);
   constexpr int kPer = kMfma / kReads > 0 ? kMfma / kReads : 1;
   constexpr int kLead = kMfma - kReads * kPer;  // MFMAs issued before the first read
@@ -298,6 +297,7 @@ typedef __attribute__((address_space(3))) void *lds_ptr_t;
 template <class C, int CW>
 struct DtlOperand {
   using TI = typename C::TI;
+  static constexpr bool kKRows = false;
   const TI *base;
   int64_t ld, rows, K, r0;  // r0: matrix row of tile row 0
   __amdgpu_buffer_rsrc_t rsrc;
@@ -398,9 +398,127 @@ __device__ __forceinline__ void read_kgroup_dtl(const char *stage, int wm, int w
   for (int j = 0; j < C::TN; ++j) b[j] = *reinterpret_cast<const u32x4 *>(bs + j * 32 * C::ROW);
 }
 
-template <class C, bool BUF>
+// ---- B given N-major ([K, N], unit-stride N) ---------------------------------
+// For products whose B operand is stored with N contiguous (the cross
+// entropy's dW product reads E, rows of tokens by vocabulary, this way).  A
+// stage holds the BK k-rows of the tile's BN columns, 2 * BN bytes per k-row,
+// the k-row's 16-byte vectors XOR-swizzled by kn_swz(k-row); one 1 KB direct
+// copy covers 1024 / (2 * BN) k-rows.  The MFMA operand (8 consecutive k of
+// one column per lane) comes from two transposing reads
+// (ds_read_b64_tr_b16, 4 k each): in each 16-lane group, lane i receives
+// element i % 4 of the 8-byte pieces addressed by lanes i / 4 + 4 q
+// (q = 0..3), so lane a + 4 q addresses k-row k0 + q at columns 4 a .. 4 a + 3
+// and lane i receives column i at k0 .. k0 + 3.  One read instruction of a
+// wavefront covers k-rows {0..3, 8..11} + 16 kg (+ 4 for the second) x 64
+// bytes of columns; kn_swz gives those eight k-rows eight different groups of
+// four vector slots, so the 512 bytes spread evenly over the banks.
+template <class C>
+__device__ __forceinline__ int kn_swz(int krow) {
+  return 4 * ((krow & 3) | (((krow >> 3) & 1) << 2));
+}
+
+template <class C>
+struct DtlOperandKN {
+  using TI = typename C::TI;
+  static constexpr bool kKRows = true;
+  static constexpr int VPR = C::BN / 8;           // 16-byte vectors per k-row
+  static constexpr int KPC = 64 / VPR;            // k-rows per 1 KB copy
+  static constexpr int CW = C::BK / KPC / C::NW;  // copies per wavefront per stage
+  static_assert(VPR == 32 && KPC == 2 && CW == 4, "N-major B: BN = 256, BK = 64, 8 wavefronts");
+  // The lane's k-row in copy c is r0 + 2 c (r0 = 8 wave + lane / 32), whose
+  // swizzle depends on c's parity only, so copies c and c + 2 read the same
+  // columns 4 k-rows apart: two offsets describe all four.
+  const TI *base;
+  int64_t ld, ncols, K, c0;  // ncols: columns that may be read; c0: column of tile column 0
+  __amdgpu_buffer_rsrc_t rsrc;
+  uint32_t off_p[2];  // byte offset at k = 0 of copy parity p's vector
+  bool cin_p[2];      // that vector lies inside [0, ncols)
+  int r0;             // k-row of copy 0
+  uint32_t kbytes;    // bytes per k-row
+  static constexpr uint32_t kOob = 0x80000000u;
+
+  __device__ __forceinline__ void init(const TI *p, int64_t ld_, int64_t ncols_, int64_t K_,
+                                       int64_t c0_, int wave) {
+    base = p; ld = ld_; ncols = ncols_; K = K_; c0 = c0_;
+    rsrc = __builtin_amdgcn_make_buffer_rsrc(const_cast<TI *>(p), (short)0,
+                                             (int)(K_ * ld_ * (int64_t)sizeof(TI)), 0x00020000);
+    kbytes = (uint32_t)(ld_ * (int64_t)sizeof(TI));
+    const int l = threadIdx.x & 63;
+    r0 = wave * (CW * KPC) + l / VPR;
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const int row = r0 + 2 * q;
+      const int64_t col = c0_ + ((l % VPR) ^ kn_swz<C>(row)) * C::VE;
+      cin_p[q] = col < ncols_;
+      off_p[q] = (uint32_t)((row * ld_ + col) * (int64_t)sizeof(TI));
+    }
+  }
+  __device__ __forceinline__ void issue(int64_t k0, char *region, int wave) const {
+    const uint32_t kb = (uint32_t)k0 * kbytes;
+#pragma unroll
+    for (int c = 0; c < CW; ++c) {
+      const bool in = cin_p[c & 1] && k0 + r0 + 2 * c < K;
+      const uint32_t o = off_p[c & 1] + (uint32_t)(c >> 1) * (4 * kbytes) + kb;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          rsrc, (lds_ptr_t)(region + (wave * CW + c) * 1024), 16, in ? o : kOob, 0, 0, 0);
+    }
+  }
+  __device__ __forceinline__ void copy_sync(int64_t k0, int wave, char *region) const {
+    const int l = threadIdx.x & 63;
+#pragma unroll
+    for (int c = 0; c < CW; ++c) {
+      const int row = r0 + 2 * c;
+      const int v = (l % VPR) ^ kn_swz<C>(row);
+      const u32x4 x = load_vec<TI, false>(base, ld, k0 + row, K, c0 + v * C::VE, ncols);
+      *reinterpret_cast<u32x4 *>(region + (wave * CW + c) * 1024 + l * 16) = x;
+    }
+  }
+};
+
+// Operands of one 16-wide k-group, B from the N-major stage layout above
+// (A as read_kgroup_dtl).  The lane's first read is k-row r = 16 kg +
+// 8 (lane / 32) + (lane % 16) / 4, whose swizzle does not depend on kg and is
+// the same at r + 4; and MFMA tile j + 1's 16-byte slot differs from tile j's
+// in bit 2 only.  So one address per tile j (at kg = 0) and immediate offsets
+// (8 KB per k-group, 2 KB for the second read) cover every read.
+template <class C>
+__device__ __forceinline__ void read_kgroup_kn(const char *stage, int wm, int wn, int kg,
+                                               u32x4 (&a)[C::TM], u32x4 (&b)[C::TN]) {
+  typedef short v4s __attribute__((ext_vector_type(4)));
+  typedef __attribute__((address_space(3))) v4s *lds_v4s;
+  static_assert(C::BN == 256 && C::WTN == 64 && C::TN == 2, "N-major B tiling");
+  const int l = threadIdx.x & 63;
+  const int sw = dtl_slot<C>(l & 31, 2 * kg + (l >> 5)) * 16;
+  const char *as = stage + (wm * C::WTM + (l & 31)) * C::ROW + sw;
+#pragma unroll
+  for (int i = 0; i < C::TM; ++i) a[i] = *reinterpret_cast<const u32x4 *>(as + i * 32 * C::ROW);
+  const int j16 = l & 15;
+  const int r = 8 * (l >> 5) + (j16 >> 2);  // k-row at kg = 0
+  const int col = wn * C::WTN + 16 * ((l >> 4) & 1) + 4 * (j16 & 3);  // tile j = 0
+  const int off0 = r * (2 * C::BN) + (((col >> 3) ^ kn_swz<C>(r)) << 4) + (col & 7) * 2;
+  const char *bs = stage + C::BM * C::ROW + kg * 16 * (2 * C::BN);
+#pragma unroll
+  for (int j = 0; j < C::TN; ++j) {
+    const char *p = bs + (j ? (off0 ^ 64) : off0);
+    const v4s x = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s)p);
+    const v4s y = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s)(p + 4 * (2 * C::BN)));
+    b[j] = __builtin_bit_cast(u32x4, __builtin_shufflevector(x, y, 0, 1, 2, 3, 4, 5, 6, 7));
+  }
+}
+
+// k-group operands for B operand type OpB
+template <class C, class OpB>
+__device__ __forceinline__ void read_kgroup_op(const char *stage, int wm, int wn, int kg,
+                                               u32x4 (&a)[C::TM], u32x4 (&b)[C::TN]) {
+  if constexpr (OpB::kKRows)
+    read_kgroup_kn<C>(stage, wm, wn, kg, a, b);
+  else
+    read_kgroup_dtl<C>(stage, wm, wn, kg, a, b);
+}
+
+template <class C, bool BUF, class OpB>
 __device__ __forceinline__ void mainloop_dtl_ops(const DtlOperand<C, C::ACW> &opa,
-                                                 const DtlOperand<C, C::BCW> &opb, int64_t K,
+                                                 const OpB &opb, int64_t K,
                                                  char *smem, floatx16 (&acc)[C::TM][C::TN]);
 
 template <class C, bool BUF, bool ZERO>
@@ -424,12 +542,40 @@ __device__ __forceinline__ void mainloop_dtl(const bf16 *A, int64_t lda, const b
   mainloop_dtl_ops<C, BUF>(opa, opb, K, smem, acc);
 }
 
+// As mainloop_dtl with B given N-major: B[k, n] at B[k * ldb + n], k-rows
+// past K read as zero, columns at or past nb_cols read as zero (16-byte
+// vectors, so nb_cols is a multiple of 8 on the buffer path).
+template <class C, bool BUF, bool ZERO>
+__device__ __forceinline__ void mainloop_kn(const bf16 *A, int64_t lda, const bf16 *B,
+                                            int64_t ldb, int64_t M, int64_t nb_cols, int64_t K,
+                                            int64_t m0, int64_t n0, char *smem,
+                                            floatx16 (&acc)[C::TM][C::TN]) {
+  static_assert(DtlOperandKN<C>::CW == C::BCW, "stage copies per wavefront (wait counts)");
+  const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+  if constexpr (ZERO) {
+#pragma unroll
+    for (int i = 0; i < C::TM; ++i)
+#pragma unroll
+      for (int j = 0; j < C::TN; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+  }
+  DtlOperand<C, C::ACW> opa;
+  DtlOperandKN<C> opb;
+  opa.init(A, lda, M, K, m0, wave);
+  opb.init(B, ldb, nb_cols, K, n0, wave);
+  mainloop_dtl_ops<C, BUF>(opa, opb, K, smem, acc);
+}
+
 // The K loop over operands the caller has set up (a kernel may point each
 // wavefront's share of a tile at a different matrix).  acc is not cleared.
-template <class C, bool BUF>
+// OpB: DtlOperand (B K-contiguous) or DtlOperandKN (B N-major).
+template <class C, bool BUF, class OpB>
 __device__ __forceinline__ void mainloop_dtl_ops(const DtlOperand<C, C::ACW> &opa,
-                                                 const DtlOperand<C, C::BCW> &opb, int64_t K,
+                                                 const OpB &opb, int64_t K,
                                                  char *smem, floatx16 (&acc)[C::TM][C::TN]) {
+  // LDS read instructions per k-group: an N-major B takes two per MFMA tile
+  constexpr int kReadsB = C::TM + (OpB::kKRows ? 2 : 1) * C::TN;
   const int w = threadIdx.x >> 6;
   const int wave = __builtin_amdgcn_readfirstlane(w);
   const int wm = w / C::WN, wn = w % C::WN;
@@ -454,7 +600,7 @@ __device__ __forceinline__ void mainloop_dtl_ops(const DtlOperand<C, C::ACW> &op
       }
     if (nk > 0) {
       wait_stage<C>(nk - 1 < C::STAGES - 1 ? (int)(nk - 1) : C::STAGES - 1);
-      read_kgroup_dtl<C>(smem, wm, wn, 0, a0, b0);
+      read_kgroup_op<C, OpB>(smem, wm, wn, 0, a0, b0);
     }
     int cur = 0;  // buffer of stage kt
     static_assert(C::KG % 2 == 0, "k-groups alternate register sets in pairs");
@@ -462,17 +608,17 @@ __device__ __forceinline__ void mainloop_dtl_ops(const DtlOperand<C, C::ACW> &op
       const char *st = smem + cur * C::STAGE;
 #pragma unroll
       for (int kg = 0; kg + 1 < C::KG; kg += 2) {
-        read_kgroup_dtl<C>(st, wm, wn, kg + 1, a1, b1);
+        read_kgroup_op<C, OpB>(st, wm, wn, kg + 1, a1, b1);
         mfma_block<C>(a0, b0, acc);
-        interleave_hint<C>();
+        interleave_hint<C, kReadsB>();
         if (kg + 2 < C::KG) {
-          read_kgroup_dtl<C>(st, wm, wn, kg + 2, a0, b0);
+          read_kgroup_op<C, OpB>(st, wm, wn, kg + 2, a0, b0);
           mfma_block<C>(a1, b1, acc);
-          interleave_hint<C>();
+          interleave_hint<C, kReadsB>();
         }
       }
       mfma_block<C>(a1, b1, acc);  // the last k-group, then the hand-over
-      interleave_hint<C>();
+      interleave_hint<C, kReadsB>();
       if (kt + 1 < nk) {
         if constexpr (C::STAGES == 2) {
           // stage kt + 1 is the only one in flight: wait for all of it
@@ -487,7 +633,7 @@ __device__ __forceinline__ void mainloop_dtl_ops(const DtlOperand<C, C::ACW> &op
           opb.issue((kt + C::STAGES) * C::BK, re + C::BM * C::ROW, wave);
         }
         cur = cur + 1 == C::STAGES ? 0 : cur + 1;
-        read_kgroup_dtl<C>(smem + cur * C::STAGE, wm, wn, 0, a0, b0);
+        read_kgroup_op<C, OpB>(smem + cur * C::STAGE, wm, wn, 0, a0, b0);
       }
     }
   } else {
@@ -497,8 +643,8 @@ __device__ __forceinline__ void mainloop_dtl_ops(const DtlOperand<C, C::ACW> &op
       __syncthreads();
 #pragma unroll
       for (int kg = 0; kg < C::KG; kg += 2) {
-        read_kgroup_dtl<C>(smem, wm, wn, kg, a0, b0);
-        read_kgroup_dtl<C>(smem, wm, wn, kg + 1, a1, b1);
+        read_kgroup_op<C, OpB>(smem, wm, wn, kg, a0, b0);
+        read_kgroup_op<C, OpB>(smem, wm, wn, kg + 1, a1, b1);
         mfma_block<C>(a0, b0, acc);
         mfma_block<C>(a1, b1, acc);
       }

@@ -112,6 +112,13 @@ struct GemmJob {
   const int *dyn;    // device count giving the dynamic extent, or null
   int64_t dyn_base;  // the extent is *dyn - dyn_base, clamped to [0, M or K]
   int dyn_rows;      // 1: the dynamic extent is M; 0: it is K
+  // bt: B is given N-major, B[k, n] at B[k * ldb + n] (columns up to ldb may
+  // be read; 16-bit inputs on the direct-to-LDS path only).  ct: C is stored
+  // transposed, element (m, n) at C[n * ldc + m] (no K split); Cin keeps
+  // [M, ldcin].
+  int bt, ct;
+  int ct_vec;     // ct with M and ldc multiples of 8: the LDS-transposed store
+  int64_t ldcin;  // row stride of Cin (make_job: ldc)
 };
 
 // The job's (M, K) after its dynamic extent, if any.
@@ -144,6 +151,148 @@ __device__ __forceinline__ uint16_t to_half_bits(float v, int dt) {
     __builtin_memcpy(&bits, &h, 2);
   }
   return bits;
+}
+
+// One block's tile of job j: the K loop (B K-contiguous, or N-major when BT)
+// and the store epilogue.  The kernel instantiates it once per B layout in
+// separate branches, so the two K loops never share a merge point (which
+// would force one register assignment on both and spill).
+template <class C, bool BUF, bool SB, bool BT>
+__device__ __forceinline__ void store_tile(const GemmJob<typename C::TI> &j, int64_t M,
+                                           int64_t K, int ks, int64_t m0, int64_t n0,
+                                           char *smem) {
+  const int64_t N = j.N;
+  const bool split = j.ksplit > 1;
+  const int64_t k0 = ks * j.kslice;
+  int64_t klen = K - k0 < j.kslice ? K - k0 : j.kslice;
+  if (klen < 0) klen = 0;
+  // a split block writes its fp32 partial densely; the reduce does the rest
+  const int64_t ldc = split ? N : j.ldc;
+  const int cdt = split ? NF_DTYPE_F32 : j.cdt;
+  const bool preload = !split && j.Cin != nullptr;
+  // element (m, n) of C sits at idx(m, n); of Cin at m * ldcin + n
+  const bool ct = !split && j.ct;
+  auto idx = [&](int64_t m, int64_t n) { return ct ? n * ldc + m : m * ldc + n; };
+  const int64_t c_rows = ct ? N : j.M;
+  OutBuf<SB> out, cin;
+  out.init(split ? static_cast<void *>(j.part + ks * j.M * N) : j.C,
+           c_rows * ldc * (int64_t)dtype_bytes(cdt));
+  cin.init(const_cast<float *>(j.Cin), j.M * j.ldcin * (int64_t)sizeof(float));
+  const int w = threadIdx.x >> 6, wm = w / C::WN, wn = w % C::WN;
+  // element (i, jj, r) of this lane sits at byte offset base + i * 32 rows
+  // + 8 * (r / 4) + (r % 4) rows + jj * 32 columns
+  const int64_t row0 = m0 + gemm::acc_row<C>(wm, 0, 0);
+  const int64_t col0 = n0 + gemm::acc_col<C>(wn, 0);
+  floatx16 acc[C::TM][C::TN];
+#pragma unroll
+  for (int i = 0; i < C::TM; ++i)
+#pragma unroll
+    for (int jj = 0; jj < C::TN; ++jj)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int dr = i * 32 + 8 * (r >> 2) + (r & 3);
+        const bool ok = row0 + dr < M && col0 + jj * 32 < N;
+        acc[i][jj][r] =
+            preload ? cin.ld32(((row0 + dr) * j.ldcin + col0 + jj * 32) * 4, ok) : 0.f;
+      }
+  if constexpr (BT)
+    gemm::mainloop_kn<C, BUF, false>(j.A + k0, j.lda, j.B + k0 * j.ldb, j.ldb, M, j.ldb, klen,
+                                     m0, n0, smem, acc);
+  else
+    gemm::mainloop<C, BUF, false>(j.A + k0, j.lda, j.B + k0, j.ldb, M, N, klen, m0, n0, smem, acc);
+  const float g = (!split && j.scale) ? *j.scale : 1.f;
+  if constexpr (C::DTL) {
+  if (ct && j.ct_vec) {
+    // Transposed store through LDS (free after the K loop), so that global
+    // stores are whole 16-byte vectors along m: in pass p the wavefronts of
+    // column p (tile columns 64 p .. 64 p + 63) put their scaled accumulators
+    // into LDS as 64 rows n of 256 m (row pitch 256 elements + 16 bytes, so
+    // the 32 rows a write instruction touches start on different banks), then
+    // every thread stores row vectors.  Needs M and ldc multiples of 8.
+    static_assert(C::WTN == 64 && C::WN * C::WTN == C::BN && C::BM == 256, "tiling");
+    const int es = dtype_bytes(cdt);
+    const int pitch = 256 * es + 16;
+    const int l = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int wm = w / C::WN, wn = w % C::WN;
+    const int vpr = 256 * es / 16;  // 16-byte vectors per LDS row
+#pragma unroll 1
+    for (int p = 0; p < C::WN; ++p) {
+      if (wn == p) {
+#pragma unroll
+        for (int i = 0; i < C::TM; ++i)
+#pragma unroll
+          for (int jj = 0; jj < C::TN; ++jj)
+#pragma unroll
+            for (int rq = 0; rq < 4; ++rq) {
+              const int ml = wm * C::WTM + i * 32 + 8 * rq + 4 * (l >> 5);
+              char *dst = smem + (jj * 32 + (l & 31)) * pitch + ml * es;
+              float v[4];
+#pragma unroll
+              for (int q = 0; q < 4; ++q) v[q] = acc[i][jj][4 * rq + q] * g;
+              if (es == 4) {
+                u32x4 x;
+                x.x = __float_as_uint(v[0]); x.y = __float_as_uint(v[1]);
+                x.z = __float_as_uint(v[2]); x.w = __float_as_uint(v[3]);
+                *reinterpret_cast<u32x4 *>(dst) = x;
+              } else {
+                u32x2 x;
+                x.x = (uint32_t)to_half_bits(v[0], cdt) | ((uint32_t)to_half_bits(v[1], cdt) << 16);
+                x.y = (uint32_t)to_half_bits(v[2], cdt) | ((uint32_t)to_half_bits(v[3], cdt) << 16);
+                *reinterpret_cast<u32x2 *>(dst) = x;
+              }
+            }
+      }
+      __syncthreads();
+      for (int e = threadIdx.x; e < 64 * vpr; e += C::NT) {
+        const int nl = e / vpr, vi = e % vpr;
+        const int64_t n = n0 + p * 64 + nl, m = m0 + (int64_t)vi * (16 / es);
+        const u32x4 x = *reinterpret_cast<const u32x4 *>(smem + nl * pitch + vi * 16);
+        out.st128((n * ldc + m) * es, n < N && m < M, x);
+      }
+      __syncthreads();
+    }
+    return;
+  }
+  }
+  // the per-row factor of the lane's 16 rows of MFMA tile i (rows past M: 0)
+  const float *rsc = split ? nullptr : j.row_scale;
+  auto row_factors = [&](int i, float (&f)[16]) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int64_t row = row0 + i * 32 + 8 * (r >> 2) + (r & 3);
+      f[r] = rsc ? (row < M ? rsc[row] * g : 0.f) : g;
+    }
+  };
+  if (cdt == NF_DTYPE_F32) {
+#pragma unroll
+    for (int i = 0; i < C::TM; ++i) {
+      float f[16];
+      row_factors(i, f);
+#pragma unroll
+      for (int jj = 0; jj < C::TN; ++jj)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int dr = i * 32 + 8 * (r >> 2) + (r & 3);
+          const bool ok = row0 + dr < M && col0 + jj * 32 < N;
+          out.st32(idx(row0 + dr, col0 + jj * 32) * 4, ok, acc[i][jj][r] * f[r]);
+        }
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < C::TM; ++i) {
+      float f[16];
+      row_factors(i, f);
+#pragma unroll
+      for (int jj = 0; jj < C::TN; ++jj)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int dr = i * 32 + 8 * (r >> 2) + (r & 3);
+          const bool ok = row0 + dr < M && col0 + jj * 32 < N;
+          out.st16(idx(row0 + dr, col0 + jj * 32) * 2, ok,
+                   to_half_bits(acc[i][jj][r] * f[r], cdt));
+        }
+    }
+  }
 }
 
 template <class C, bool BUF, bool SB>
@@ -183,76 +332,13 @@ __global__ NF_GEMM_BOUNDS(C) void gemm_store_kernel(GemmJob<typename C::TI> j0,
   gemm::group_tile(t % per_split, tiles_m, tiles_n, gemm::kTileGroup, tm, tn);
   const int64_t m0 = (int64_t)tm * C::BM;
   const int64_t n0 = (int64_t)tn * C::BN;
-  const int64_t N = j.N;
-  const bool split = j.ksplit > 1;
-  const int64_t k0 = ks * j.kslice;
-  int64_t klen = K - k0 < j.kslice ? K - k0 : j.kslice;
-  if (klen < 0) klen = 0;
-  // a split block writes its fp32 partial densely; the reduce does the rest
-  const int64_t ldc = split ? N : j.ldc;
-  const int cdt = split ? NF_DTYPE_F32 : j.cdt;
-  const bool preload = !split && j.Cin != nullptr;
-  OutBuf<SB> out, cin;
-  out.init(split ? static_cast<void *>(j.part + ks * j.M * N) : j.C,
-           j.M * ldc * (int64_t)dtype_bytes(cdt));
-  cin.init(const_cast<float *>(j.Cin), j.M * ldc * (int64_t)sizeof(float));
-  const int w = threadIdx.x >> 6, wm = w / C::WN, wn = w % C::WN;
-  // element (i, jj, r) of this lane sits at byte offset base + i * 32 rows
-  // + 8 * (r / 4) + (r % 4) rows + jj * 32 columns
-  const int64_t row0 = m0 + gemm::acc_row<C>(wm, 0, 0);
-  const int64_t col0 = n0 + gemm::acc_col<C>(wn, 0);
-  floatx16 acc[C::TM][C::TN];
-#pragma unroll
-  for (int i = 0; i < C::TM; ++i)
-#pragma unroll
-    for (int jj = 0; jj < C::TN; ++jj)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int dr = i * 32 + 8 * (r >> 2) + (r & 3);
-        const bool ok = row0 + dr < M && col0 + jj * 32 < N;
-        acc[i][jj][r] = preload ? cin.ld32(((row0 + dr) * ldc + col0 + jj * 32) * 4, ok) : 0.f;
-      }
-  gemm::mainloop<C, BUF, false>(j.A + k0, j.lda, j.B + k0, j.ldb, M, N, klen, m0, n0, smem, acc);
-  const float g = (!split && j.scale) ? *j.scale : 1.f;
-  // the per-row factor of the lane's 16 rows of MFMA tile i (rows past M: 0)
-  const float *rsc = split ? nullptr : j.row_scale;
-  auto row_factors = [&](int i, float (&f)[16]) {
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int64_t row = row0 + i * 32 + 8 * (r >> 2) + (r & 3);
-      f[r] = rsc ? (row < M ? rsc[row] * g : 0.f) : g;
-    }
-  };
-  if (cdt == NF_DTYPE_F32) {
-#pragma unroll
-    for (int i = 0; i < C::TM; ++i) {
-      float f[16];
-      row_factors(i, f);
-#pragma unroll
-      for (int jj = 0; jj < C::TN; ++jj)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int dr = i * 32 + 8 * (r >> 2) + (r & 3);
-          const bool ok = row0 + dr < M && col0 + jj * 32 < N;
-          out.st32(((row0 + dr) * ldc + col0 + jj * 32) * 4, ok, acc[i][jj][r] * f[r]);
-        }
-    }
-  } else {
-#pragma unroll
-    for (int i = 0; i < C::TM; ++i) {
-      float f[16];
-      row_factors(i, f);
-#pragma unroll
-      for (int jj = 0; jj < C::TN; ++jj)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int dr = i * 32 + 8 * (r >> 2) + (r & 3);
-          const bool ok = row0 + dr < M && col0 + jj * 32 < N;
-          out.st16(((row0 + dr) * ldc + col0 + jj * 32) * 2, ok,
-                   to_half_bits(acc[i][jj][r] * f[r], cdt));
-        }
+  if constexpr (C::DTL) {
+    if (j.bt) {
+      store_tile<C, BUF, SB, true>(j, M, K, ks, m0, n0, smem);
+      return;
     }
   }
+  store_tile<C, BUF, SB, false>(j, M, K, ks, m0, n0, smem);
 }
 
 // C[m, n] = scale * row_scale[m] * (Cin[m, n] + sum over s = 0 .. S-1 of
@@ -484,31 +570,49 @@ GemmJob<typename C::TI> make_job(const typename C::TI *A, int64_t lda, const typ
   j.dyn = nullptr;
   j.dyn_base = 0;
   j.dyn_rows = 0;
+  j.bt = 0;
+  j.ct = 0;
+  j.ct_vec = 0;
+  j.ldcin = ldc;
   return j;
 }
 
 template <typename TI>
 bool job_buf_ok(const GemmJob<TI> &j) {
-  return j.tiles == 0 || (buf_ok<TI>(j.A, j.lda, j.M, j.K) && buf_ok<TI>(j.B, j.ldb, j.N, j.K));
+  if (j.tiles == 0) return true;
+  if (j.bt)  // B's K rows of ldb elements, read as whole 16-byte vectors
+    return buf_ok<TI>(j.A, j.lda, j.M, j.K) && buf_ok<TI>(j.B, j.ldb, j.K, j.ldb);
+  return buf_ok<TI>(j.A, j.lda, j.M, j.K) && buf_ok<TI>(j.B, j.ldb, j.N, j.K);
 }
 // every buffer the epilogue addresses through a 32-bit offset is under 2 GiB
 template <typename TI>
 bool job_sb_ok(const GemmJob<TI> &j) {
   if (j.tiles == 0) return true;
   if (j.ksplit > 1) return sb_ok(j.M * j.N * (int64_t)sizeof(float));
-  return sb_ok(j.M * j.ldc * (int64_t)dtype_bytes(j.cdt)) &&
-         (!j.Cin || sb_ok(j.M * j.ldc * (int64_t)sizeof(float)));
+  const int64_t rows = j.ct ? j.N : j.M;
+  return sb_ok(rows * j.ldc * (int64_t)dtype_bytes(j.cdt)) &&
+         (!j.Cin || sb_ok(j.M * j.ldcin * (int64_t)sizeof(float)));
 }
 
 // Both jobs in one grid (j1 may be empty: tiles == 0), then the split-K
 // reductions of a split job (unless `reduce` is false: the caller then adds
 // the slices itself, as splitk_reduce_kernel would).
 template <class C>
-int launch_gemm_store(const GemmJob<typename C::TI> &j0, const GemmJob<typename C::TI> &j1,
+int launch_gemm_store(const GemmJob<typename C::TI> &j0_in, const GemmJob<typename C::TI> &j1_in,
                       hipStream_t s, bool reduce = true) {
+  GemmJob<typename C::TI> j0 = j0_in, j1 = j1_in;
+  for (auto *jp : {&j0, &j1})  // the LDS-transposed store where it applies
+    jp->ct_vec = C::DTL && jp->ct && !jp->row_scale && jp->M % 8 == 0 && jp->ldc % 8 == 0;
   const int64_t total = (int64_t)j0.tiles + j1.tiles;
   if (total == 0) return NF_OK;
   if (total > 0x7fffffffLL) return set_error(NF_ERR_ARG, "gemm: too many tiles");
+  for (const auto *jp : {&j0, &j1}) {
+    if (jp->tiles == 0) continue;
+    if (jp->bt && (!C::DTL || !job_buf_ok(*jp)))
+      return set_error(NF_ERR_ARG, "gemm: an N-major B needs 16-bit operands on the buffer path");
+    if (jp->ct && jp->ksplit > 1)
+      return set_error(NF_ERR_ARG, "gemm: a transposed C cannot be split along K");
+  }
   const dim3 grid((unsigned)total);
   const bool sb = job_sb_ok(j0) && job_sb_ok(j1);
   const bool buf = job_buf_ok(j0) && job_buf_ok(j1);

@@ -40,3 +40,27 @@ extern "C" int nf_gemm_nt(const void *A, int64_t lda, const void *B, int64_t ldb
   }
   return set_error(NF_ERR_DTYPE, "nf_gemm_nt: dtype %d unsupported", dtype);
 }
+
+extern "C" int nf_gemm_nn(const void *A, int64_t lda, const void *B, int64_t ldb, float *C,
+                          int64_t ldc, int64_t M, int64_t N, int64_t K, int c_transposed,
+                          void *stream) {
+  if (M < 0 || N < 0 || K < 0) return set_error(NF_ERR_ARG, "nf_gemm_nn: negative size");
+  if (M > 0x7fffffffLL || N > 0x7fffffffLL || K > 0x7fffffffLL)
+    return set_error(NF_ERR_ARG, "nf_gemm_nn: a size exceeds int32");
+  if (M == 0 || N == 0) return NF_OK;
+  if (!A || !B || !C) return set_error(NF_ERR_ARG, "nf_gemm_nn: null pointer");
+  if (lda < K || ldb < N || ldc < (c_transposed ? M : N))
+    return set_error(NF_ERR_ARG, "nf_gemm_nn: bad leading dim");
+  if (((M + 255) / 256) * ((N + 255) / 256) > 0x7fffffffLL)
+    return set_error(NF_ERR_ARG, "nf_gemm_nn: grid too large");
+  using C16 = MainCfg<bf16>;
+  auto j = make_job<C16>((const bf16 *)A, lda, (const bf16 *)B, ldb, nullptr, C, NF_DTYPE_F32,
+                         nullptr, ldc, M, N, K);
+  j.bt = 1;
+  j.ct = c_transposed ? 1 : 0;
+  if (!job_buf_ok(j))
+    return set_error(NF_ERR_ARG, "nf_gemm_nn: needs lda, K and ldb multiples of 8, 16-byte "
+                     "aligned operands, each under 2 GiB");
+  const GemmJob<bf16> none{};
+  return launch_gemm_store<C16>(j, none, static_cast<hipStream_t>(stream));
+}

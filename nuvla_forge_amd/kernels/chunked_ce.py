@@ -27,13 +27,15 @@ device-to-host read per call (skipped while a graph is being captured).
 Host tensors (and ``force_reference=True``) run the reference's own row-chunk
 loop in ATen (chunked_ce.py:133-167 with ``_ce_chunk_torch``, :101-117).
 
-``chunk_size`` keeps the reference's meaning, rows per chunk (rounded up to
-the 256-row MFMA tile here, and counting only valid rows): a chunk's
-probabilities are held in the input type in both layouts the two gradient
-products read, 4 * chunk_size * V bytes in bf16 -- the reference's
-[chunk_size, V] fp32 logits tile.  Bigger chunks are faster (fewer passes
-over the fp32 dW accumulator); results do not depend on it beyond fp
-rounding.
+``chunk_size`` bounds a chunk's memory as the reference's rows per chunk do
+(counting only valid rows): a chunk's probabilities take 4 * chunk_size * V
+bytes, the reference's [chunk_size, V] fp32 logits tile.  In bf16, where
+chunk_size rows do not cover every row at once, they are held once (the dW
+product reads them transposed), so a chunk holds 2 * chunk_size rows
+(rounded up to the 256-row MFMA tile); otherwise, and in fp32, both layouts
+the gradient products read are held for chunk_size rows.  Bigger chunks are
+faster (fewer passes over the fp32 dW accumulator); results do not depend on
+it beyond fp rounding.
 
 Element types: under bf16 autocast for the device the products run in bf16
 (MFMA, fp32 accumulation) whatever the input types, as the reference's

@@ -230,19 +230,27 @@ def _ceil(a: int, b: int) -> int:
 def _ce_state_closed_form(m, d, v, chunk_rows, es=2):
     """The state nf_ce_fwd leaves for nf_ce_bwd, term by term (each buffer
     256-byte aligned): scalars, pos [M], the fp32 row factors [M], W^T
-    [D, V8], the scaled Hc^T [D, M8], one chunk's E [C, V8] and E^T [V, C],
-    fp32 dH rows [M, D], and the fp32 dW accumulator when more than one chunk
-    (C = chunk_rows rounded up to 256, at most M rounded up to 256)."""
+    [D, V8], the scaled Hc^T [D, M8], one chunk's E, fp32 dH rows [M, D], and
+    the fp32 dW accumulator when more than one chunk.  bf16 (es 2), when
+    chunk_rows rows would not cover M in one chunk, holds E once, [C, V8] with
+    C = 2 * chunk_rows rounded up to 256, and the accumulator transposed,
+    [D, V8]; otherwise E [C, V8] and E^T [V, C] with C = chunk_rows rounded
+    up to 256, and the accumulator [V, D].  C is at most M rounded up to 256."""
     a = lambda x: _ceil(x, 256) * 256  # noqa: E731
-    c = min(_ceil(chunk_rows, 256) * 256, _ceil(m, 256) * 256)
+    mcap = _ceil(m, 256) * 256
+    want = min(chunk_rows, mcap)
+    single = es == 2 and _ceil(want, 256) * 256 < mcap
+    c = min(_ceil(2 * want if single else want, 256) * 256, mcap)
     v8, m8 = _ceil(v, 8) * 8, _ceil(m, 8) * 8
     nch = _ceil(m, c)
-    return (a(64) + a(4 * m) + a(4 * m) + a(es * d * v8) + a(es * d * m8) + a(es * c * v8)
-            + a(es * v * c) + a(4 * m * d) + (a(4 * v * d) if nch > 1 else 0))
+    e_bytes = a(es * c * v8) + (0 if single else a(es * v * c))
+    acc = (a(4 * d * v8) if single else a(4 * v * d)) if nch > 1 else 0
+    return (a(64) + a(4 * m) + a(4 * m) + a(es * d * v8) + a(es * d * m8) + e_bytes
+            + a(4 * m * d) + acc)
 
 
 def sb_at(L, chunk_rows):
-    return L.nf_ce_state_bytes(4096, 2048, 32000, chunk_rows, 1)
+    return L.nf_ce_state_bytes(16384, 2048, 32000, chunk_rows, 1)
 
 
 def test_ce_state_and_workspace_sizes():
@@ -251,9 +259,10 @@ def test_ce_state_and_workspace_sizes():
                         (512, 384, 32000, 1024), (300, 72, 1030, 100), (17, 36, 333, 7)]:
         assert L.nf_ce_state_bytes(m, d, v, cr, 1) == _ce_state_closed_form(m, d, v, cr), (m, cr)
         assert L.nf_ce_state_bytes(m, d, v, cr, 0) == _ce_state_closed_form(m, d, v, cr, es=4)
-    # a chunk's P and PT (bf16) are the reference's [chunk_size, V] fp32 logits
-    # tile: each 1024 more rows per chunk hold 4 * 1024 * 32000 more bytes
-    more = L.nf_ce_state_bytes(4096, 2048, 32000, 2048, 1) - sb_at(L, 1024)
+    # a chunk's E (bf16, 2 * chunk_size rows, once) is the bytes of the
+    # reference's [chunk_size, V] fp32 logits tile: each 1024 more rows of
+    # chunk_size hold 4 * 1024 * 32000 more bytes
+    more = sb_at(L, 2048) - sb_at(L, 1024)
     assert more == 4 * 1024 * 32000
     assert L.nf_ce_state_bytes(4096, 2048, 32000, 1024, 2) == 0  # fp16 unsupported
     assert L.nf_ce_state_bytes(0, 2048, 32000, 1024, 1) == 0
@@ -274,6 +283,11 @@ def test_ce_argument_validation():
     M_ = _measure.lib()
     assert M_.nf_gemm_nt(FAKE, 1 << 40, FAKE, 1 << 40, FAKE, 16, 16, 16, 1 << 40, 1,
                          None) == NF_ERR_ARG and "int32" in _err()
+    # the N-major path needs whole 16-byte vectors: K = 20, then ldb < N
+    assert M_.nf_gemm_nn(FAKE, 24, FAKE, 16, FAKE, 16, 16, 16, 20, 0,
+                         None) == NF_ERR_ARG and "multiples of 8" in _err()
+    assert M_.nf_gemm_nn(FAKE, 24, FAKE, 8, FAKE, 16, 16, 16, 24, 0, None) == NF_ERR_ARG
+    assert M_.nf_gemm_nn(FAKE, 24, FAKE, 16, FAKE, 8, 16, 16, 24, 1, None) == NF_ERR_ARG  # ldc < M
     ws = L.nf_ce_workspace(16, 8, 50, 64, 1)
     base = [FAKE, FAKE, FAKE]
     out = [FAKE, FAKE, FAKE, None, FAKE]
