@@ -19,8 +19,8 @@
 //                 lane holds each token's logits along the vocabulary); per
 //                 (vocabulary tile of WTM rows, token) the max and the sum of
 //                 exp(S - max), the target logit, and E = exp(S - mref) in
-//                 the input type, row-major [crows, ldp] and transposed
-//                 [V, crows];
+//                 the input type, row-major [crows, ldp] and (unless E is
+//                 held once: "single", see Plan) transposed [V, crows];
 //      ce_lse:    lse per row from the tile statistics (fixed order), the
 //                 row's loss lse - S[target], the row factor cfac =
 //                 exp(mref - lse) / n, and the one-hot term folded into E's
@@ -29,16 +29,19 @@
 //      ce_scale_hct: Hct = (cfac * Hc_c)^T, the dW product's B operand; in
 //                 the last chunk's launch, also the mean loss;
 //      gradient products of every chunk but the last (one launch):
-//                 dW_acc (+)= E^T_c Hct_c^T  (fp32 [V, D], K = the chunk's rows)
+//                 dW_acc (+)= E^T_c Hct_c^T  (fp32 [V, D], K = the chunk's rows;
+//                             single: dW_acc^T (+)= Hct_c E_c, fp32 [D, V],
+//                             E read N-major)
 //                 dHc_c   = cfac * (E_c Wt^T) (fp32, K = V, split along K)
 // Backward (nf_ce_bwd, with the loss's grad_output g): the last chunk's
-// products, dW = g * (dW_acc + E^T Hct^T) written in dweight's type, and the
-// scatter of dHc back to the hidden rows as g * dH (0 for ignored rows).
+// products, dW = g * (dW_acc + E^T Hct^T) written in dweight's type (single:
+// formed transposed and stored through LDS as [V, D]), and the scatter of
+// dHc back to the hidden rows as g * dH (0 for ignored rows).
 //
-// Memory: the state kept between the calls holds one chunk's E in both
-// layouts, W^T, the scaled Hc^T and the fp32 dH rows, plus the fp32 dW
-// accumulator when there is more than one chunk; the [M, V] logits never
-// exist (unless one chunk covers M).
+// Memory: the state kept between the calls holds one chunk's E (once, for
+// twice the rows, when single), W^T, the scaled Hc^T and the fp32 dH rows,
+// plus the fp32 dW accumulator when there is more than one chunk; the [M, V]
+// logits never exist (unless one chunk covers M).
 #include <type_traits>
 
 #include "gemm_store.h"
@@ -193,7 +196,8 @@ __global__ __launch_bounds__(kGatherThreads) void ce_gather_kernel(
 // rows [t * WTM, (t + 1) * WTM): stats[t * crows + token] = (max, sum
 // exp(S - max)), taken from the sum of E (see the epilogue).  The target
 // logit comes from the one lane holding it.  E = exp(S - mref) goes out
-// row-major [token, ldp] (columns V..ldp zero) and transposed [V, ldet]
+// row-major [token, ldp] (columns V..ldp zero, tokens past the chunk's rows
+// zero up to a multiple of 8) and, when ET is given, transposed [V, ldet]
 // (tokens past the chunk's rows zero up to a multiple of 8): with 16-bit
 // 256 x 256 tiles through LDS (free once the K loop ends) -- element (t, c)
 // at byte t * 512 + 2 * (c ^ e_swz(t)), the XOR moving whole 8-element
