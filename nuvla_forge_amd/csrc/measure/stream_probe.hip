@@ -2,10 +2,12 @@
 // arrays and writes W arrays of 16-byte vectors with no dependency between
 // its accesses (no row reduction, no LDS, no barrier), two vectors per thread
 // per pass with all their loads issued first, non-temporal stores like the
-// row kernels', up to 8192 blocks (the best of 2048 / 4096 / 8192 blocks,
-// one or two vectors per pass, plain or non-temporal stores on the cfg2 and
-// cfg5 sizes).  bench.py times it on the adaLN step's traffic
-// shapes (forward: 2 reads + 2 writes; backward: 4 reads + 2 writes) so that
+// row kernels', and non-temporal loads under the row kernels' rule
+// (nt_loads_for: more input than the Infinity Cache holds), up to 8192
+// blocks (the best of 2048 / 4096 / 8192 blocks, one or two vectors per
+// pass, plain or non-temporal stores on the cfg2 and cfg5 sizes).  bench.py
+// times it on the adaLN step's traffic shapes (forward: 2 reads + 2 writes;
+// backward: 4 reads + 2 writes) so that
 // each row kernel can be set against what plain streaming reaches on the
 // same box, the same bytes and the same cache state.  A measurement aid
 // only; no op of the library calls it.
@@ -25,7 +27,7 @@ struct StreamArgs {
   int64_t n;  // 16-byte vectors per array
 };
 
-template <int R, int W>
+template <int R, int W, bool NTL>
 __global__ __launch_bounds__(kStreamThreads) void stream_probe_kernel(StreamArgs a) {
   constexpr int U = kStreamUnroll;
   const int64_t stride = (int64_t)gridDim.x * kStreamThreads * U;
@@ -36,7 +38,8 @@ __global__ __launch_bounds__(kStreamThreads) void stream_probe_kernel(StreamArgs
     for (int u = 0; u < U; ++u) {
       const int64_t i = i0 + (int64_t)u * kStreamThreads;
 #pragma unroll
-      for (int r = 0; r < R; ++r) v[u][r] = i < a.n ? a.in[r][i] : u32x4{0u, 0u, 0u, 0u};
+      for (int r = 0; r < R; ++r)
+        v[u][r] = i < a.n ? stream_load16<NTL>(&a.in[r][i]) : u32x4{0u, 0u, 0u, 0u};
     }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
@@ -106,13 +109,17 @@ extern "C" int nf_stream_probe(int reads, int writes, const void *in0, const voi
   int64_t blocks = (n16 + kStreamThreads * kStreamUnroll - 1) / (kStreamThreads * kStreamUnroll);
   if (blocks > kStreamMaxBlocks) blocks = kStreamMaxBlocks;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  if (writes == 0)
+  const bool ntl = nt_loads_for((int64_t)reads * n16 * 16);
+  if (writes == 0)  // plain loads: an evicting pass must allocate in the caches
     stream_read_kernel<<<(unsigned)blocks, kStreamThreads, 0, s>>>(a);
   else if (reads == 1)
-    stream_probe_kernel<1, 1><<<(unsigned)blocks, kStreamThreads, 0, s>>>(a);
+    ntl ? stream_probe_kernel<1, 1, true><<<(unsigned)blocks, kStreamThreads, 0, s>>>(a)
+        : stream_probe_kernel<1, 1, false><<<(unsigned)blocks, kStreamThreads, 0, s>>>(a);
   else if (reads == 2)
-    stream_probe_kernel<2, 2><<<(unsigned)blocks, kStreamThreads, 0, s>>>(a);
+    ntl ? stream_probe_kernel<2, 2, true><<<(unsigned)blocks, kStreamThreads, 0, s>>>(a)
+        : stream_probe_kernel<2, 2, false><<<(unsigned)blocks, kStreamThreads, 0, s>>>(a);
   else
-    stream_probe_kernel<4, 2><<<(unsigned)blocks, kStreamThreads, 0, s>>>(a);
+    ntl ? stream_probe_kernel<4, 2, true><<<(unsigned)blocks, kStreamThreads, 0, s>>>(a)
+        : stream_probe_kernel<4, 2, false><<<(unsigned)blocks, kStreamThreads, 0, s>>>(a);
   return check_launch("nf_stream_probe");
 }
