@@ -1,8 +1,9 @@
 """nf_stream_probe, the streaming ceiling bench.py sets the row kernels
 against (GPU): every output vector is the xor of the input vectors plus the
 output's index in each 32-bit lane, for each supported (reads, writes) pair,
-at a size that fits one pass of the grid and one that needs the grid-stride
-loop (more vectors than 8192 blocks x 256 threads x 2)."""
+at a size that fits one pass of the grid and ones that need the grid-stride
+loop (more vectors than 8192 blocks x 256 threads x 2), the largest with
+4 x 96 MB of input, past the non-temporal-load threshold (320 MiB)."""
 
 from __future__ import annotations
 
@@ -16,7 +17,7 @@ pytestmark = pytest.mark.gpu
 
 
 @pytest.mark.parametrize("reads,writes", [(1, 1), (2, 2), (4, 2)])
-@pytest.mark.parametrize("n16", [1000, 4_500_001])
+@pytest.mark.parametrize("n16", [1000, 4_500_001, 6_000_001])
 def test_stream_probe_values(cuda, reads, writes, n16):
     note(f"stream probe reads={reads} writes={writes} n16={n16}")
     g = torch.Generator().manual_seed(reads * 10 + writes)
