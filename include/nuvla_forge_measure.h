@@ -32,10 +32,11 @@ int nf_gemm_nt(const void *A, int64_t lda, const void *B, int64_t ldb,
 /* ------------------------------------------------------------------------
  * Test hook with no counterpart in the reference: C = A[M, K] @ B[K, N]
  * (bf16 A and B, fp32 C) through the MFMA core's N-major-B path: A
- * row-major with unit-stride K (lda, K multiples of 8), B row-major with
- * unit-stride N (ldb >= N, a multiple of 8; columns up to ldb are read),
- * 16-byte aligned.  C[m, n] is stored at C[m * ldc + n], or at
- * C[n * ldc + m] when c_transposed is nonzero.
+ * row-major with unit-stride K, B row-major with unit-stride N (ldb >= N;
+ * columns up to ldb are read).  With lda, K and ldb multiples of 8, 16-byte
+ * aligned operands each under 2 GiB, the operands go global -> LDS by the
+ * buffer unit; otherwise through registers.  C[m, n] is stored at
+ * C[m * ldc + n], or at C[n * ldc + m] when c_transposed is nonzero.
  * ---------------------------------------------------------------------- */
 int nf_gemm_nn(const void *A, int64_t lda, const void *B, int64_t ldb,
                float *C, int64_t ldc, int64_t M, int64_t N, int64_t K,

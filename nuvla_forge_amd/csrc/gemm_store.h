@@ -113,7 +113,7 @@ struct GemmJob {
   int64_t dyn_base;  // the extent is *dyn - dyn_base, clamped to [0, M or K]
   int dyn_rows;      // 1: the dynamic extent is M; 0: it is K
   // bt: B is given N-major, B[k, n] at B[k * ldb + n] (columns up to ldb may
-  // be read; 16-bit inputs on the direct-to-LDS path only).  ct: C is stored
+  // be read; 16-bit inputs, DCfg only).  ct: C is stored
   // transposed, element (m, n) at C[n * ldc + m] (no K split); Cin keeps
   // [M, ldcin].
   int bt, ct;
@@ -608,8 +608,8 @@ int launch_gemm_store(const GemmJob<typename C::TI> &j0_in, const GemmJob<typena
   if (total > 0x7fffffffLL) return set_error(NF_ERR_ARG, "gemm: too many tiles");
   for (const auto *jp : {&j0, &j1}) {
     if (jp->tiles == 0) continue;
-    if (jp->bt && (!C::DTL || !job_buf_ok(*jp)))
-      return set_error(NF_ERR_ARG, "gemm: an N-major B needs 16-bit operands on the buffer path");
+    if (jp->bt && !C::DTL)
+      return set_error(NF_ERR_ARG, "gemm: an N-major B needs 16-bit operands");
     if (jp->ct && jp->ksplit > 1)
       return set_error(NF_ERR_ARG, "gemm: a transposed C cannot be split along K");
   }

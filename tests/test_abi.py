@@ -283,9 +283,9 @@ def test_ce_argument_validation():
     M_ = _measure.lib()
     assert M_.nf_gemm_nt(FAKE, 1 << 40, FAKE, 1 << 40, FAKE, 16, 16, 16, 1 << 40, 1,
                          None) == NF_ERR_ARG and "int32" in _err()
-    # the N-major path needs whole 16-byte vectors: K = 20, then ldb < N
-    assert M_.nf_gemm_nn(FAKE, 24, FAKE, 16, FAKE, 16, 16, 16, 20, 0,
-                         None) == NF_ERR_ARG and "multiples of 8" in _err()
+    # leading dimensions below the extents they hold
+    assert M_.nf_gemm_nn(FAKE, 16, FAKE, 16, FAKE, 16, 16, 16, 24, 0,
+                         None) == NF_ERR_ARG and "leading dim" in _err()  # lda < K
     assert M_.nf_gemm_nn(FAKE, 24, FAKE, 8, FAKE, 16, 16, 16, 24, 0, None) == NF_ERR_ARG
     assert M_.nf_gemm_nn(FAKE, 24, FAKE, 16, FAKE, 8, 16, 16, 24, 1, None) == NF_ERR_ARG  # ldc < M
     ws = L.nf_ce_workspace(16, 8, 50, 64, 1)

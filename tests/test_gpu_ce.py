@@ -224,7 +224,11 @@ def test_ce_large_vocabulary(cuda, dtype, chunk):
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("m,d,v,chunk", [(17, 36, 333, 7), (300, 40, 1030, 1000), (9, 4, 6, 1),
-                                         (130, 264, 129, 64)])
+                                         (130, 264, 129, 64),
+                                         # bf16 holds E once here (chunks of 256 rows): the
+                                         # dW product reads it N-major; D = 36 stores dW
+                                         # transposed element by element, D = 72 through LDS
+                                         (600, 36, 333, 100), (1100, 72, 1000, 200)])
 def test_ce_ragged_shapes(cuda, dtype, m, d, v, chunk):
     note(f"ce ragged dtype={dtype} m={m} d={d} v={v} chunk={chunk}")
     hid, w, tgt = _ce_inputs(m, d, v, dtype, cuda, seed=4, w_std=0.3,

@@ -3,7 +3,8 @@ through transposing LDS reads) and its transposed store (C[n * ldc + m]),
 which the cross entropy's dW product uses in bf16: against float64 products
 at ragged sizes (K, N and M not multiples of the 256 x 256 tile or the
 64-wide stage, columns between N and ldb present but excluded, M not a
-multiple of 8 for the per-element transposed store).  The hook's argument
+multiple of 8 for the per-element transposed store, K and ldb not multiples
+of 8 for the register-staged operand copies).  The hook's argument
 checks run on the CPU (tests/test_abi.py)."""
 
 from __future__ import annotations
@@ -21,7 +22,9 @@ pytestmark = pytest.mark.gpu
 @pytest.mark.parametrize("m,n,k,ldb", [(256, 256, 64, 256), (300, 1000, 264, 1008),
                                        (513, 777, 1000, 784), (264, 1000, 200, 1000),
                                        (2048, 300, 64, 304), (1, 8, 8, 8), (40, 16, 2000, 24),
-                                       (2048, 4000, 1024, 4000)])
+                                       (2048, 4000, 1024, 4000),
+                                       # K and ldb not multiples of 8: operands through registers
+                                       (100, 200, 37, 203), (300, 257, 300, 261)])
 @pytest.mark.parametrize("ct", [0, 1])
 def test_gemm_nn_matches_numpy(cuda, m, n, k, ldb, ct):
     note(f"gemm_nn m={m} n={n} k={k} ldb={ldb} ct={ct}")
