@@ -605,16 +605,16 @@ def bench_ce(args, dev):
                 "tflops": tflops, "mfma_frac": tflops / MFMA_BF16_PEAK_TFLOPS}
 
     # The figure of record is the reference's default chunk_size 1024
-    # (chunked_ce.py:189): E held once in bf16 for 2048 rows at a time, the
-    # bytes of the reference's [1024, V] fp32 logits tile, so two chunks of
-    # the 3687 valid rows with the fp32 dW accumulator between them.  Beside
-    # it 512 (four chunks of 1024 rows) and 4096 (one chunk over every valid
-    # row in both layouts: E and E^T of all 3687 rows, 2 x 236 MB, what the
-    # reference's [4096, V] fp32 tile holds at that setting).
+    # (chunked_ce.py:189).  chunk_size bounds E and the dW accumulator by the
+    # bytes the reference's loop holds for them (its fp32 [1024, V] tile and
+    # fp32 [V, D] accumulator, 393 MB): E held once in bf16 for all 3687
+    # valid rows takes 262 MB with no accumulator, so one chunk.  Beside it
+    # 4096: one chunk in both layouts (E and E^T, 2 x 262 MB, inside the
+    # reference's 786 MB at that setting).
     main = run(1024)
     return {"m": m, "d": d, "v": v, "m_valid": m_valid, "alg_flops": flops, **main,
-            "chunk_512": run(512),
-            "chunk_4096_one_chunk": {**run(4096), "holds": "E and E^T of every valid row"}}
+            "holds": "E of every valid row, once",
+            "chunk_4096": {**run(4096), "holds": "E and E^T of every valid row"}}
 
 
 def bench_stress(args, dev):

@@ -758,13 +758,32 @@ inline Plan make_plan(int64_t M, int64_t D, int64_t V, int64_t chunk_rows) {
   Plan P{};
   const int64_t mcap = round_up(M, 256);
   const int64_t want = chunk_rows < 1 ? 1 : (chunk_rows > mcap ? mcap : chunk_rows);
-  // E held once where that saves chunks: with one chunk over every row the
-  // two layouts cost no accumulator pass, and their dW product (K-contiguous
-  // operands) is faster than the N-major one (reasoning head M512 D384
-  // V32000: 116 us against 130 us).
-  P.single = sizeof(TI) == 2 && round_up(want, 256) < mcap;
-  const int64_t cr = round_up(P.single ? 2 * want : want, 256);
-  P.crows = cr > mcap ? mcap : cr;
+  if (sizeof(TI) == 2) {
+    // chunk_rows bounds E and the dW accumulator together by what the
+    // reference's chunk loop holds for the same roles: an fp32
+    // [chunk_rows, V] logits tile and an fp32 [V, D] dW accumulator, i.e.
+    // 2 (chunk_rows + D) rows of 16-bit E.  The first form inside it of:
+    //  * one chunk, E in both layouts (2 mcap rows), for D >= 2048 only:
+    //    the dW product on K-contiguous operands (one chunk, V 32000, fwd+bwd:
+    //    M4096 D4096 2.96 ms against 3.06 held once; M8192 D2048 3.02
+    //    against 3.05; M4096 D2048 level);
+    //  * one chunk, E held once (mcap rows), no accumulator pass (at D 384 -
+    //    1024 also faster than both layouts: M4096 D384 0.52 ms against
+    //    0.55, M1024 D1024 0.30-0.31 against 0.32; at cfg4, M4096 D2048 with
+    //    3687 valid rows, the accumulator alone is the bytes of E for every
+    //    row, and chunk_size 1024 runs in 1.48 ms against 1.64 in two chunks);
+    //  * chunks of 2 chunk_rows rows held once, beside the fp32 accumulator.
+    const int64_t budget = 2 * ((chunk_rows < M ? chunk_rows : M) + D);
+    P.single = D < 2048 || 2 * mcap > budget;
+    const int64_t cr = P.single && mcap > budget ? round_up(2 * want, 256) : mcap;
+    P.crows = cr > mcap ? mcap : cr;
+  } else {
+    // fp32: chunks of chunk_rows rows in both layouts (E alone is the
+    // reference's tile) with the fp32 accumulator between them
+    P.single = false;
+    const int64_t cr = round_up(want, 256);
+    P.crows = cr > mcap ? mcap : cr;
+  }
   P.nch = (M + P.crows - 1) / P.crows;
   P.ldp = round_up(V, 8);
   P.ldwt = P.ldp;

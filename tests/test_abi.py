@@ -231,16 +231,25 @@ def _ce_state_closed_form(m, d, v, chunk_rows, es=2):
     """The state nf_ce_fwd leaves for nf_ce_bwd, term by term (each buffer
     256-byte aligned): scalars, pos [M], the fp32 row factors [M], W^T
     [D, V8], the scaled Hc^T [D, M8], one chunk's E, fp32 dH rows [M, D], and
-    the fp32 dW accumulator when more than one chunk.  bf16 (es 2), when
-    chunk_rows rows would not cover M in one chunk, holds E once, [C, V8] with
-    C = 2 * chunk_rows rounded up to 256, and the accumulator transposed,
-    [D, V8]; otherwise E [C, V8] and E^T [V, C] with C = chunk_rows rounded
-    up to 256, and the accumulator [V, D].  C is at most M rounded up to 256."""
+    the fp32 dW accumulator when more than one chunk.  bf16 (es 2) has a
+    budget of 2 * (min(chunk_rows, M) + D) rows of E (the bytes of the
+    reference's fp32 [chunk_rows, V] tile and fp32 [V, D] accumulator) and
+    takes the first of: one chunk in both layouts, E [C, V8] and E^T [V, C]
+    (D >= 2048 and 2 C inside the budget); one chunk held once, E [C, V8] (C
+    inside the budget); chunks of C = 2 * chunk_rows rows rounded up to 256
+    held once, with the accumulator transposed, [D, V8].  fp32 holds chunks
+    of C = chunk_rows rows rounded up to 256 in both layouts with the
+    accumulator [V, D].  C is at most M rounded up to 256."""
     a = lambda x: _ceil(x, 256) * 256  # noqa: E731
     mcap = _ceil(m, 256) * 256
     want = min(chunk_rows, mcap)
-    single = es == 2 and _ceil(want, 256) * 256 < mcap
-    c = min(_ceil(2 * want if single else want, 256) * 256, mcap)
+    if es == 2:
+        budget = 2 * (min(chunk_rows, m) + d)
+        single = d < 2048 or 2 * mcap > budget
+        c = min(a(2 * want) if single and mcap > budget else mcap, mcap)
+    else:
+        single = False
+        c = min(a(want), mcap)
     v8, m8 = _ceil(v, 8) * 8, _ceil(m, 8) * 8
     nch = _ceil(m, c)
     e_bytes = a(es * c * v8) + (0 if single else a(es * v * c))
@@ -255,10 +264,26 @@ def sb_at(L, chunk_rows):
 
 def test_ce_state_and_workspace_sizes():
     L = _lib.lib()
-    for m, d, v, cr in [(4096, 2048, 32000, 1024), (4096, 2048, 32000, 4096),
-                        (512, 384, 32000, 1024), (300, 72, 1030, 100), (17, 36, 333, 7)]:
+    shapes = [(4096, 2048, 32000, 1024), (4096, 2048, 32000, 4096), (4096, 4096, 32000, 4096),
+              (4096, 4096, 32000, 1024), (16384, 2048, 32000, 1024), (16384, 384, 32000, 1024),
+              (512, 384, 32000, 1024), (300, 72, 1030, 100), (17, 36, 333, 7)]
+    for m, d, v, cr in shapes:
         assert L.nf_ce_state_bytes(m, d, v, cr, 1) == _ce_state_closed_form(m, d, v, cr), (m, cr)
         assert L.nf_ce_state_bytes(m, d, v, cr, 0) == _ce_state_closed_form(m, d, v, cr, es=4)
+    # bf16: E and the dW accumulator together stay within what the
+    # reference's chunk loop holds for the same roles at the same chunk_size
+    # (an fp32 [chunk_size, V] tile, an fp32 [V, D] accumulator), up to the
+    # rounding of a chunk to 256 rows
+    for m, d, v, cr in shapes:
+        a = lambda x: _ceil(x, 256) * 256  # noqa: E731
+        v8, m8 = _ceil(v, 8) * 8, _ceil(m, 8) * 8
+        rest = a(64) + 2 * a(4 * m) + a(2 * d * v8) + a(2 * d * m8) + a(4 * m * d)
+        e_acc = L.nf_ce_state_bytes(m, d, v, cr, 1) - rest
+        assert e_acc <= 4 * v8 * (min(cr, m) + d) + 4 * 256 * v8 + 512, (m, d, cr)
+    # cfg4 at the reference's default chunk_size holds E once for every row
+    # (262 MB) and no accumulator: the reference's accumulator alone is 262 MB
+    assert (L.nf_ce_state_bytes(4096, 2048, 32000, 1024, 1)
+            == _ce_state_closed_form(4096, 2048, 32000, 4096 * 4, es=2) - 2 * 4096 * 32000)
     # a chunk's E (bf16, 2 * chunk_size rows, once) is the bytes of the
     # reference's [chunk_size, V] fp32 logits tile: each 1024 more rows of
     # chunk_size hold 4 * 1024 * 32000 more bytes
