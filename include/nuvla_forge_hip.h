@@ -214,14 +214,15 @@ int nf_adaln_bwd_noalloc(const void *dh_up, const void *dout, const void *x,
  * a chunk at a time: a chunk's logits are held as exp(logit - the row's
  * target logit) in the input type, with the target entry carrying the
  * one-hot term and a per-row fp32 factor making them (softmax - onehot) *
- * inv, so memory is O(chunk_rows * V), not O(M * V), as the reference's row
- * chunks (chunk_size) are; results do not depend on chunk_rows beyond fp
- * rounding.  Where chunk_rows rows (rounded up to 256) do not cover M, bf16
- * holds a chunk's logits once (row-major; the dweight product reads them
- * transposed) and so takes 2 * chunk_rows rows per chunk (rounded up to
- * 256): 4 * chunk_rows * V bytes, the reference's fp32 [chunk_size, V]
- * logits tile.  Otherwise, and for fp32, they are held in both layouts the
- * products read, chunk_rows rows per chunk (rounded up to 256).
+ * inv; results do not depend on chunk_rows beyond fp rounding.  bf16 keeps
+ * a chunk's logits and the fp32 dweight accumulator together within the
+ * bytes the reference's row chunks hold for them (an fp32 [chunk_rows, V]
+ * tile and an fp32 [V, D] accumulator, up to 256-row rounding): one chunk
+ * over every row with no accumulator where that fits (logits held in both
+ * layouts the products read for D >= 2048 when those fit, otherwise once,
+ * row-major, the dweight product reading them transposed), else chunks of
+ * 2 * chunk_rows rows held once beside the accumulator.  fp32 holds chunks
+ * of chunk_rows rows (rounded up to 256) in both layouts.
  * The forward also runs the gradient products of every chunk but the last
  * (into fp32 accumulators in `state`).  Replaces _ChunkedCrossEntropy.forward
  * and the `_ce_fwd_bwd` kernel, nuvla_forge/kernels/chunked_ce.py:49-98 and

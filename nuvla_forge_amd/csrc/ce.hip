@@ -40,8 +40,9 @@
 //
 // Memory: the state kept between the calls holds one chunk's E (once, for
 // twice the rows, when single), W^T, the scaled Hc^T and the fp32 dH rows,
-// plus the fp32 dW accumulator when there is more than one chunk; the [M, V]
-// logits never exist (unless one chunk covers M).
+// plus the fp32 dW accumulator when there is more than one chunk; E and the
+// accumulator stay within the bytes the reference's chunk loop holds for
+// them (see make_plan), so E covers every row at once only where that fits.
 #include <type_traits>
 
 #include "gemm_store.h"

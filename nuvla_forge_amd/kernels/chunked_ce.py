@@ -27,15 +27,17 @@ device-to-host read per call (skipped while a graph is being captured).
 Host tensors (and ``force_reference=True``) run the reference's own row-chunk
 loop in ATen (chunked_ce.py:133-167 with ``_ce_chunk_torch``, :101-117).
 
-``chunk_size`` bounds a chunk's memory as the reference's rows per chunk do
-(counting only valid rows): a chunk's probabilities take 4 * chunk_size * V
-bytes, the reference's [chunk_size, V] fp32 logits tile.  In bf16, where
-chunk_size rows do not cover every row at once, they are held once (the dW
-product reads them transposed), so a chunk holds 2 * chunk_size rows
-(rounded up to the 256-row MFMA tile); otherwise, and in fp32, both layouts
-the gradient products read are held for chunk_size rows.  Bigger chunks are
-faster (fewer passes over the fp32 dW accumulator); results do not depend on
-it beyond fp rounding.
+``chunk_size`` bounds memory by what the reference's row-chunk loop holds at
+the same setting: in bf16 a chunk's probabilities and the fp32 dW
+accumulator together stay within the bytes of its fp32 [chunk_size, V]
+logits tile plus its fp32 [V, D] dW accumulator (up to 256-row rounding).
+Where the probabilities of every row fit that, one chunk takes them all with
+no accumulator (held once, or for D >= 2048 in both layouts the gradient
+products read when those fit); otherwise chunks of 2 * chunk_size valid
+rows are held once (the dW product reads them transposed) beside the
+accumulator.  fp32 holds chunks of chunk_size rows in both layouts.  Fewer
+chunks are faster (no passes over the accumulator); results do not depend
+on chunk_size beyond fp rounding.
 
 Element types: under bf16 autocast for the device the products run in bf16
 (MFMA, fp32 accumulation) whatever the input types, as the reference's
@@ -245,7 +247,8 @@ def chunked_cross_entropy(
         hidden: [M, D] pre-projection hidden states.
         lm_weight: [V, D] output embedding.
         targets: [M] int64 class indices, ``ignore_index`` to mask.
-        chunk_size: memory budget in rows of a [chunk_size, V] logits tile.
+        chunk_size: memory budget: the bytes of the reference's fp32
+            [chunk_size, V] logits tile plus its fp32 [V, D] dW accumulator.
         ignore_index: target value that contributes no loss and no gradient.
         force_reference: run the reference's eager row-chunk loop instead.
 
