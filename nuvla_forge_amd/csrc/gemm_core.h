@@ -506,6 +506,181 @@ __device__ __forceinline__ void read_kgroup_kn(const char *stage, int wm, int wn
   }
 }
 
+// ---- 16x16x32 products on K-contiguous operands -------------------------------
+#ifndef NF_MFMA16
+#define NF_MFMA16 1
+#endif
+constexpr bool kMfma16 = NF_MFMA16 != 0;
+
+// v_mfma_f32_16x16x32_bf16 sustains ~14% more than v_mfma_f32_32x32x16_bf16
+// on this chip under its power limit (register-held random bf16 operands, one
+// wavefront per SIMD: 2.06-2.09 against 1.80-1.83 PFLOP/s).  With K-contiguous
+// B the mainloop computes each 32 x 32 accumulator tile of the wavefront as
+// four 16 x 16 products over 32-wide k-groups, product s = 2 ti + tj in the
+// tile's registers 4 s .. 4 s + 3, and hands the tile over in the 32x32x16
+// layout, so every epilogue sees the layout it was written for.  Product
+// (ti, tj) leaves in lane l column 16 tj + l % 16 and rows
+// rA(ti, 4 (l / 16) + q), q = 0..3, where rA(ti, i) is the tile row lane i
+// of its A operand supplies; taking rA(ti, i) = 16 ti + (i with bits 2 and 3
+// swapped), one v_permlane16_swap per register pair (tj = 0, tj = 1) leaves
+// lane l holding column l % 32 and rows 8 (r / 4) + 4 (l / 32) + r % 4, the
+// 32x32x16 layout (the swap is its own inverse, so it also takes a loaded
+// accumulator into the 16 x 16 form).
+template <class C>
+struct Mfma16 {
+  static constexpr int NA = 2 * C::TM, NB = 2 * C::TN;  // operand vectors per k-group
+  static constexpr int KG = C::BK / 32;                 // k-groups per stage
+};
+
+// Operands of 32-wide k-group kg: A vector i = 2 I + ti for tile rows
+// 32 I + rA(ti, lane % 16), B vector j = 2 J + tj for tile columns
+// 32 J + 16 tj + lane % 16, k-vector 4 kg + lane / 16.  Tile row offsets are
+// multiples of 16, so the swizzle only depends on the row's low four bits.
+template <class C>
+__device__ __forceinline__ void read_kgroup16(const char *stage, int wm, int wn, int kg,
+                                              u32x4 (&a)[Mfma16<C>::NA],
+                                              u32x4 (&b)[Mfma16<C>::NB]) {
+  const int l = threadIdx.x & 63;
+  const int r16 = l & 15;
+  const int ra = (r16 & 3) | ((r16 & 4) << 1) | ((r16 & 8) >> 1);
+  const int kv = 4 * kg + (l >> 4);
+  const char *as = stage + (wm * C::WTM + ra) * C::ROW + dtl_slot<C>(ra, kv) * 16;
+  const char *bs = stage + (C::BM + wn * C::WTN + r16) * C::ROW + dtl_slot<C>(r16, kv) * 16;
+#pragma unroll
+  for (int i = 0; i < Mfma16<C>::NA; ++i)
+    a[i] = *reinterpret_cast<const u32x4 *>(as + i * 16 * C::ROW);
+#pragma unroll
+  for (int j = 0; j < Mfma16<C>::NB; ++j)
+    b[j] = *reinterpret_cast<const u32x4 *>(bs + j * 16 * C::ROW);
+}
+
+template <class C>
+__device__ __forceinline__ void mfma_block16(const u32x4 (&a)[Mfma16<C>::NA],
+                                             const u32x4 (&b)[Mfma16<C>::NB],
+                                             floatx16 (&acc)[C::TM][C::TN]) {
+#pragma unroll
+  for (int i = 0; i < C::TM; ++i)
+#pragma unroll
+    for (int j = 0; j < C::TN; ++j)
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        floatx4 c = {acc[i][j][4 * s], acc[i][j][4 * s + 1], acc[i][j][4 * s + 2],
+                     acc[i][j][4 * s + 3]};
+        c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+            __builtin_bit_cast(bf16x8, a[2 * i + (s >> 1)]),
+            __builtin_bit_cast(bf16x8, b[2 * j + (s & 1)]), c, 0, 0, 0);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc[i][j][4 * s + e] = c[e];
+      }
+}
+
+// Between the two layouts of a tile, in place: registers (8 ti + r,
+// 8 ti + 4 + r) hold products (2 ti, 2 ti + 1) at element r in the 16 x 16
+// form and rows (16 ti + r, 16 ti + 8 + r) (plus 4 for lanes 32-63) in the
+// 32x32x16 layout; v_permlane16_swap of each pair goes either way.
+__device__ __forceinline__ void acc_swap16(floatx16 &acc) {
+#pragma unroll
+  for (int ti = 0; ti < 2; ++ti)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const auto v = __builtin_amdgcn_permlane16_swap(__float_as_uint(acc[8 * ti + r]),
+                                                      __float_as_uint(acc[8 * ti + 4 + r]),
+                                                      false, false);
+      acc[8 * ti + r] = __uint_as_float(v[0]);
+      acc[8 * ti + 4 + r] = __uint_as_float(v[1]);
+    }
+}
+
+// As interleave_hint for a 16x16x32 k-group: 4 TM TN MFMAs, 2 (TM + TN) reads.
+template <class C>
+__device__ __forceinline__ void interleave_hint16() {
+  constexpr int kMfma = 4 * C::TM * C::TN;
+  constexpr int kReads = Mfma16<C>::NA + Mfma16<C>::NB;
+  constexpr int kPer = kMfma / kReads > 0 ? kMfma / kReads : 1;
+  constexpr int kLead = kMfma - kReads * kPer;
+  if constexpr (kLead > 0) __builtin_amdgcn_sched_group_barrier(0x008, kLead, 0);
+#pragma unroll
+  for (int r = 0; r < kReads; ++r) {
+    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    __builtin_amdgcn_sched_group_barrier(0x008, kPer, 0);
+  }
+}
+
+// The K loop of mainloop_dtl_ops in 16x16x32 products (K-contiguous B, BK 64);
+// ZERO: acc holds zeros, which both layouts share.
+template <class C, bool BUF, bool ZERO>
+__device__ __forceinline__ void mainloop_dtl16(const DtlOperand<C, C::ACW> &opa,
+                                               const DtlOperand<C, C::BCW> &opb, int64_t K,
+                                               char *smem, floatx16 (&acc)[C::TM][C::TN]) {
+  using Q = Mfma16<C>;
+  static_assert(Q::KG == 2, "two 32-wide k-groups per stage");
+  const int w = threadIdx.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(w);
+  const int wm = w / C::WN, wn = w % C::WN;
+  const int64_t nk = (K + C::BK - 1) / C::BK;
+  if constexpr (!ZERO) {
+#pragma unroll
+    for (int i = 0; i < C::TM; ++i)
+#pragma unroll
+      for (int j = 0; j < C::TN; ++j) acc_swap16(acc[i][j]);
+  }
+  u32x4 a0[Q::NA], b0[Q::NB], a1[Q::NA], b1[Q::NB];
+  if constexpr (BUF) {
+    // the stage hand-over of mainloop_dtl_ops, with two k-groups per stage
+#pragma unroll
+    for (int s = 0; s < C::STAGES; ++s)
+      if (s < nk) {
+        char *st = smem + s * C::STAGE;
+        opa.issue((int64_t)s * C::BK, st, wave);
+        opb.issue((int64_t)s * C::BK, st + C::BM * C::ROW, wave);
+      }
+    if (nk > 0) {
+      wait_stage<C>(nk - 1 < C::STAGES - 1 ? (int)(nk - 1) : C::STAGES - 1);
+      read_kgroup16<C>(smem, wm, wn, 0, a0, b0);
+    }
+    int cur = 0;
+    for (int64_t kt = 0; kt < nk; ++kt) {
+      const char *st = smem + cur * C::STAGE;
+      read_kgroup16<C>(st, wm, wn, 1, a1, b1);
+      mfma_block16<C>(a0, b0, acc);
+      interleave_hint16<C>();
+      mfma_block16<C>(a1, b1, acc);
+      interleave_hint16<C>();
+      if (kt + 1 < nk) {
+        if constexpr (C::STAGES == 2) {
+          wait_vm_barrier<0>();
+        } else {
+          const int64_t later = nk - 2 - kt;
+          wait_stage<C>(later < C::STAGES - 2 ? (int)later : C::STAGES - 2);
+        }
+        if (kt + C::STAGES < nk) {
+          char *re = smem + cur * C::STAGE;
+          opa.issue((kt + C::STAGES) * C::BK, re, wave);
+          opb.issue((kt + C::STAGES) * C::BK, re + C::BM * C::ROW, wave);
+        }
+        cur = cur + 1 == C::STAGES ? 0 : cur + 1;
+        read_kgroup16<C>(smem + cur * C::STAGE, wm, wn, 0, a0, b0);
+      }
+    }
+  } else {
+    for (int64_t kt = 0; kt < nk; ++kt) {
+      opa.copy_sync(kt * C::BK, wave, smem);
+      opb.copy_sync(kt * C::BK, wave, smem + C::BM * C::ROW);
+      __syncthreads();
+      read_kgroup16<C>(smem, wm, wn, 0, a0, b0);
+      read_kgroup16<C>(smem, wm, wn, 1, a1, b1);
+      mfma_block16<C>(a0, b0, acc);
+      mfma_block16<C>(a1, b1, acc);
+      __syncthreads();
+    }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < C::TM; ++i)
+#pragma unroll
+    for (int j = 0; j < C::TN; ++j) acc_swap16(acc[i][j]);
+}
+
 // k-group operands for B operand type OpB
 template <class C, class OpB>
 __device__ __forceinline__ void read_kgroup_op(const char *stage, int wm, int wn, int kg,
@@ -516,7 +691,7 @@ __device__ __forceinline__ void read_kgroup_op(const char *stage, int wm, int wn
     read_kgroup_dtl<C>(stage, wm, wn, kg, a, b);
 }
 
-template <class C, bool BUF, class OpB>
+template <class C, bool BUF, bool ZERO = false, class OpB>
 __device__ __forceinline__ void mainloop_dtl_ops(const DtlOperand<C, C::ACW> &opa,
                                                  const OpB &opb, int64_t K,
                                                  char *smem, floatx16 (&acc)[C::TM][C::TN]);
@@ -539,7 +714,7 @@ __device__ __forceinline__ void mainloop_dtl(const bf16 *A, int64_t lda, const b
   DtlOperand<C, C::BCW> opb;
   opa.init(A, lda, M, K, m0, wave);
   opb.init(B, ldb, N, K, n0, wave);
-  mainloop_dtl_ops<C, BUF>(opa, opb, K, smem, acc);
+  mainloop_dtl_ops<C, BUF, ZERO>(opa, opb, K, smem, acc);
 }
 
 // As mainloop_dtl with B given N-major: B[k, n] at B[k * ldb + n], k-rows
@@ -564,16 +739,21 @@ __device__ __forceinline__ void mainloop_kn(const bf16 *A, int64_t lda, const bf
   DtlOperandKN<C> opb;
   opa.init(A, lda, M, K, m0, wave);
   opb.init(B, ldb, nb_cols, K, n0, wave);
-  mainloop_dtl_ops<C, BUF>(opa, opb, K, smem, acc);
+  mainloop_dtl_ops<C, BUF, ZERO>(opa, opb, K, smem, acc);
 }
 
 // The K loop over operands the caller has set up (a kernel may point each
 // wavefront's share of a tile at a different matrix).  acc is not cleared.
-// OpB: DtlOperand (B K-contiguous) or DtlOperandKN (B N-major).
-template <class C, bool BUF, class OpB>
+// OpB: DtlOperand (B K-contiguous) or DtlOperandKN (B N-major).  ZERO: acc
+// holds zeros on entry.
+template <class C, bool BUF, bool ZERO, class OpB>
 __device__ __forceinline__ void mainloop_dtl_ops(const DtlOperand<C, C::ACW> &opa,
                                                  const OpB &opb, int64_t K,
                                                  char *smem, floatx16 (&acc)[C::TM][C::TN]) {
+  if constexpr (!OpB::kKRows && C::BK == 64 && kMfma16) {
+    mainloop_dtl16<C, BUF, ZERO>(opa, opb, K, smem, acc);
+    return;
+  }
   // LDS read instructions per k-group: an N-major B takes two per MFMA tile
   constexpr int kReadsB = C::TM + (OpB::kKRows ? 2 : 1) * C::TN;
   const int w = threadIdx.x >> 6;

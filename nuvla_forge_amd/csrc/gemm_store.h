@@ -153,6 +153,23 @@ __device__ __forceinline__ uint16_t to_half_bits(float v, int dt) {
   return bits;
 }
 
+// Tilings the N-major B path (DtlOperandKN, read_kgroup_kn) and the
+// LDS-transposed C store are written for.
+template <class C>
+constexpr bool kn_tiling() {
+  if constexpr (!C::DTL)
+    return false;
+  else
+    return C::BN == 256 && C::BK == 64 && C::NW == 8 && C::WTN == 64 && C::TN == 2;
+}
+template <class C>
+constexpr bool ct_vec_tiling() {
+  if constexpr (!C::DTL)
+    return false;
+  else
+    return C::WTN == 64 && C::WN * C::WTN == C::BN && C::BM == 256;
+}
+
 // One block's tile of job j: the K loop (B K-contiguous, or N-major when BT)
 // and the store epilogue.  The kernel instantiates it once per B layout in
 // separate branches, so the two K loops never share a merge point (which
@@ -201,7 +218,7 @@ __device__ __forceinline__ void store_tile(const GemmJob<typename C::TI> &j, int
   else
     gemm::mainloop<C, BUF, false>(j.A + k0, j.lda, j.B + k0, j.ldb, M, N, klen, m0, n0, smem, acc);
   const float g = (!split && j.scale) ? *j.scale : 1.f;
-  if constexpr (C::DTL) {
+  if constexpr (ct_vec_tiling<C>()) {
   if (ct && j.ct_vec) {
     // Transposed store through LDS (free after the K loop), so that global
     // stores are whole 16-byte vectors along m: in pass p the wavefronts of
@@ -209,7 +226,6 @@ __device__ __forceinline__ void store_tile(const GemmJob<typename C::TI> &j, int
     // into LDS as 64 rows n of 256 m (row pitch 256 elements + 16 bytes, so
     // the 32 rows a write instruction touches start on different banks), then
     // every thread stores row vectors.  Needs M and ldc multiples of 8.
-    static_assert(C::WTN == 64 && C::WN * C::WTN == C::BN && C::BM == 256, "tiling");
     const int es = dtype_bytes(cdt);
     const int pitch = 256 * es + 16;
     const int l = threadIdx.x & 63, w = threadIdx.x >> 6;
@@ -332,7 +348,7 @@ __global__ NF_GEMM_BOUNDS(C) void gemm_store_kernel(GemmJob<typename C::TI> j0,
   gemm::group_tile(t % per_split, tiles_m, tiles_n, gemm::kTileGroup, tm, tn);
   const int64_t m0 = (int64_t)tm * C::BM;
   const int64_t n0 = (int64_t)tn * C::BN;
-  if constexpr (C::DTL) {
+  if constexpr (kn_tiling<C>()) {
     if (j.bt) {
       store_tile<C, BUF, SB, true>(j, M, K, ks, m0, n0, smem);
       return;
@@ -602,14 +618,15 @@ int launch_gemm_store(const GemmJob<typename C::TI> &j0_in, const GemmJob<typena
                       hipStream_t s, bool reduce = true) {
   GemmJob<typename C::TI> j0 = j0_in, j1 = j1_in;
   for (auto *jp : {&j0, &j1})  // the LDS-transposed store where it applies
-    jp->ct_vec = C::DTL && jp->ct && !jp->row_scale && jp->M % 8 == 0 && jp->ldc % 8 == 0;
+    jp->ct_vec = ct_vec_tiling<C>() && jp->ct && !jp->row_scale && jp->M % 8 == 0 &&
+                 jp->ldc % 8 == 0;
   const int64_t total = (int64_t)j0.tiles + j1.tiles;
   if (total == 0) return NF_OK;
   if (total > 0x7fffffffLL) return set_error(NF_ERR_ARG, "gemm: too many tiles");
   for (const auto *jp : {&j0, &j1}) {
     if (jp->tiles == 0) continue;
-    if (jp->bt && !C::DTL)
-      return set_error(NF_ERR_ARG, "gemm: an N-major B needs 16-bit operands");
+    if (jp->bt && !kn_tiling<C>())
+      return set_error(NF_ERR_ARG, "gemm: an N-major B needs the 16-bit 256-column tiling");
     if (jp->ct && jp->ksplit > 1)
       return set_error(NF_ERR_ARG, "gemm: a transposed C cannot be split along K");
   }

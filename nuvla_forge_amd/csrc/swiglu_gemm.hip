@@ -72,7 +72,7 @@ __global__ NF_GEMM_BOUNDS(C) void gate_up_swiglu_kernel(Args p) {
   const int64_t unit0 = u0 + 32 * (wave >> 1);
   opb.init((wave & 1) ? p.wu : p.wg, (wave & 1) ? p.ldu : p.ldg, p.H, p.D, unit0 - 32 * wave,
            wave);
-  gemm::mainloop_dtl_ops<C, BUF>(opa, opb, p.D, smem, acc);
+  gemm::mainloop_dtl_ops<C, BUF, true>(opa, opb, p.D, smem, acc);
 
   const int l = threadIdx.x & 63;
   const int w = threadIdx.x >> 6, wm = w / C::WN, wn = w % C::WN;
