@@ -334,16 +334,17 @@ def bench_ce_gemm_ceiling(args, dev):
 
 def bench_mfma_ceiling(args, dev, blocks=2048, iters=300):
     """`nf_mfma_probe` for context (never the roofline denominator): bf16
-    v_mfma_f32_32x32x16 products on operands held in registers, with no
-    memory access in the loop -- 2048 blocks of 256 threads (one block per CU
-    at a time: a block holds the register file of its CU's four SIMDs), each
-    300 rounds of 128 products per wavefront -- timed as 20 back-to-back
-    launches in a HIP graph, on random N(0,1) bf16 operands and on zeros.
-    The shader clock comes from the stamps of the graph's last launch (shader
+    MFMAs on operands held in registers, with no memory access in the loop --
+    2048 blocks of 256 threads (one block per CU at a time: a block holds the
+    register file of its CU's four SIMDs), each 300 rounds of 1 MFLOP per
+    wavefront -- timed as 20 back-to-back launches in a HIP graph, on random
+    N(0,1) bf16 operands and on zeros; v_mfma_f32_16x16x32 (the GEMM core's
+    form) at the top level, v_mfma_f32_32x32x16 under `form_32x32x16`.  The
+    shader clock comes from the stamps of the graph's last launch (shader
     cycles over the 100 MHz real-time counter, summed over blocks).  On
     random data the chip's power limit lowers the clock (a real product's
     operands toggle the multipliers; zeros do not), so the random-operand
-    rate is the most any bf16 product of this build's data can reach."""
+    rate is the most a bf16 product of this build's data can reach."""
     import torch
 
     from nuvla_forge_amd import _lib, _measure
@@ -353,19 +354,22 @@ def bench_mfma_ceiling(args, dev, blocks=2048, iters=300):
     ops = torch.randn(16, 256, 8, generator=g).to(torch.bfloat16).to(dev)
     out = torch.empty(blocks, 256, device=dev)
     stamps = torch.zeros(blocks, 4, dtype=torch.int64, device=dev)
-    flops = blocks * 4 * iters * 32 * (2 * 32 * 32 * 16)
-    res = {"blocks": blocks, "iters": iters, "flops_per_launch": flops}
-    for name, ptr in (("random", ops.data_ptr()), ("zero", None)):
-        def launch(ptr=ptr):
-            _lib.check(L.nf_mfma_probe(ptr, iters, blocks, out.data_ptr(), stamps.data_ptr(),
-                                       _lib.stream_of(out)), "nf_mfma_probe")
+    flops = blocks * 4 * iters * 64 * (2 * 16 * 16 * 32)  # = 32 * (2 * 32 * 32 * 16) per round
+    res = {"blocks": blocks, "iters": iters, "flops_per_launch": flops,
+           "form": "v_mfma_f32_16x16x32_bf16", "form_32x32x16": {}}
+    for form, dst in ((0, res), (1, res["form_32x32x16"])):
+        for name, ptr in (("random", ops.data_ptr()), ("zero", None)):
+            def launch(ptr=ptr, form=form):
+                _lib.check(L.nf_mfma_probe(ptr, iters, blocks, form, out.data_ptr(),
+                                           stamps.data_ptr(), _lib.stream_of(out)),
+                           "nf_mfma_probe")
 
-        ms = per_launch_ms(launch, max(5, args.steps // 5))
-        st = stamps.cpu().double()
-        ghz = float((st[:, 1] - st[:, 0]).sum() / ((st[:, 3] - st[:, 2]).sum() / 100e6) / 1e9)
-        tflops = flops / (ms * 1e-3) / 1e12
-        res[name] = {"us": ms * 1e3, "tflops": tflops,
-                     "frac_of_spec": tflops / MFMA_BF16_PEAK_TFLOPS, "clock_ghz": ghz}
+            ms = per_launch_ms(launch, max(5, args.steps // 5))
+            st = stamps.cpu().double()
+            ghz = float((st[:, 1] - st[:, 0]).sum() / ((st[:, 3] - st[:, 2]).sum() / 100e6) / 1e9)
+            tflops = flops / (ms * 1e-3) / 1e12
+            dst[name] = {"us": ms * 1e3, "tflops": tflops,
+                         "frac_of_spec": tflops / MFMA_BF16_PEAK_TFLOPS, "clock_ghz": ghz}
     return res
 
 

@@ -60,16 +60,18 @@ int nf_stream_probe(int reads, int writes, const void *in0, const void *in1,
 /* ------------------------------------------------------------------------
  * Measurement aid with no counterpart in the reference: the MFMA ceiling
  * bench.py sets the cross entropy's products against.  `blocks` blocks of
- * 256 threads each issue iters * 128 bf16 v_mfma_f32_32x32x16 products
- * (2 * 32 * 32 * 16 flops each) on operands held in registers, with no
- * memory access in the loop.  ops: 16 * 256 16-byte vectors (vector v of
- * thread t at index v * 256 + t; every block reads the same ones), or NULL
- * for zero operands.  out[b * 256 + t] = the sum of thread t's accumulators
- * in block b (blocks * 256 floats).  stamps (NULL or blocks * 4 values):
- * per block, the shader clock counter at start and end, then the 100 MHz
- * real-time counter at start and end.
+ * 256 threads each issue iters * 256 bf16 v_mfma_f32_16x16x32 products
+ * (form 0, the GEMM core's; 2 * 16 * 16 * 32 flops each) or iters * 128
+ * v_mfma_f32_32x32x16 products (form 1; 2 * 32 * 32 * 16 flops each) on
+ * operands held in registers, with no memory access in the loop.  ops:
+ * 16 * 256 16-byte vectors (vector v of thread t at index v * 256 + t; A
+ * operands from vectors 0-3 and 8-11, B from 4-7 and 12-15; every block
+ * reads the same ones), or NULL for zero operands.  out[b * 256 + t] = the
+ * sum of thread t's 256 accumulators in block b (blocks * 256 floats).
+ * stamps (NULL or blocks * 4 values): per block, the shader clock counter
+ * at start and end, then the 100 MHz real-time counter at start and end.
  * ---------------------------------------------------------------------- */
-int nf_mfma_probe(const void *ops, int64_t iters, int64_t blocks, float *out,
+int nf_mfma_probe(const void *ops, int64_t iters, int64_t blocks, int form, float *out,
                   uint64_t *stamps, void *stream);
 
 #ifdef __cplusplus

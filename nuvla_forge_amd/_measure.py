@@ -27,7 +27,7 @@ SIGNATURES = {
     "nf_gemm_nt": (_I32, [_P, _I64, _P, _I64, _P, _I64, _I64, _I64, _I64, _I32, _P]),
     "nf_gemm_nn": (_I32, [_P, _I64, _P, _I64, _P, _I64, _I64, _I64, _I64, _I32, _P]),
     "nf_stream_probe": (_I32, [_I32, _I32, _P, _P, _P, _P, _P, _P, _I64, _P]),
-    "nf_mfma_probe": (_I32, [_P, _I64, _I64, _P, _P, _P]),
+    "nf_mfma_probe": (_I32, [_P, _I64, _I64, _I32, _P, _P, _P]),
 }
 
 _lib_m: ctypes.CDLL | None = None

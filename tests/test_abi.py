@@ -358,12 +358,13 @@ def test_mfma_probe_argument_validation():
     """The MFMA-ceiling entry point refuses bad sizes and pointers before any
     launch (no GPU needed)."""
     L = _measure.lib()
-    assert L.nf_mfma_probe(FAKE, -1, 1, FAKE, None, None) == NF_ERR_ARG and "iters" in _err()
-    assert L.nf_mfma_probe(FAKE, 2**30 + 1, 1, FAKE, None, None) == NF_ERR_ARG
-    assert L.nf_mfma_probe(FAKE, 1, 0, FAKE, None, None) == NF_ERR_ARG and "blocks" in _err()
-    assert L.nf_mfma_probe(FAKE, 1, 2**20 + 1, FAKE, None, None) == NF_ERR_ARG
-    assert L.nf_mfma_probe(FAKE, 1, 1, None, None, None) == NF_ERR_ARG and "out" in _err()
-    assert L.nf_mfma_probe(FAKE + 8, 1, 1, FAKE, None, None) == NF_ERR_ARG
+    assert L.nf_mfma_probe(FAKE, -1, 1, 0, FAKE, None, None) == NF_ERR_ARG and "iters" in _err()
+    assert L.nf_mfma_probe(FAKE, 2**30 + 1, 1, 0, FAKE, None, None) == NF_ERR_ARG
+    assert L.nf_mfma_probe(FAKE, 1, 0, 0, FAKE, None, None) == NF_ERR_ARG and "blocks" in _err()
+    assert L.nf_mfma_probe(FAKE, 1, 2**20 + 1, 0, FAKE, None, None) == NF_ERR_ARG
+    assert L.nf_mfma_probe(FAKE, 1, 1, 2, FAKE, None, None) == NF_ERR_ARG and "form" in _err()
+    assert L.nf_mfma_probe(FAKE, 1, 1, 0, None, None, None) == NF_ERR_ARG and "out" in _err()
+    assert L.nf_mfma_probe(FAKE + 8, 1, 1, 0, FAKE, None, None) == NF_ERR_ARG
     assert "aligned" in _err()
 
 

@@ -1,8 +1,9 @@
 """nf_mfma_probe, the MFMA ceiling bench.py sets the cross entropy's products
 against (GPU): with every A operand a and every B operand b (bf16), each of a
-thread's 256 accumulators receives 2 * iters products of 16-term dot products,
-so its sum is 256 * 32 * iters * a * b, exact in fp32 at these sizes; zero
-operands (a null `ops`) give 0; the stamps count forward."""
+thread's 256 accumulators receives iters products of 32-term dot products
+(form 0, 16x16x32) or 2 * iters of 16-term ones (form 1, 32x32x16), so its
+sum is 256 * 32 * iters * a * b either way, exact in fp32 at these sizes;
+zero operands (a null `ops`) give 0; the stamps count forward."""
 
 from __future__ import annotations
 
@@ -15,10 +16,11 @@ from tests.helpers import note
 pytestmark = pytest.mark.gpu
 
 
+@pytest.mark.parametrize("form", [0, 1])
 @pytest.mark.parametrize("a,b,iters,blocks", [(1.0, 1.0, 10, 3), (0.5, 0.25, 7, 300),
                                               (0.0, 3.0, 5, 1), (None, None, 4, 2)])
-def test_mfma_probe_values(cuda, a, b, iters, blocks):
-    note(f"mfma probe a={a} b={b} iters={iters} blocks={blocks}")
+def test_mfma_probe_values(cuda, a, b, iters, blocks, form):
+    note(f"mfma probe form={form} a={a} b={b} iters={iters} blocks={blocks}")
     L = _measure.lib()
     ops = None
     if a is not None:
@@ -29,7 +31,7 @@ def test_mfma_probe_values(cuda, a, b, iters, blocks):
         ops[12:16].fill_(b)
     out = torch.full((blocks, 256), -1.0, device=cuda)
     stamps = torch.zeros(blocks, 4, dtype=torch.int64, device=cuda)
-    _lib.check(L.nf_mfma_probe(None if ops is None else ops.data_ptr(), iters, blocks,
+    _lib.check(L.nf_mfma_probe(None if ops is None else ops.data_ptr(), iters, blocks, form,
                                out.data_ptr(), stamps.data_ptr(), _lib.stream_of(out)),
                "nf_mfma_probe")
     torch.cuda.synchronize()
