@@ -309,7 +309,9 @@ def bench_ce_gemm_ceiling(args, dev):
     [32000, 2048]) and dW = P^T H_valid ([32000, 3687] x [3687, 2048]) --
     6 M_valid V D flops in all, each timed as 20 back-to-back launches in a
     HIP graph, with fp32 outputs as this build's fp32 accumulators where the
-    product is accumulated, bf16 where it is final."""
+    product is accumulated, bf16 where it is final; beside them 8192^3 on
+    the library and this build's GEMM core (nf_gemm_nt, fp32 C) on the
+    logits product and on 8192^3."""
     import torch
 
     g = torch.Generator().manual_seed(50)
@@ -329,6 +331,31 @@ def bench_ce_gemm_ceiling(args, dev):
         out[name] = {"us": ms * 1e3, "tflops": flops / (ms * 1e-3) / 1e12}
     out["sum_us"] = total * 1e3
     out["tflops_6MvVD"] = 6 * mv * v * d / (total * 1e-3) / 1e12
+    # this build's GEMM core on the logits product and on 8192^3, beside the
+    # library (the core stores fp32 C: twice the library's bf16 output bytes)
+    from nuvla_forge_amd import _lib, _measure
+
+    L = _measure.lib()
+    sq = torch.randn(8192, 8192, generator=g).to(torch.bfloat16).to(dev)
+    sq2 = torch.randn(8192, 8192, generator=g).to(torch.bfloat16).to(dev)
+    core = {}
+    for name, (a_, b_, flops) in {"logits_S": (h, w, 2 * mv * v * d),
+                                  "square_8192": (sq, sq2, 2 * 8192 ** 3)}.items():
+        m_, k_ = a_.shape
+        n_ = b_.shape[0]
+        c32 = torch.empty(m_, n_, device=dev)
+
+        def launch(a_=a_, b_=b_, c32=c32, m_=m_, n_=n_, k_=k_):
+            _lib.check(L.nf_gemm_nt(a_.data_ptr(), k_, b_.data_ptr(), k_, c32.data_ptr(), n_,
+                                    m_, n_, k_, _lib.dtype_code(torch.bfloat16),
+                                    _lib.stream_of(c32)), "nf_gemm_nt")
+
+        ms = per_launch_ms(launch, max(5, args.steps // 5))
+        core[name] = {"us": ms * 1e3, "tflops": flops / (ms * 1e-3) / 1e12}
+        del c32
+    ms = per_launch_ms(lambda: torch.mm(sq, sq2.t()), max(5, args.steps // 5))
+    out["square_8192"] = {"us": ms * 1e3, "tflops": 2 * 8192 ** 3 / (ms * 1e-3) / 1e12}
+    out["this_build_fp32_out"] = core
     return out
 
 
