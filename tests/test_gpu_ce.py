@@ -405,6 +405,35 @@ def test_ce_cfg4_bf16_full_size_and_deterministic(cuda, chunk):
     assert np.all(dh.float().cpu().numpy()[(tgt == -100).cpu().numpy()] == 0)
 
 
+def test_ce_probabilities_over_2gib(cuda):
+    """One chunk whose probabilities exceed 2 GiB (bf16 E [8448, 128256],
+    2.17 GB, held once at D = 64): the logits launch stores E through 64-bit
+    offsets and the gradient products read it through registers.  Checked
+    against torch's fp32 cross entropy on the device (the fp64 oracle would
+    take minutes at this size) at the bf16 tolerance."""
+    note("ce E over 2 GiB m=8448 d=64 v=128256 chunk=100000")
+    m, d, v = 8448, 64, 128256
+    hid, w, tgt = _ce_inputs(m, d, v, torch.bfloat16, cuda, seed=13, w_std=0.1,
+                             ignore=slice(None, None, 5))
+    L = _lib.lib()
+    assert L.nf_ce_state_bytes(m, d, v, 100000, _lib.dtype_code(torch.bfloat16)) > 2 * m * v
+    assert 2 * m * v > 2 ** 31
+    loss, dh, dw = _run_ce(hid, w, tgt, 100000)
+    h32 = hid.float().requires_grad_(True)
+    w32 = w.float().requires_grad_(True)
+    ref = torch.nn.functional.cross_entropy(h32 @ w32.t(), tgt, ignore_index=-100)
+    ref.backward()
+    torch.cuda.synchronize()
+
+    def rel(a, b):
+        return float((a.float() - b).norm() / b.norm())
+
+    lo = float(ref.detach())
+    assert abs(float(loss) - lo) / lo < 2e-2
+    assert rel(dh, h32.grad) < 2e-2 and rel(dw, w32.grad) < 2e-2
+    assert not dh[::5].any()
+
+
 def test_ce_state_is_released_after_backward(cuda):
     """The state nf_ce_fwd leaves for nf_ce_bwd (E, W^T, the scaled Hc^T, the
     fp32 dH rows and, with several chunks, the fp32 dW accumulator) is saved through
