@@ -1,8 +1,10 @@
 // MFMA GEMM mainloop for gfx950: acc[M_tile x N_tile] = A[M x K] . B[N x K]^T
-// with both operands K-contiguous ("NT"), fp32 accumulation.
+// with both operands K-contiguous ("NT"), or B N-major, fp32 accumulation.
 //
-//  * bf16 inputs use v_mfma_f32_32x32x16_bf16: lane l supplies 8 consecutive
-//    k of row (l % 32), k-half (l / 32).
+//  * bf16 inputs use v_mfma_f32_32x32x16_bf16 (lane l supplies 8 consecutive
+//    k of row (l % 32), k-half (l / 32)) or, on the direct-to-LDS path with B
+//    K-contiguous, four v_mfma_f32_16x16x32_bf16 per 32x32 tile brought to
+//    the same accumulator layout (mainloop_dtl16).
 //  * f32 inputs use v_mfma_f32_32x32x2_f32: lane l supplies one k of row
 //    (l % 32); four MFMAs consume a 16-byte k-slab per lane half, the half
 //    h = l / 32 covering k = 4h .. 4h+3 of each 8-wide group (the sum over k
