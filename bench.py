@@ -601,6 +601,52 @@ def ce_inputs(dev, m=4096, d=2048, v=32000, n_ignore=409):
     return hid, w, tgt.to(dev)
 
 
+def ce_call_times(hid, w, tgt, chunk, steps):
+    """nf_ce_fwd and nf_ce_bwd apart, through the C ABI: a HIP graph of 5
+    (forward, backward) pairs and one of 5 forwards, each replayed `steps`
+    times; the forward's time is the second's, the backward's the
+    difference, so the two add up to the pair.  The forward holds the logits
+    GEMM with its statistics and E store (and the small compaction, gather,
+    lse and scaling kernels), the backward the gradient GEMM launch (dW and
+    dH) and the dH scatter."""
+    import torch
+
+    from nuvla_forge_amd import _lib
+
+    L = _lib.lib()
+    m, d = hid.shape
+    v = w.shape[0]
+    code = _lib.dtype_code(torch.bfloat16)
+    shape = (m, d, v, chunk, code)
+    sb, fw, bw = L.nf_ce_state_bytes(*shape), L.nf_ce_fwd_workspace(*shape), L.nf_ce_bwd_workspace(*shape)
+    state = torch.empty(sb, dtype=torch.uint8, device=hid.device)
+    wsf = torch.empty(fw, dtype=torch.uint8, device=hid.device)
+    wsb = torch.empty(bw, dtype=torch.uint8, device=hid.device)
+    loss = torch.empty((), device=hid.device)
+    g = torch.ones((), device=hid.device)
+    dh, dw = torch.empty_like(hid), torch.empty_like(w)
+
+    def fwd():
+        _lib.check(L.nf_ce_fwd(hid.data_ptr(), w.data_ptr(), tgt.data_ptr(), m, d, v, -100, chunk,
+                               code, loss.data_ptr(), None, state.data_ptr(), sb, wsf.data_ptr(),
+                               fw, _lib.stream_of(hid)), "nf_ce_fwd")
+
+    def bwd():
+        _lib.check(L.nf_ce_bwd(m, d, v, chunk, code, state.data_ptr(), sb, g.data_ptr(),
+                               dh.data_ptr(), code, dw.data_ptr(), code, wsb.data_ptr(), bw,
+                               _lib.stream_of(hid)), "nf_ce_bwd")
+
+    def pair():
+        fwd()
+        bwd()
+
+    fwd()
+    torch.cuda.synchronize()
+    both = per_launch_ms(pair, steps, reps=5)
+    f = per_launch_ms(fwd, steps, reps=5)
+    return f, both - f
+
+
 def bench_ce(args, dev):
     import torch
 
@@ -643,7 +689,15 @@ def bench_ce(args, dev):
     # 4096: one chunk in both layouts (E and E^T, 2 x 262 MB, inside the
     # reference's 786 MB at that setting).
     main = run(1024)
+    # the two calls apart: logits (2 M_valid V D credited) and gradients (4 M_valid V D)
+    fms, bms = ce_call_times(hid, w, tgt, 1024, max(5, args.steps // 5))
+    calls = {"nf_ce_fwd_ms": fms, "nf_ce_bwd_ms": bms,
+             "fwd_tflops": flops / 3 / (fms * 1e-3) / 1e12,
+             "bwd_tflops": 2 * flops / 3 / (bms * 1e-3) / 1e12}
+    calls["fwd_mfma_frac"] = calls["fwd_tflops"] / MFMA_BF16_PEAK_TFLOPS
+    calls["bwd_mfma_frac"] = calls["bwd_tflops"] / MFMA_BF16_PEAK_TFLOPS
     return {"m": m, "d": d, "v": v, "m_valid": m_valid, "alg_flops": flops, **main,
+            "calls_chunk_1024": calls,
             "holds": "E of every valid row, once",
             "chunk_4096": {**run(4096), "holds": "E and E^T of every valid row"}}
 
