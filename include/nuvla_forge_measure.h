@@ -30,6 +30,14 @@ int nf_gemm_nt(const void *A, int64_t lda, const void *B, int64_t ldb,
                int dtype, void *stream);
 
 /* ------------------------------------------------------------------------
+ * Test hook with no counterpart in the reference: C += A[M, K] @ B[N, K]^T
+ * for bf16 A, B and fp32 C (ldc >= N), the accumulator preloaded from C
+ * before the K loop: the path of a product accumulated onto an earlier one.
+ * ---------------------------------------------------------------------- */
+int nf_gemm_nt_acc(const void *A, int64_t lda, const void *B, int64_t ldb, float *C,
+                   int64_t ldc, int64_t M, int64_t N, int64_t K, void *stream);
+
+/* ------------------------------------------------------------------------
  * Test hook with no counterpart in the reference: C = A[M, K] @ B[K, N]
  * (bf16 A and B, fp32 C) through the MFMA core's N-major-B path: A
  * row-major with unit-stride K, B row-major with unit-stride N (ldb >= N;

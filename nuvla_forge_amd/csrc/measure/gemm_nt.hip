@@ -41,6 +41,26 @@ extern "C" int nf_gemm_nt(const void *A, int64_t lda, const void *B, int64_t ldb
   return set_error(NF_ERR_DTYPE, "nf_gemm_nt: dtype %d unsupported", dtype);
 }
 
+extern "C" int nf_gemm_nt_acc(const void *A, int64_t lda, const void *B, int64_t ldb, float *C,
+                              int64_t ldc, int64_t M, int64_t N, int64_t K, void *stream) {
+  if (M < 0 || N < 0 || K < 0) return set_error(NF_ERR_ARG, "nf_gemm_nt_acc: negative size");
+  if (M > 0x7fffffffLL || N > 0x7fffffffLL || K > 0x7fffffffLL)
+    return set_error(NF_ERR_ARG, "nf_gemm_nt_acc: a size exceeds int32");
+  if (M == 0 || N == 0) return NF_OK;
+  if (!A || !B || !C) return set_error(NF_ERR_ARG, "nf_gemm_nt_acc: null pointer");
+  if (lda < K || ldb < K || ldc < N)
+    return set_error(NF_ERR_ARG, "nf_gemm_nt_acc: bad leading dim");
+  if (((M + 255) / 256) * ((N + 255) / 256) > 0x7fffffffLL)
+    return set_error(NF_ERR_ARG, "nf_gemm_nt_acc: grid too large");
+  using C16 = MainCfg<bf16>;
+  // C as its own preload: every element is read and written by one thread
+  auto j = make_job<C16>((const bf16 *)A, lda, (const bf16 *)B, ldb, C, C, NF_DTYPE_F32, nullptr,
+                         ldc, M, N, K);
+  j.ldcin = ldc;
+  const GemmJob<bf16> none{};
+  return launch_gemm_store<C16>(j, none, static_cast<hipStream_t>(stream));
+}
+
 extern "C" int nf_gemm_nn(const void *A, int64_t lda, const void *B, int64_t ldb, float *C,
                           int64_t ldc, int64_t M, int64_t N, int64_t K, int c_transposed,
                           void *stream) {

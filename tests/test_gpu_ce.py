@@ -41,6 +41,28 @@ def test_gemm_nt_matches_numpy(cuda, dtype, m, n, k):
     assert on.rel_err(np64(c), want) < 1e-5
 
 
+@pytest.mark.parametrize("m,n,k", [(256, 256, 128), (300, 520, 200), (1024, 768, 2048),
+                                   (33, 17, 64), (512, 256, 72)])
+def test_gemm_nt_accumulates_onto_c(cuda, m, n, k):
+    """nf_gemm_nt_acc: C += A B^T with the accumulator preloaded from C (row
+    stride n + 3), so a non-zero accumulator goes through the 16x16x32
+    mainloop's layout change on the way in and back on the way out; the
+    columns past n stay untouched."""
+    note(f"gemm_nt_acc m={m} n={n} k={k}")
+    g = gen(7)
+    a = randn((m, k), g, torch.bfloat16, cuda)
+    b = randn((n, k), g, torch.bfloat16, cuda)
+    c0 = randn((m, n + 3), g, torch.float32, cuda)
+    c = c0.clone()
+    L = _measure.lib()
+    _lib.check(L.nf_gemm_nt_acc(a.data_ptr(), k, b.data_ptr(), k, c.data_ptr(), n + 3, m, n, k,
+                                _lib.stream_of(a)), "nf_gemm_nt_acc")
+    torch.cuda.synchronize()
+    want = np64(c0[:, :n]) + np64(a) @ np64(b).T
+    assert on.rel_err(np64(c[:, :n]), want) < 1e-5
+    assert torch.equal(c[:, n:], c0[:, n:])
+
+
 def test_gemm_nt_leading_dimensions(cuda):
     note("gemm_nt strided operands")
     g = gen(1)
