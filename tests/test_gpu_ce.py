@@ -266,6 +266,20 @@ def test_ce_ragged_shapes(cuda, dtype, m, d, v, chunk):
     _check_ce(hid, w, tgt, loss, dh, dw, TOL[dtype], f"ragged {m},{d},{v}")
 
 
+def test_ce_wide_rows_in_many_chunks(cuda):
+    """bf16 at D = 2048 with chunk_size 256 over 8192 rows: the budget
+    2 (256 + 2048) rows of E is under M, so the rows go in 16 chunks of 512
+    held once, the fp32 dW^T accumulator carried through 15 of them (every
+    other chunk-size test with several chunks has D <= 256); against the
+    fp64 oracle."""
+    note("ce wide rows many chunks bf16 m=8192 d=2048 v=1000 chunk=256")
+    m, d, v = 8192, 2048, 1000
+    hid, w, tgt = _ce_inputs(m, d, v, torch.bfloat16, cuda, seed=17, w_std=0.02,
+                             ignore=slice(None, None, 9))
+    loss, dh, dw = _run_ce(hid, w, tgt, 256)
+    _check_ce(hid, w, tgt, loss, dh, dw, TOL[torch.bfloat16], "wide rows, 16 chunks")
+
+
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("chunk_rows", [256, 100000])
 def test_ce_one_call_entry_point(cuda, dtype, chunk_rows):
