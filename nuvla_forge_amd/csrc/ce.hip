@@ -770,9 +770,10 @@ inline Plan make_plan(int64_t M, int64_t D, int64_t V, int64_t chunk_rows) {
     //    against 3.05; M4096 D2048 level);
     //  * one chunk, E held once (mcap rows), no accumulator pass (at D 384 -
     //    1024 also faster than both layouts: M4096 D384 0.52 ms against
-    //    0.55, M1024 D1024 0.30-0.31 against 0.32; at cfg4, M4096 D2048 with
-    //    3687 valid rows, the accumulator alone is the bytes of E for every
-    //    row, and chunk_size 1024 runs in 1.48 ms against 1.64 in two chunks);
+    //    0.55, M2048 D384 0.28 against 0.30-0.32, M1024 D1024 0.31 against
+    //    0.33; at cfg4, M4096 D2048 with 3687 valid rows, the accumulator
+    //    alone is the bytes of E for every row, and chunk_size 1024 runs in
+    //    1.41-1.46 ms against 1.64 in two chunks);
     //  * chunks of 2 chunk_rows rows held once, beside the fp32 accumulator.
     const int64_t budget = 2 * ((chunk_rows < M ? chunk_rows : M) + D);
     P.single = D < 2048 || 2 * mcap > budget;
