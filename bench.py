@@ -61,7 +61,8 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--no-extra", action="store_true", help="headline workload only")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baselines")
     ap.add_argument("--only", choices=("swiglu", "ce", "stress", "traffic", "dit", "head",
-                                       "gateup", "copy", "adaln", "ce_gemm_ceiling", "mfma"),
+                                       "gateup", "copy", "adaln", "adaln_cold", "ce_gemm_ceiling",
+                                       "mfma"),
                     default=None,
                     help="run one secondary workload alone (for profiling) and print its "
                          "record instead of the headline line")
@@ -529,6 +530,50 @@ def cold_graph_ms(make_step, dev, per_graph=5, replays=6, flush_bytes=1 << 30):
     return with_ms - flush_ms, flush_ms
 
 
+def bench_adaln_cold(args, dev):
+    """The adaLN cfg2 kernels one by one with their operands in HBM (the
+    per-kernel view of `config.cold_ms_per_step`): cold_graph_ms of each C
+    call, of the backward with its reduction, of the three, and of the
+    streaming probe moving the forward's and the backward's arrays (2 reads +
+    2 writes, 4 + 2, no dependency between accesses); beside each, the warm
+    time of 10 back-to-back launches in one graph.  Microseconds."""
+    import torch
+
+    from nuvla_forge_amd import _lib, _measure
+
+    b, t, n = 8, 1024, 1024
+    inp, dh, dout = adaln_inputs(b, t, n, dev)
+    fwd, bwd, red = adaln_launchers(inp, t, dh, dout)
+    M = _measure.lib()
+    x, y = inp["x"], inp["y"]
+    h, o, dx, dy = (torch.empty_like(x) for _ in range(4))
+    n16 = x.numel() * x.element_size() // 16
+
+    def probe(reads, writes, ins, outs):
+        ptrs = [a.data_ptr() for a in ins] + [None] * (4 - len(ins))
+        optr = [a.data_ptr() for a in outs] + [None] * (2 - len(outs))
+        _lib.check(M.nf_stream_probe(reads, writes, *ptrs, *optr, n16, _lib.stream_of(x)),
+                   "nf_stream_probe")
+
+    cases = {"nf_adaln_fwd": [fwd], "nf_adaln_bwd": [bwd], "nf_adaln_bwd_reduce": [red],
+             "bwd_and_reduce": [bwd, red], "step_kernels": [fwd, bwd, red],
+             "probe_2r2w_fwd_arrays": [lambda: probe(2, 2, [x, y], [h, o])],
+             "probe_4r2w_bwd_arrays": [lambda: probe(4, 2, [x, y, dh, dout], [dx, dy])]}
+    out = {}
+    for name, fns in cases.items():
+        def make(fns=fns):
+            def run():
+                for f in fns:
+                    f()
+            return run
+
+        cold_ms, flush_ms = cold_graph_ms(make, dev)
+        warm = per_launch_ms(make(), max(5, args.steps // 5), 10)
+        out[name] = {"cold_us": cold_ms * 1e3, "warm_us": warm * 1e3}
+    out["read_pass_1gib_us"] = flush_ms * 1e3
+    return out
+
+
 def single_replay_floor_ms(dev, reps):
     """What cold_replay_ms reads for a one-kernel graph that moves nothing (a
     64-element fill): the method's own cost of events around one replay."""
@@ -922,7 +967,8 @@ def main() -> int:
         fn = {"swiglu": bench_swiglu, "ce": bench_ce, "stress": bench_stress,
               "traffic": bench_traffic, "dit": bench_dit_seam,
               "head": bench_ce_reasoning_head, "gateup": bench_gate_up, "copy": bench_copy,
-              "adaln": bench_adaln, "ce_gemm_ceiling": bench_ce_gemm_ceiling,
+              "adaln": bench_adaln, "adaln_cold": bench_adaln_cold,
+              "ce_gemm_ceiling": bench_ce_gemm_ceiling,
               "mfma": bench_mfma_ceiling}[args.only]
         print(json.dumps({"workload": args.only, **fn(args, dev)}), flush=True)
         return 0
