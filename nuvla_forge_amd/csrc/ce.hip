@@ -25,7 +25,7 @@
 //                 row's loss lse - S[target], the row factor cfac =
 //                 exp(mref - lse) / n, and the one-hot term folded into E's
 //                 target entry, so cfac * E = (softmax - onehot) / n; rows
-//                 whose maximum lies far above mref are recomputed exactly;
+//                 whose maximum lies far above mref are rescaled to it;
 //      ce_scale_hct: Hct = (cfac * Hc_c)^T, the dW product's B operand; in
 //                 the last chunk's launch, also the mean loss;
 //      gradient products of every chunk but the last (one launch):
@@ -142,8 +142,9 @@ __global__ __launch_bounds__(kCompactThreads) void ce_compact_kernel(
 // fixed-order sum; 0 past n_valid).  One wavefront per row.  E is stored
 // relative to mref (exp(S - mref)), so mref needs only to lie within the
 // exponent range of the row's largest logit; the target logit does for every
-// row whose loss is below ~50 nats, and the statistics pass sends any other
-// row through an exact recomputation (ce_lse_kernel).  VEC: 16-byte vectors
+// row whose loss is below ~50 nats, and for any other row the logits pass
+// keeps E in range and the statistics pass rescales it (ce_lse_kernel).
+// VEC: 16-byte vectors
 // (D a multiple of the vector width, aligned rows).
 // ---------------------------------------------------------------------------
 constexpr int kGatherThreads = 256;
@@ -209,6 +210,10 @@ __global__ __launch_bounds__(kGatherThreads) void ce_gather_kernel(
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ int e_swz(int t) { return 8 * (((t >> 3) ^ (t & 7)) & 31); }
 constexpr float kStatsGap = 64.f;  // exp(-64) of a row maximum is below fp32 resolution
+// E entries relative to mref stay below exp(kBaseGap): a wavefront whose
+// maximum for a token lies further above mref stores that token's E relative
+// to its own maximum instead (see the epilogue)
+constexpr float kBaseGap = 60.f;
 
 // Blocks past the vtiles x ttiles logits tiles run the transpose regions of
 // `tp` (16-bit inputs only): dispatched last, they fill the CUs that the
@@ -298,21 +303,26 @@ __global__ NF_GEMM_BOUNDS(C) void ce_logits_kernel(
     // follow from its sum: s = sum exp(S - mx) = exp(mref - mx) * sum E.  A
     // tile more than kStatsGap below mref keeps s = 1: its share of the row
     // total, below exp(-kStatsGap) of the row maximum's, is under fp32
-    // resolution.  A row whose maximum lies far above mref (its E leaves
-    // the exponent range, its sums overflow) is recomputed exactly by the
-    // statistics pass (kFactorGap); a wavefront with no row inside the
-    // vocabulary keeps (-inf, 0).
+    // resolution.  Where the maximum lies more than kBaseGap above mref (a
+    // row far from its reference), E = exp(S - mx) instead, so no entry
+    // leaves the exponent range, and s = sum E is stored negated: the
+    // statistics pass then rescales the row to its maximum.  A wavefront
+    // with no row inside the vocabulary keeps (-inf, 0).
+    const bool own = mx - mr > kBaseGap;
+    const float base = own ? mx : mr;
 #pragma unroll
     for (int i = 0; i < C::TM; ++i)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) acc[i][j][r] = exp_f32(acc[i][j][r] - mr);
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = exp_f32(acc[i][j][r] - base);
     float se = 0.f;
 #pragma unroll
     for (int i = 0; i < C::TM; ++i)
 #pragma unroll
       for (int r = 0; r < 16; ++r) se += acc[i][j][r];
     se += __shfl_xor(se, 32);
-    const float s = mx == -INFINITY ? 0.f : (mr - mx > kStatsGap ? 1.f : se * exp_f32(mr - mx));
+    const float s = mx == -INFINITY ? 0.f
+                    : own           ? -se
+                    : (mr - mx > kStatsGap ? 1.f : se * exp_f32(mr - mx));
     if (half == 0 && tok < cnt) stats[(int64_t)stile * crows + tok] = make_float2(mx, s);
 
 #pragma unroll
@@ -418,29 +428,36 @@ __global__ NF_GEMM_BOUNDS(C) void ce_logits_kernel(
 // then stays above exp(-kFactorGap), far inside the normal range of bf16 and
 // fp32, and every E entry below exp(kFactorGap), far from overflow in the
 // products' sums (lse is at least the row's largest logit).  Any other row
-// (a loss above kFactorGap - ln n nats, ~52 at n = 4096; also a row whose
-// tile sums overflowed, or a NaN / inf row) is recomputed exactly by its
-// block: fp32 dot products in a fixed order, the row's max and sum of
-// exponentials (so its lse and loss) from them, E relative to the row max
-// (cfac is then at least 1 / (n V)), written to both layouts.
+// (a loss above kFactorGap - ln n nats, ~52 at n = 4096, which includes every
+// row with a tile stored relative to its own maximum; also a NaN / inf row)
+// is rescaled by its block to the row's maximum M: each entry of statistics
+// tile t is multiplied by exp(base_t - M), base_t being the reference that
+// tile's E was formed with (mref, or the tile's maximum where its sum is
+// negated), and the target entry becomes exp(z - M) - exp(lse - M); both
+// layouts are rewritten, and mref becomes M (cfac is then at least
+// 1 / (n V)).  No E entry left the exponent range in the logits pass, so
+// nothing is lost but one rounding of the rescaled entries.
 constexpr float kFactorGap = 60.f;
+static_assert(kBaseGap <= kFactorGap, "a row with a tile of its own base must take the rescale");
 constexpr int kLseRows = 16, kLseParts = 16, kLseThreads = kLseRows * kLseParts;
 
 template <typename TI>
 __global__ __launch_bounds__(kLseThreads) void ce_lse_kernel(
-    const float2 *__restrict__ stats, int ntiles, int64_t crows, const float *tgt,
+    const float2 *__restrict__ stats, int ntiles, int wtm, int64_t crows, const float *tgt,
     const int *n_ptr, int64_t j0, const float *inv_ptr, const int *__restrict__ tcol,
     float *__restrict__ mref, float *__restrict__ cfac, float *loss_row, TI *P, int64_t ldp,
-    TI *PT, int64_t ldet, const TI *__restrict__ W, const TI *__restrict__ Hc, int64_t D,
-    int64_t V) {
+    TI *PT, int64_t ldet, int64_t V) {
   __shared__ float2 part[kLseParts][kLseRows];
+  __shared__ int own[kLseParts][kLseRows];
   __shared__ int redo[kLseRows];
-  __shared__ float2 red[kLseThreads / 64];
+  __shared__ float2 rowst[kLseRows];
+  __shared__ float mold[kLseRows];  // mref as the logits pass used it
   const int64_t cnt = chunk_count(n_ptr, j0, crows);
   const int rl = threadIdx.x % kLseRows, q = threadIdx.x / kLseRows;
   const int64_t row = (int64_t)blockIdx.x * kLseRows + rl;
   if ((int64_t)blockIdx.x * kLseRows >= cnt) return;  // the whole block is past the chunk
   float2 a = make_float2(-INFINITY, 0.f);
+  int flag = 0;
   if (row < cnt) {
     constexpr int kBatch = 16;
     for (int t0 = q; t0 < ntiles; t0 += kLseParts * kBatch) {
@@ -451,22 +468,29 @@ __global__ __launch_bounds__(kLseThreads) void ce_lse_kernel(
         v[u] = t < ntiles ? stats[(int64_t)t * crows + row] : make_float2(-INFINITY, 0.f);
       }
 #pragma unroll
-      for (int u = 0; u < kBatch; ++u) a = combine_stats(a, v[u]);
+      for (int u = 0; u < kBatch; ++u) {
+        flag |= v[u].y < 0.f;
+        a = combine_stats(a, make_float2(v[u].x, fabsf(v[u].y)));
+      }
     }
   }
   part[q][rl] = a;
+  own[q][rl] = flag;
   __syncthreads();
   const float inv = *inv_ptr;
   if (q == 0) {
     int again = 0;
     if (row < cnt) {
 #pragma unroll
-      for (int k = 1; k < kLseParts; ++k) a = combine_stats(a, part[k][rl]);
+      for (int k = 1; k < kLseParts; ++k) {
+        a = combine_stats(a, part[k][rl]);
+        flag |= own[k][rl];
+      }
       const float ls = a.x + log_f32(a.y);
       const float z = tgt[row];
-      loss_row[j0 + row] = ls - z;  // rewritten below for a recomputed row
+      loss_row[j0 + row] = ls - z;
       const float m = mref[j0 + row];
-      again = !(ls - m - log_f32(inv) <= kFactorGap);  // also for a NaN / inf row
+      again = flag || !(ls - m - log_f32(inv) <= kFactorGap);  // also for a NaN / inf row
       if (!again) {
         cfac[j0 + row] = inv * exp_f32(m - ls);
         const int64_t tc = tcol[j0 + row];
@@ -476,55 +500,47 @@ __global__ __launch_bounds__(kLseThreads) void ce_lse_kernel(
       }
     }
     redo[rl] = again;
+    rowst[rl] = a;
+    mold[rl] = row < cnt ? mref[j0 + row] : 0.f;
   }
   __syncthreads();
-  // the recomputation of rows outside the reference's range (rare)
-  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  // the rows outside the reference's range (rare), one at a time
   for (int k = 0; k < kLseRows; ++k) {
     if (!redo[k]) continue;  // uniform across the block
     const int64_t r = (int64_t)blockIdx.x * kLseRows + k;
-    const TI *h = Hc + (j0 + r) * D;
-    auto logit = [&](int64_t v) {
-      const TI *w = W + v * D;
-      float s = 0.f;
-      for (int64_t d = 0; d < D; ++d) s += static_cast<float>(h[d]) * static_cast<float>(w[d]);
-      return s;
-    };
-    // the row's maximum and sum of exponentials: each thread keeps a running
-    // (max, sum) over its logits, a fixed butterfly combines the wavefront's
-    // lanes (every lane ends with the same pair) and the wavefronts are
-    // combined in order (the tile statistics of such a row overflowed)
-    float2 st = make_float2(-INFINITY, 0.f);
-    for (int64_t v = threadIdx.x; v < V; v += kLseThreads) {
-      const float x = logit(v);
-      if (x > st.x) {
-        st.y = st.y * exp_f32(st.x - x) + 1.f;
-        st.x = x;
-      } else {
-        st.y += exp_f32(x - st.x);
-      }
-    }
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1)
-      st = combine_stats(st, make_float2(__shfl_xor(st.x, off), __shfl_xor(st.y, off)));
-    if (lane == 0) red[wv] = st;
-    __syncthreads();
-    st = red[0];
-    for (int u = 1; u < kLseThreads / 64; ++u) st = combine_stats(st, red[u]);
-    __syncthreads();
-    const float mx = st.x;
-    const float ls = st.x + log_f32(st.y);
-    if (threadIdx.x == 0) loss_row[j0 + r] = ls - tgt[r];
+    const float mx = rowst[k].x;
+    const float ls = rowst[k].x + log_f32(rowst[k].y);
+    const float m_old = mold[k];  // mref[j0 + r] is rewritten below
+    const float z = tgt[r];
     const int64_t tc = tcol[j0 + r];
-    for (int64_t v = threadIdx.x; v < ldp; v += kLseThreads) {
-      float e = 0.f;
-      if (v < V) {
-        e = exp_f32(logit(v) - mx);
-        if (v == tc) e -= exp_f32(ls - mx);
+    // 8 entries a thread at a time (ldp and wtm are multiples of 8, so the
+    // eight lie in one statistics tile; rows of P are 16-byte aligned)
+    constexpr int kVec = 8, kWords = kVec * (int)sizeof(TI) / 16;
+    TI *prow = P + r * ldp;
+#pragma unroll 2
+    for (int64_t v0 = (int64_t)threadIdx.x * kVec; v0 < ldp; v0 += (int64_t)kLseThreads * kVec) {
+      u32x4 raw[kWords];
+#pragma unroll
+      for (int w = 0; w < kWords; ++w) raw[w] = reinterpret_cast<const u32x4 *>(prow + v0)[w];
+      TI ev[kVec];
+      __builtin_memcpy(ev, raw, sizeof(ev));
+      float f = 0.f;
+      if (v0 < V) {
+        const float2 ts = stats[(v0 / wtm) * crows + r];
+        f = exp_f32((ts.y < 0.f ? ts.x : m_old) - mx);
       }
-      const TI te = static_cast<TI>(e);
-      P[r * ldp + v] = te;
-      if (PT && v < V) PT[v * ldet + r] = te;
+#pragma unroll
+      for (int i = 0; i < kVec; ++i) {
+        const int64_t v = v0 + i;
+        const float e = v >= V   ? 0.f
+                        : v == tc ? exp_f32(z - mx) - exp_f32(ls - mx)
+                                  : static_cast<float>(ev[i]) * f;
+        ev[i] = static_cast<TI>(e);
+        if (PT && v < V) PT[v * ldet + r] = ev[i];
+      }
+      __builtin_memcpy(raw, ev, sizeof(ev));
+#pragma unroll
+      for (int w = 0; w < kWords; ++w) reinterpret_cast<u32x4 *>(prow + v0)[w] = raw[w];
     }
     if (threadIdx.x == 0) {
       mref[j0 + r] = mx;
@@ -971,8 +987,8 @@ int ce_fwd_run(const TI *H, const TI *W, const int64_t *targets, int64_t M, int6
           L.vtiles, L.ttiles, tj);
     if ((e = check_launch("ce_logits"))) return e;
     ce_lse_kernel<TI><<<(unsigned)(L.crows / kLseRows), kLseThreads, 0, s>>>(
-        stats, L.ntiles, L.crows, tgt, S.n, j0, S.inv, tcol, mref, S.cfac, loss_row, S.P, L.ldp,
-        PT, L.crows, W, Hc, D, V);
+        stats, L.ntiles, L.wtm, L.crows, tgt, S.n, j0, S.inv, tcol, mref, S.cfac, loss_row, S.P,
+        L.ldp, PT, L.crows, V);
     if ((e = check_launch("ce_lse"))) return e;
     const bool last = c + 1 == L.nch;  // the mean loss comes with the last chunk's launch
     if (vec)

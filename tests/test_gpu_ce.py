@@ -163,8 +163,10 @@ def test_ce_rows_far_from_their_reference(cuda, dtype, chunk):
     N(0, 1) x 4, weights N(0, 1)), so that in about half of the rows the loss
     plus ln n exceeds 65 nats: E is stored relative to the target logit and
     scaled by a per-row factor exp(mref - lse) / n, and those rows would
-    leave the exponent range, so they go through the exact recomputation;
-    the others (loss + ln n under 55) keep the fast path.  Against the fp64
+    leave the exponent range, so the logits pass keeps their far tiles
+    relative to the tile maximum and the statistics pass rescales the row to
+    its maximum; the others (loss + ln n under 55) keep the fast path.
+    Against the fp64
     oracle on the same rounded inputs.  Tolerances: bf16 2e-2; fp32 1e-4,
     because an fp32 logit of magnitude ~100 carries an absolute rounding
     error of ~1e-5, which exp turns into a relative error of the same size in
@@ -184,7 +186,7 @@ def test_ce_rows_far_from_their_reference(cuda, dtype, chunk):
     mx = logits.max(axis=1)
     lse = mx + np.log(np.exp(logits - mx[:, None]).sum(axis=1))
     crit = (lse - logits[np.arange(m), tcol] + np.log(valid.sum()))[valid]
-    assert (crit > 65).sum() >= 0.3 * valid.sum()  # the recomputation is exercised
+    assert (crit > 65).sum() >= 0.3 * valid.sum()  # the rescale is exercised
     assert (crit < 55).sum() >= 0.3 * valid.sum()  # and so is the fast path
     loss, dh, dw = _run_ce(hid, w, tgt, chunk)
     tol = 2e-2 if dtype == torch.bfloat16 else 1e-4
@@ -198,7 +200,8 @@ def test_ce_tiny_row_factor_keeps_its_weight_gradient(cuda, chunk):
     that maximum).  On the fast path such a row's factor exp(mref - lse) / n
     is ~3e-40, below bf16's normal range, and its share of the dW operand
     (factor x hidden row, rounded to bf16) would vanish while its dH stayed
-    right; the criterion (loss + ln n above 60 nats: recompute) keeps it.
+    right; the criterion (loss + ln n above 60 nats: rescale the row to its
+    maximum) keeps it.
     The 32 rows are the only ones with a nonzero hidden column 0, so dW[:, 0]
     is their contribution alone, checked on its own besides dH row by row."""
     note(f"ce tiny row factor bf16 m=4096 d=64 v=4096 chunk={chunk}")
@@ -228,6 +231,44 @@ def test_ce_tiny_row_factor_keeps_its_weight_gradient(cuda, chunk):
     for r in rows:
         assert on.rel_err(np64(dh)[r], dho[r]) < 2e-2, f"dH row {r}"
     assert on.rel_err(np64(dh), dho) < 2e-2 and on.rel_err(np64(dw), dwo) < 2e-2
+
+
+@pytest.mark.parametrize("dtype,m,d,v,chunk", [
+    (torch.bfloat16, 512, 384, 32000, 1024),   # the reasoning head's shape, E held once
+    (torch.float32, 512, 384, 32000, 1024),
+    (torch.bfloat16, 512, 2048, 4096, 4096),   # E in both layouts
+    (torch.bfloat16, 1000, 384, 5000, 64),     # chunks of 256 rows with the dW accumulator
+])
+def test_ce_every_row_far_from_its_reference(cuda, dtype, m, d, v, chunk):
+    """Hidden and weights both N(0, 1): logits of standard deviation ~sqrt(D)
+    (20-45), so nearly every row's maximum lies far above its target logit
+    and most wavefront tiles store E relative to their own maximum; every
+    such row is rescaled to its maximum by the statistics pass.  Against the
+    fp64 oracle (tolerances as in the far-rows test), and the call stays
+    within a few milliseconds (rows like these were once recomputed one at a
+    time with scalar dot products, ~0.2 s for the first case)."""
+    note(f"ce every row far dtype={dtype} m={m} d={d} v={v} chunk={chunk}")
+    g = gen(57)
+    hid = randn((m, d), g, torch.float32, "cpu")
+    w = randn((v, d), g, torch.float32, "cpu")
+    tgt = torch.randint(0, v, (m,), generator=g)
+    tgt[::11] = -100
+    hid, w, tgt = hid.to(dtype).to(cuda), w.to(dtype).to(cuda), tgt.to(cuda)
+    logits = np64(hid) @ np64(w).T
+    valid = (tgt != -100).cpu().numpy()
+    tcol = np.where(valid, tgt.cpu().numpy(), 0)
+    gap = (logits.max(axis=1) - logits[np.arange(m), tcol])[valid]
+    assert (gap > 60).mean() > 0.5  # tiles far above the target logit in most rows
+    _run_ce(hid, w, tgt, chunk)  # warm
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    loss, dh, dw = _run_ce(hid, w, tgt, chunk)
+    end.record()
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end)
+    tol = 2e-2 if dtype == torch.bfloat16 else 1e-4
+    _check_ce(hid, w, tgt, loss, dh, dw, tol, f"every row far {dtype} m={m} d={d} v={v}")
+    assert ms < 50.0, f"{ms:.1f} ms for one forward + backward"
 
 
 @pytest.mark.parametrize("dtype,chunk,d", [(torch.bfloat16, 128, 64), (torch.bfloat16, 4096, 256),
