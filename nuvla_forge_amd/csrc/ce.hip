@@ -504,48 +504,80 @@ __global__ __launch_bounds__(kLseThreads) void ce_lse_kernel(
     mold[rl] = row < cnt ? mref[j0 + row] : 0.f;
   }
   __syncthreads();
-  // the rows outside the reference's range (rare), one at a time
-  for (int k = 0; k < kLseRows; ++k) {
-    if (!redo[k]) continue;  // uniform across the block
-    const int64_t r = (int64_t)blockIdx.x * kLseRows + k;
-    const float mx = rowst[k].x;
-    const float ls = rowst[k].x + log_f32(rowst[k].y);
-    const float m_old = mold[k];  // mref[j0 + r] is rewritten below
-    const float z = tgt[r];
-    const int64_t tc = tcol[j0 + r];
-    // 8 entries a thread at a time (ldp and wtm are multiples of 8, so the
-    // eight lie in one statistics tile; rows of P are 16-byte aligned)
-    constexpr int kVec = 8, kWords = kVec * (int)sizeof(TI) / 16;
-    TI *prow = P + r * ldp;
-#pragma unroll 2
-    for (int64_t v0 = (int64_t)threadIdx.x * kVec; v0 < ldp; v0 += (int64_t)kLseThreads * kVec) {
-      u32x4 raw[kWords];
+  // The rows outside the reference's range (rare), all of the block's rows
+  // together: a thread takes 8 entries (ldp and wtm are multiples of 8, so
+  // the eight lie in one statistics tile; rows of P are 16-byte aligned) of
+  // each row and rescales those of the rows off the fast path.  With E also
+  // held transposed it then writes the block's 16 columns of E^T for those 8
+  // vocabulary entries from all 16 rows (the other rows' entries are final
+  // and go back unchanged; rows past the chunk's count give zeros, the K
+  // padding of the dW product).
+  int any = 0;
 #pragma unroll
-      for (int w = 0; w < kWords; ++w) raw[w] = reinterpret_cast<const u32x4 *>(prow + v0)[w];
-      TI ev[kVec];
-      __builtin_memcpy(ev, raw, sizeof(ev));
+  for (int k = 0; k < kLseRows; ++k) any |= redo[k];
+  if (!any) return;  // uniform across the block
+  constexpr int kVec = 8, kWords = kVec * (int)sizeof(TI) / 16;
+  constexpr int kColWords = kLseRows * (int)sizeof(TI) / 16;
+  const int64_t r0 = (int64_t)blockIdx.x * kLseRows;
+  for (int64_t v0 = (int64_t)threadIdx.x * kVec; v0 < ldp; v0 += (int64_t)kLseThreads * kVec) {
+    TI ev[kLseRows][kVec];
+#pragma unroll
+    for (int k = 0; k < kLseRows; ++k) {
+      if ((redo[k] || PT) && r0 + k < cnt) {
+        u32x4 raw[kWords];
+#pragma unroll
+        for (int w = 0; w < kWords; ++w)
+          raw[w] = reinterpret_cast<const u32x4 *>(P + (r0 + k) * ldp + v0)[w];
+        __builtin_memcpy(ev[k], raw, sizeof(ev[k]));
+      } else {
+#pragma unroll
+        for (int i = 0; i < kVec; ++i) ev[k][i] = static_cast<TI>(0.f);
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < kLseRows; ++k) {
+      if (!redo[k]) continue;
+      const int64_t r = r0 + k;
+      const float mx = rowst[k].x, ls = rowst[k].x + log_f32(rowst[k].y);
       float f = 0.f;
       if (v0 < V) {
         const float2 ts = stats[(v0 / wtm) * crows + r];
-        f = exp_f32((ts.y < 0.f ? ts.x : m_old) - mx);
+        f = exp_f32((ts.y < 0.f ? ts.x : mold[k]) - mx);
       }
+      const int64_t tc = tcol[j0 + r];
 #pragma unroll
       for (int i = 0; i < kVec; ++i) {
         const int64_t v = v0 + i;
         const float e = v >= V   ? 0.f
-                        : v == tc ? exp_f32(z - mx) - exp_f32(ls - mx)
-                                  : static_cast<float>(ev[i]) * f;
-        ev[i] = static_cast<TI>(e);
-        if (PT && v < V) PT[v * ldet + r] = ev[i];
+                        : v == tc ? exp_f32(tgt[r] - mx) - exp_f32(ls - mx)
+                                  : static_cast<float>(ev[k][i]) * f;
+        ev[k][i] = static_cast<TI>(e);
       }
-      __builtin_memcpy(raw, ev, sizeof(ev));
+      u32x4 raw[kWords];
+      __builtin_memcpy(raw, ev[k], sizeof(ev[k]));
 #pragma unroll
-      for (int w = 0; w < kWords; ++w) reinterpret_cast<u32x4 *>(prow + v0)[w] = raw[w];
+      for (int w = 0; w < kWords; ++w) reinterpret_cast<u32x4 *>(P + r * ldp + v0)[w] = raw[w];
     }
-    if (threadIdx.x == 0) {
-      mref[j0 + r] = mx;
-      cfac[j0 + r] = inv * exp_f32(mx - ls);
+    if (PT) {
+#pragma unroll
+      for (int i = 0; i < kVec; ++i) {
+        if (v0 + i >= V) break;
+        TI col[kLseRows];
+#pragma unroll
+        for (int k = 0; k < kLseRows; ++k) col[k] = ev[k][i];
+        u32x4 raw[kColWords];
+        __builtin_memcpy(raw, col, sizeof(col));
+#pragma unroll
+        for (int w = 0; w < kColWords; ++w)
+          reinterpret_cast<u32x4 *>(PT + (v0 + i) * ldet + r0)[w] = raw[w];
+      }
     }
+  }
+  if (threadIdx.x < kLseRows && redo[threadIdx.x]) {
+    const int k = threadIdx.x;
+    const float mx = rowst[k].x, ls = rowst[k].x + log_f32(rowst[k].y);
+    mref[j0 + r0 + k] = mx;
+    cfac[j0 + r0 + k] = inv * exp_f32(mx - ls);
   }
 }
 
