@@ -589,14 +589,17 @@ def test_ce_fp16_inputs_give_fp16_gradients(cuda):
     _check_ce(hid, w, tgt, loss, dh, dw, 2e-3, "fp16", scale=2.0)
 
 
-def test_ce_reasoning_head_step_replays_in_a_graph(cuda):
+@pytest.mark.parametrize("lm_scale", [1.0, 50.0])
+def test_ce_reasoning_head_step_replays_in_a_graph(cuda, lm_scale):
     """The device path needs no host synchronisation (the reference's
     n_valid .item(), chunked_ce.py:126, is gone): forward + backward of the
     reasoning head capture into one HIP graph, and every replay, with eager
     work and synchronisations between replays, reproduces the eager step
-    bit for bit."""
-    note("ce reasoning head graph capture")
+    bit for bit.  lm_scale 50 (lm_head N(0, 1)) puts nearly every row far
+    from its reference logit, so the replays run the far-row rescale too."""
+    note(f"ce reasoning head graph capture lm_scale={lm_scale}")
     hid0, lm0, tgt = _reasoning_head_inputs(cuda, seed=9)
+    lm0 = lm0.detach() * lm_scale
 
     def make():
         h = hid0.detach().requires_grad_(True)
