@@ -62,7 +62,7 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baselines")
     ap.add_argument("--only", choices=("swiglu", "ce", "stress", "traffic", "dit", "head",
                                        "gateup", "copy", "adaln", "adaln_cold", "ce_gemm_ceiling",
-                                       "mfma"),
+                                       "mfma", "mainloop"),
                     default=None,
                     help="run one secondary workload alone (for profiling) and print its "
                          "record instead of the headline line")
@@ -398,6 +398,49 @@ def bench_mfma_ceiling(args, dev, blocks=2048, iters=300):
             tflops = flops / (ms * 1e-3) / 1e12
             dst[name] = {"us": ms * 1e3, "tflops": tflops,
                          "frac_of_spec": tflops / MFMA_BF16_PEAK_TFLOPS, "clock_ghz": ghz}
+    return res
+
+
+def bench_mainloop_probe(args, dev, blocks=2048, iters=300):
+    """`nf_mainloop_probe` for context (never the roofline denominator): the
+    GEMM core's mainloop instruction mix one ingredient at a time -- two
+    wavefronts per SIMD, 128 accumulators each, 64 v_mfma_f32_16x16x32 per
+    iteration on random bf16 operands; mode 1 registers only, 2 + the LDS
+    operand reads, 3 + the direct-to-LDS copies (L2-resident source), 4 +
+    the per-iteration barrier, 5 the copies over a 64 MiB footprint shared
+    by the blocks of one XCD -- each timed as 20 back-to-back launches in a
+    HIP graph, with the shader clock from the last launch's stamps.  Under
+    the power limit each ingredient also lowers the clock."""
+    import torch
+
+    from nuvla_forge_amd import _lib, _measure
+
+    L = _measure.lib()
+    g = torch.Generator().manual_seed(61)
+    ops = torch.randn(12, 512, 8, generator=g).to(torch.bfloat16).to(dev)
+    src_bytes = 64 << 20
+    src = torch.randn(src_bytes // 2, generator=g).to(torch.bfloat16).to(dev)
+    out = torch.empty(blocks, 512, device=dev)
+    stamps = torch.zeros(blocks, 4, dtype=torch.int64, device=dev)
+    flops = blocks * 8 * iters * 64 * (2 * 16 * 16 * 32)
+    names = {1: "registers", 2: "lds_reads", 3: "lds_reads_copies_l2", 4: "lds_reads_copies_barrier",
+             5: "copies_64MiB_shared_streams"}
+    res = {"blocks": blocks, "iters": iters, "flops_per_launch": flops}
+    for mode, name in names.items():
+        def launch(mode=mode):
+            _lib.check(L.nf_mainloop_probe(mode, ops.data_ptr(), src.data_ptr(), src_bytes, iters,
+                                           blocks, out.data_ptr(), stamps.data_ptr(),
+                                           _lib.stream_of(out)), "nf_mainloop_probe")
+
+        ms = per_launch_ms(launch, max(5, args.steps // 5))
+        st = stamps.cpu().double()
+        ghz = float((st[:, 1] - st[:, 0]).sum() / ((st[:, 3] - st[:, 2]).sum() / 100e6) / 1e9)
+        tflops = flops / (ms * 1e-3) / 1e12
+        # MFMA busy fraction at that clock: 1024 flops per SIMD per cycle
+        busy = tflops * 1e12 / (1024 * 4 * 256 * ghz * 1e9)
+        res[f"mode{mode}_{name}"] = {"us": ms * 1e3, "tflops": tflops,
+                                     "frac_of_spec": tflops / MFMA_BF16_PEAK_TFLOPS,
+                                     "clock_ghz": ghz, "mfma_busy_at_clock": busy}
     return res
 
 
@@ -977,7 +1020,7 @@ def main() -> int:
               "head": bench_ce_reasoning_head, "gateup": bench_gate_up, "copy": bench_copy,
               "adaln": bench_adaln, "adaln_cold": bench_adaln_cold,
               "ce_gemm_ceiling": bench_ce_gemm_ceiling,
-              "mfma": bench_mfma_ceiling}[args.only]
+              "mfma": bench_mfma_ceiling, "mainloop": bench_mainloop_probe}[args.only]
         print(json.dumps({"workload": args.only, **fn(args, dev)}), flush=True)
         return 0
 

@@ -82,6 +82,32 @@ int nf_stream_probe(int reads, int writes, const void *in0, const void *in1,
 int nf_mfma_probe(const void *ops, int64_t iters, int64_t blocks, int form, float *out,
                   uint64_t *stamps, void *stream);
 
+/* ------------------------------------------------------------------------
+ * The GEMM core's mainloop instruction mix, one ingredient at a time: what
+ * each costs the matrix pipes (and the power-limited clock).  `blocks`
+ * blocks of 512 threads (two wavefronts per SIMD), each wavefront issuing
+ * iters * 64 v_mfma_f32_16x16x32_bf16 products (2 * 16 * 16 * 32 flops each)
+ * on 128 accumulators:
+ *   mode 1  operands in registers, no memory access in the loop;
+ *   mode 2  + the operands read from LDS, 12 ds_read_b128 per 32 products,
+ *           interleaved with the products as the GEMM core does;
+ *   mode 3  + 8 direct-to-LDS copies of 1 KB per wavefront per iteration
+ *           (the GEMM's 64 KB stage per block) from the first 1 MiB of src
+ *           (L2-resident), waited for one iteration later;
+ *   mode 4  + one s_barrier per iteration;
+ *   mode 5  mode 4 with the copies walking 32 streams over 64 MiB of src
+ *           (blocks b and b + 32 k share stream b % 32 and one XCD's L2).
+ * ops: 12 * 512 16-byte vectors of bf16 operands (random data toggles the
+ * multipliers as a real product does).  src: 16-byte aligned, at least
+ * 1 MiB for modes 3-4 and 64 MiB for mode 5 (may be NULL for modes 1-2).
+ * out[b * 512 + t] = the sum of thread t's accumulators in block b; stamps
+ * (NULL or blocks * 4): per block the shader clock counter at start and end,
+ * then the 100 MHz real-time counter at start and end.
+ * ---------------------------------------------------------------------- */
+int nf_mainloop_probe(int mode, const void *ops, const void *src, size_t src_bytes,
+                      int64_t iters, int64_t blocks, float *out, uint64_t *stamps,
+                      void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,7 +1,7 @@
 """ctypes binding of libnf_measure.so (include/nuvla_forge_measure.h).
 
 The measurement aids the benchmark sets the product kernels against
-(``nf_stream_probe``, ``nf_mfma_probe``) and the GEMM test hooks
+(``nf_stream_probe``, ``nf_mfma_probe``, ``nf_mainloop_probe``) and the GEMM test hooks
 (``nf_gemm_nt``, ``nf_gemm_nt_acc``, ``nf_gemm_nn``).  None of them is part of the product ABI and no op calls
 them; they sit in their own library so that libnf_hip.so exports only the
 product's entry points.  Failures are reported through the product library's
@@ -29,6 +29,7 @@ SIGNATURES = {
     "nf_gemm_nn": (_I32, [_P, _I64, _P, _I64, _P, _I64, _I64, _I64, _I64, _I32, _P]),
     "nf_stream_probe": (_I32, [_I32, _I32, _P, _P, _P, _P, _P, _P, _I64, _P]),
     "nf_mfma_probe": (_I32, [_P, _I64, _I64, _I32, _P, _P, _P]),
+    "nf_mainloop_probe": (_I32, [_I32, _P, _P, ctypes.c_size_t, _I64, _I64, _P, _P, _P]),
 }
 
 _lib_m: ctypes.CDLL | None = None

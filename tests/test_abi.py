@@ -368,6 +368,29 @@ def test_mfma_probe_argument_validation():
     assert "aligned" in _err()
 
 
+def test_mainloop_probe_argument_validation():
+    """The mainloop-ingredients probe refuses bad modes, sizes and pointers,
+    and a source too small for its mode, before any launch (no GPU needed)."""
+    L = _measure.lib()
+    mib = 1 << 20
+    for mode in (0, 6):
+        assert L.nf_mainloop_probe(mode, FAKE, FAKE, 64 * mib, 1, 1, FAKE, None, None) == NF_ERR_ARG
+        assert "mode" in _err()
+    assert L.nf_mainloop_probe(1, FAKE, None, 0, -1, 1, FAKE, None, None) == NF_ERR_ARG
+    assert "iters" in _err()
+    assert L.nf_mainloop_probe(1, FAKE, None, 0, 1, 0, FAKE, None, None) == NF_ERR_ARG
+    assert "blocks" in _err()
+    assert L.nf_mainloop_probe(1, FAKE, None, 0, 1, 2**20 + 1, FAKE, None, None) == NF_ERR_ARG
+    assert L.nf_mainloop_probe(1, None, None, 0, 1, 1, FAKE, None, None) == NF_ERR_ARG
+    assert L.nf_mainloop_probe(1, FAKE, None, 0, 1, 1, None, None, None) == NF_ERR_ARG
+    assert L.nf_mainloop_probe(1, FAKE + 8, None, 0, 1, 1, FAKE, None, None) == NF_ERR_ARG
+    assert "aligned" in _err()
+    assert L.nf_mainloop_probe(3, FAKE, None, 0, 1, 1, FAKE, None, None) == NF_ERR_ARG
+    assert L.nf_mainloop_probe(4, FAKE, FAKE, mib - 16, 1, 1, FAKE, None, None) == NF_ERR_ARG
+    assert L.nf_mainloop_probe(5, FAKE, FAKE, mib, 1, 1, FAKE, None, None) == NF_ERR_ARG
+    assert "needs" in _err()
+
+
 def test_chunk_rows_argument():
     assert chunked_ce.chunk_rows_for(1024) == 1024
     assert chunked_ce.chunk_rows_for(7) == 7

@@ -3,7 +3,10 @@ against (GPU): with every A operand a and every B operand b (bf16), each of a
 thread's 256 accumulators receives iters products of 32-term dot products
 (form 0, 16x16x32) or 2 * iters of 16-term ones (form 1, 32x32x16), so its
 sum is 256 * 32 * iters * a * b either way, exact in fp32 at these sizes;
-zero operands (a null `ops`) give 0; the stamps count forward."""
+zero operands (a null `ops`) give 0; the stamps count forward.  Likewise
+nf_mainloop_probe in each mode: with every operand c, each of a thread's 128
+accumulators receives 2 * iters 32-term dot products, so its sum is
+128 * 64 * iters * c * c."""
 
 from __future__ import annotations
 
@@ -37,5 +40,24 @@ def test_mfma_probe_values(cuda, a, b, iters, blocks, form):
     torch.cuda.synchronize()
     want = 0.0 if a is None else 256 * 32 * iters * a * b
     assert torch.equal(out, torch.full_like(out, want))
+    st = stamps.cpu()
+    assert bool((st[:, 1] >= st[:, 0]).all()) and bool((st[:, 3] >= st[:, 2]).all())
+
+
+@pytest.mark.parametrize("mode", [1, 2, 3, 4, 5])
+def test_mainloop_probe_values(cuda, mode):
+    iters, blocks, c = 5, 40, 0.5
+    note(f"mainloop probe mode={mode} iters={iters} blocks={blocks}")
+    L = _measure.lib()
+    ops = torch.full((12, 512, 8), c, dtype=torch.bfloat16, device=cuda)
+    src_bytes = 64 << 20
+    src = torch.zeros(src_bytes // 2, dtype=torch.bfloat16, device=cuda)
+    out = torch.full((blocks, 512), -1.0, device=cuda)
+    stamps = torch.zeros(blocks, 4, dtype=torch.int64, device=cuda)
+    _lib.check(L.nf_mainloop_probe(mode, ops.data_ptr(), src.data_ptr(), src_bytes, iters, blocks,
+                                   out.data_ptr(), stamps.data_ptr(), _lib.stream_of(out)),
+               "nf_mainloop_probe")
+    torch.cuda.synchronize()
+    assert torch.equal(out, torch.full_like(out, 128 * 64 * iters * c * c))
     st = stamps.cpu()
     assert bool((st[:, 1] >= st[:, 0]).all()) and bool((st[:, 3] >= st[:, 2]).all())
